@@ -1,0 +1,555 @@
+// Grouped SwiGLU expert FFN over cache slots (bf16 in, fp32 accumulate, bf16 out).
+//
+// Reference: ferry/csrc/expert_ops.cpp:13-45 (execute_experts) and expert_ops.cu:6-25
+// (silu_mul).  For each expert e with rows p in [starts[e], starts[e+1]):
+//   x = in[rows[p]];  g = bf16(x Wg^T);  u = bf16(x Wu^T);  a = bf16(silu(g) * u) (fp32 math)
+//   y = bf16(a Wd^T);  out = bf16(y * w[rows[p], cols[p]])
+// with cache[slot] = [Wg (I x H) | Wu (I x H) | Wd (H x I)], all row-major bf16.  Both GEMMs
+// are "NT" (both operands contiguous along K), which is the native operand order of the
+// CDNA4 MFMA instructions used here.  The bf16 rounding points of the reference are kept.
+//
+// Two kernel families, selected per expert by its row count n_e:
+//  * skinny (n_e <= 64, decode): bandwidth-bound.  Weight fragments go straight from HBM
+//    into MFMA B-operand registers (16 B per lane, no LDS) and are reused across up to four
+//    16-row M tiles; x rows come from L2.  v_mfma_f32_16x16x32_bf16.  A workgroup owns 16*NT
+//    weight rows and splits K over 4/NT wavefronts; the partial sums meet in LDS.
+//  * tiled (n_e > 64, prefill): MFMA-bound.  Persistent workgroups walk a device-computed
+//    list of 128x128 output tiles; A (gathered x rows / activation rows) and B (weight rows)
+//    tiles of 64 along K are staged through padded, double-buffered LDS.
+//    v_mfma_f32_32x32x16_bf16, 2x2 wavefronts of 64x64.
+// Phase 1 ("up") computes the gate and up projections together and applies silu(g)*u in the
+// epilogue; phase 2 ("down") applies the routing weight in the epilogue and writes the
+// per-(token, expert) row that the combine kernel sums.
+#include "common.h"
+
+namespace ferry {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kListMax = 256;   // experts per launch (longer lists are split by the host)
+constexpr int kSkinnyMax = 64;  // rows handled by the skinny kernels (4 tiles of 16)
+
+struct ExpertList {
+  int32_t n;
+  int16_t expert[kListMax];
+  int32_t slot[kListMax];
+};
+
+struct FfnArgs {
+  const bf16_t* cache;
+  const bf16_t* x;        // [R, H]
+  const bf16_t* w;        // [R, k] routing weights in sorted-ID order
+  const int64_t* starts;  // [E+1]
+  const int64_t* rows;    // [R*k]
+  const int64_t* cols;    // [R*k]
+  bf16_t* act;            // [R*k, I]
+  bf16_t* out;            // [R*k, H]
+  int64_t H, I, k;
+  int32_t out_mode;
+  ExpertList list;
+};
+
+__device__ __forceinline__ float bf16r(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  // silu(g) * u in fp32 on the bf16-rounded GEMM outputs
+  return (g / (1.0f + expf(-g))) * u;
+}
+
+__device__ __forceinline__ bf16x8 load8(const bf16_t* p) {
+  return *reinterpret_cast<const bf16x8*>(p);
+}
+
+// =============================================================================================
+// Skinny kernels
+// =============================================================================================
+
+// Phase 1, skinny: one workgroup = (expert, 16*NT intermediate columns), K split KS ways.
+template <int NT>
+__global__ __launch_bounds__(256) void ffn_up_skinny(FfnArgs a) {
+  constexpr int KS = 4 / NT;
+  const int li = blockIdx.y;
+  if (li >= a.list.n) return;
+  const int e = a.list.expert[li];
+  const int64_t start = a.starts[e];
+  const int n = (int)(a.starts[e + 1] - start);
+  if (n == 0 || n > kSkinnyMax) return;
+  const int H = (int)a.H;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nt = wave % NT, ks = wave / NT;
+  const int i0 = blockIdx.x * 16 * NT + nt * 16;
+  const bf16_t* wg = a.cache + (int64_t)a.list.slot[li] * 3 * a.H * a.I;
+  const bf16_t* wu = wg + a.H * a.I;
+  const int r16 = lane & 15, kg = (lane >> 4) * 8;
+  const bf16_t* pg = wg + (int64_t)(i0 + r16) * H + kg;
+  const bf16_t* pu = wu + (int64_t)(i0 + r16) * H + kg;
+  const int MT = (n + 15) / 16;
+  const bf16_t* px[4];
+  bool okx[4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const int r = mt * 16 + r16;
+    okx[mt] = r < n;
+    const int64_t t = okx[mt] ? a.rows[start + r] : 0;
+    px[mt] = a.x + t * a.H + kg;
+  }
+  floatx4 accg[4], accu[4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    accg[mt] = floatx4{0, 0, 0, 0};
+    accu[mt] = floatx4{0, 0, 0, 0};
+  }
+  const int kspan = H / KS;
+  const int kbeg = ks * kspan, kend = kbeg + kspan;
+  const bf16x8 zero8 = {};
+  int k0 = kbeg;
+  for (; k0 + 4 * 32 <= kend; k0 += 4 * 32) {
+    bf16x8 bg[4], bu[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      bg[s] = load8(pg + k0 + s * 32);
+      bu[s] = load8(pu + k0 + s * 32);
+    }
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      if (mt < MT) {
+        bf16x8 ax[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) ax[s] = okx[mt] ? load8(px[mt] + k0 + s * 32) : zero8;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          accg[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax[s], bg[s], accg[mt], 0, 0, 0);
+          accu[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax[s], bu[s], accu[mt], 0, 0, 0);
+        }
+      }
+    }
+  }
+  for (; k0 < kend; k0 += 32) {
+    const bf16x8 bg = load8(pg + k0), bu = load8(pu + k0);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      if (mt < MT) {
+        const bf16x8 ax = okx[mt] ? load8(px[mt] + k0) : zero8;
+        accg[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, bg, accg[mt], 0, 0, 0);
+        accu[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, bu, accu[mt], 0, 0, 0);
+      }
+    }
+  }
+  // cross-wavefront K reduction, fixed order ks = 0..KS-1
+  __shared__ floatx4 red[KS > 1 ? KS : 1][NT][4][2][64];
+  if (KS > 1) {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      red[ks][nt][mt][0][lane] = accg[mt];
+      red[ks][nt][mt][1][lane] = accu[mt];
+    }
+    __syncthreads();
+    if (ks != 0) return;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      accg[mt] = red[0][nt][mt][0][lane];
+      accu[mt] = red[0][nt][mt][1][lane];
+      for (int q = 1; q < KS; ++q) {
+        accg[mt] += red[q][nt][mt][0][lane];
+        accu[mt] += red[q][nt][mt][1][lane];
+      }
+    }
+  }
+  // 16x16 accumulator layout: column = lane & 15, rows (lane >> 4) * 4 + [0, 4)
+  const int col = i0 + (lane & 15);
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    if (mt < MT) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = mt * 16 + (lane >> 4) * 4 + q;
+        if (r < n) {
+          const float g = bf16r(accg[mt][q]), u = bf16r(accu[mt][q]);
+          a.act[(start + r) * a.I + col] = f32_to_bf16(silu_mul(g, u));
+        }
+      }
+    }
+  }
+}
+
+// Phase 2, skinny: one workgroup = (expert, 16*NT hidden rows), K = I split KS ways.
+template <int NT>
+__global__ __launch_bounds__(256) void ffn_down_skinny(FfnArgs a) {
+  constexpr int KS = 4 / NT;
+  const int li = blockIdx.y;
+  if (li >= a.list.n) return;
+  const int e = a.list.expert[li];
+  const int64_t start = a.starts[e];
+  const int n = (int)(a.starts[e + 1] - start);
+  if (n == 0 || n > kSkinnyMax) return;
+  const int I = (int)a.I;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nt = wave % NT, ks = wave / NT;
+  const int h0 = blockIdx.x * 16 * NT + nt * 16;
+  const bf16_t* wd = a.cache + (int64_t)a.list.slot[li] * 3 * a.H * a.I + 2 * a.H * a.I;
+  const int r16 = lane & 15, kg = (lane >> 4) * 8;
+  const bf16_t* pd = wd + (int64_t)(h0 + r16) * I + kg;
+  const int MT = (n + 15) / 16;
+  const bf16_t* pa[4];
+  bool oka[4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const int r = mt * 16 + r16;
+    oka[mt] = r < n;
+    pa[mt] = a.act + (start + (oka[mt] ? r : 0)) * a.I + kg;
+  }
+  floatx4 acc[4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) acc[mt] = floatx4{0, 0, 0, 0};
+  const int kspan = I / KS;
+  const int kbeg = ks * kspan, kend = kbeg + kspan;
+  const bf16x8 zero8 = {};
+  int k0 = kbeg;
+  for (; k0 + 4 * 32 <= kend; k0 += 4 * 32) {
+    bf16x8 b[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) b[s] = load8(pd + k0 + s * 32);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      if (mt < MT) {
+        bf16x8 ax[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) ax[s] = oka[mt] ? load8(pa[mt] + k0 + s * 32) : zero8;
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax[s], b[s], acc[mt], 0, 0, 0);
+      }
+    }
+  }
+  for (; k0 < kend; k0 += 32) {
+    const bf16x8 b = load8(pd + k0);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      if (mt < MT) {
+        const bf16x8 ax = oka[mt] ? load8(pa[mt] + k0) : zero8;
+        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, b, acc[mt], 0, 0, 0);
+      }
+    }
+  }
+  __shared__ floatx4 red[KS > 1 ? KS : 1][NT][4][64];
+  if (KS > 1) {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) red[ks][nt][mt][lane] = acc[mt];
+    __syncthreads();
+    if (ks != 0) return;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      acc[mt] = red[0][nt][mt][lane];
+      for (int q = 1; q < KS; ++q) acc[mt] += red[q][nt][mt][lane];
+    }
+  }
+  const int h = h0 + (lane & 15);
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    if (mt < MT) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = mt * 16 + (lane >> 4) * 4 + q;
+        if (r < n) {
+          const int64_t p = start + r;
+          const int64_t t = a.rows[p], j = a.cols[p];
+          const float wt = bf16_to_f32(a.w[t * a.k + j]);
+          const float y = bf16r(acc[mt][q]);
+          const int64_t orow = a.out_mode == 0 ? t * a.k + j : p;
+          a.out[orow * a.H + h] = f32_to_bf16(y * wt);
+        }
+      }
+    }
+  }
+}
+
+// =============================================================================================
+// Tiled kernels
+// =============================================================================================
+
+constexpr int BM = 128, BN = 128, BK = 64, LDK = BK + 8;  // +8 bf16 of padding per row
+
+struct TileTable {
+  int32_t cum[kListMax + 1];  // cumulative M tiles over list entries
+  int32_t total;
+};
+
+// Wavefront 0 builds the cumulative M-tile counts of the big experts of the list.
+__device__ void build_tile_table(const FfnArgs& a, TileTable& tt) {
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    int cnt[4];
+    int local = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int li = lane * 4 + q;
+      int c = 0;
+      if (li < a.list.n) {
+        const int e = a.list.expert[li];
+        const int64_t n = a.starts[e + 1] - a.starts[e];
+        c = n > kSkinnyMax ? (int)((n + BM - 1) / BM) : 0;
+      }
+      cnt[q] = c;
+      local += c;
+    }
+    int incl = local;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int v = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += v;
+    }
+    int run = incl - local;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      tt.cum[lane * 4 + q] = run;
+      run += cnt[q];
+    }
+    if (lane == 63) {
+      tt.cum[kListMax] = incl;
+      tt.total = incl;
+    }
+  }
+  __syncthreads();
+}
+
+// largest li with cum[li] <= m (cum is non-decreasing)
+__device__ __forceinline__ int find_entry(const TileTable& tt, int m) {
+  int lo = 0, hi = kListMax;  // cum[lo] <= m < cum[hi]
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (tt.cum[mid] <= m)
+      lo = mid;
+    else
+      hi = mid;
+  }
+  return lo;
+}
+
+// MODE 0: A = gathered x rows (K = H), B rows 0..63 = Wg[i0..], 64..127 = Wu[i0..], out act.
+// MODE 1: A = act rows (K = I), B rows = Wd[h0..], out weighted rows.
+template <int MODE>
+__global__ __launch_bounds__(256) void ffn_tiled(FfnArgs a) {
+  __shared__ TileTable tt;
+  __shared__ __attribute__((aligned(16))) bf16_t As[2][BM * LDK];
+  __shared__ __attribute__((aligned(16))) bf16_t Bs[2][BN * LDK];
+  build_tile_table(a, tt);
+  const int64_t K = MODE == 0 ? a.H : a.I;
+  const int ntn = MODE == 0 ? (int)(a.I / 64) : (int)(a.H / BN);
+  const int total = tt.total * ntn;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int KT = (int)(K / BK);
+
+  for (int tile = blockIdx.x; tile < total; tile += gridDim.x) {
+    const int mt_global = tile / ntn, ntile = tile % ntn;
+    const int li = find_entry(tt, mt_global);
+    const int e = a.list.expert[li];
+    const int64_t start = a.starts[e];
+    const int n = (int)(a.starts[e + 1] - start);
+    const int m0 = (mt_global - tt.cum[li]) * BM;
+    const bf16_t* slot = a.cache + (int64_t)a.list.slot[li] * 3 * a.H * a.I;
+
+    // per-thread global load descriptors: 4 chunks of 16 B for A and for B
+    const bf16_t* ga[4];
+    const bf16_t* gb[4];
+    bool oka[4];
+    int lrow[4], lkc[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c = tid + 256 * q;
+      const int row = c >> 3, kc = (c & 7) * 8;
+      lrow[q] = row;
+      lkc[q] = kc;
+      const int r = m0 + row;
+      oka[q] = r < n;
+      if (MODE == 0) {
+        const int64_t t = oka[q] ? a.rows[start + r] : 0;
+        ga[q] = a.x + t * a.H + kc;
+        const int i0 = ntile * 64;
+        const bf16_t* wrow = row < 64 ? slot + (int64_t)(i0 + row) * a.H
+                                      : slot + a.H * a.I + (int64_t)(i0 + row - 64) * a.H;
+        gb[q] = wrow + kc;
+      } else {
+        ga[q] = a.act + (start + (oka[q] ? r : 0)) * a.I + kc;
+        const int h0 = ntile * BN;
+        gb[q] = slot + 2 * a.H * a.I + (int64_t)(h0 + row) * a.I + kc;
+      }
+    }
+    u32x4 ra[4], rb[4];
+    const u32x4 z4 = {0, 0, 0, 0};
+    auto gload = [&](int kt) {
+      const int64_t koff = (int64_t)kt * BK;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        ra[q] = oka[q] ? *reinterpret_cast<const u32x4*>(ga[q] + koff) : z4;
+        rb[q] = *reinterpret_cast<const u32x4*>(gb[q] + koff);
+      }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        *reinterpret_cast<u32x4*>(&As[buf][lrow[q] * LDK + lkc[q]]) = ra[q];
+        *reinterpret_cast<u32x4*>(&Bs[buf][lrow[q] * LDK + lkc[q]]) = rb[q];
+      }
+    };
+
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+    // B sub-tile rows of this wavefront: MODE 0 -> gate rows wn*32.., up rows 64 + wn*32..;
+    // MODE 1 -> rows wn*64 + [0, 64).
+    const int brow0 = MODE == 0 ? wn * 32 : wn * 64;
+    const int brow1 = MODE == 0 ? 64 + wn * 32 : wn * 64 + 32;
+    const int arow0 = wm * 64;
+    const int l32 = lane & 31, kh = (lane >> 5) * 8;
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < KT; ++kt) {
+      const int buf = kt & 1;
+      if (kt + 1 < KT) gload(kt + 1);
+#pragma unroll
+      for (int kk = 0; kk < BK; kk += 16) {
+        bf16x8 af[2], bf[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          af[i] = *reinterpret_cast<const bf16x8*>(&As[buf][(arow0 + i * 32 + l32) * LDK + kk + kh]);
+        bf[0] = *reinterpret_cast<const bf16x8*>(&Bs[buf][(brow0 + l32) * LDK + kk + kh]);
+        bf[1] = *reinterpret_cast<const bf16x8*>(&Bs[buf][(brow1 + l32) * LDK + kk + kh]);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+      }
+      if (kt + 1 < KT) lstore(buf ^ 1);
+      __syncthreads();
+    }
+
+    // epilogue; 32x32 accumulator layout: column = lane & 31,
+    // row(v) = (v / 4) * 8 + (lane / 32) * 4 + v % 4
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = m0 + arow0 + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+        if (r >= n) continue;
+        const int64_t p = start + r;
+        if (MODE == 0) {
+          const int icol = ntile * 64 + wn * 32 + l32;
+          const float g = bf16r(acc[i][0][v]), u = bf16r(acc[i][1][v]);
+          a.act[p * a.I + icol] = f32_to_bf16(silu_mul(g, u));
+        } else {
+          const int64_t t = a.rows[p], j = a.cols[p];
+          const float wt = bf16_to_f32(a.w[t * a.k + j]);
+          const int64_t orow = a.out_mode == 0 ? t * a.k + j : p;
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj) {
+            const int h = ntile * BN + wn * 64 + jj * 32 + l32;
+            a.out[orow * a.H + h] = f32_to_bf16(bf16r(acc[i][jj][v]) * wt);
+          }
+        }
+      }
+    }
+  }
+}
+
+int g_num_cus = 0;
+
+}  // namespace
+}  // namespace ferry
+
+using namespace ferry;
+
+extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t hidden,
+                                int64_t inter, const void* x, int64_t rows_in, int64_t topk,
+                                const void* w_sorted, const int64_t* starts, const int64_t* rows,
+                                const int64_t* cols, const int32_t* expert_list, int32_t n_list,
+                                const int32_t* slot_of, int64_t experts,
+                                int64_t max_rows_per_expert, void* act, void* out,
+                                int32_t out_mode, void* stream) {
+  clear_error();
+  FERRY_CHECK_ARG(hidden > 0 && hidden % 128 == 0, "hidden must be a positive multiple of 128");
+  FERRY_CHECK_ARG(inter > 0 && inter % 128 == 0, "intermediate must be a positive multiple of 128");
+  FERRY_CHECK_ARG(topk >= 1 && rows_in >= 0 && n_list >= 0 && max_rows_per_expert >= 0,
+                  "bad sizes");
+  FERRY_CHECK_ARG(experts >= 1 && experts <= FERRY_MAX_EXPERTS, "experts must be in [1, %d]",
+                  FERRY_MAX_EXPERTS);
+  FERRY_CHECK_ARG(out_mode == 0 || out_mode == 1, "out_mode must be 0 or 1");
+  FERRY_CHECK_ARG(rows_in * topk < (int64_t)1 << 31, "rows*topk must be < 2^31");
+  if (n_list == 0 || rows_in == 0) return 0;
+  FERRY_CHECK_ARG(cache && x && w_sorted && starts && rows && cols && expert_list && slot_of &&
+                      act && out,
+                  "null pointer argument");
+  for (int32_t i = 0; i < n_list; ++i) {
+    const int32_t e = expert_list[i];
+    FERRY_CHECK_ARG(e >= 0 && e < experts, "expert_list[%d] = %d out of range", i, e);
+    const int32_t s = slot_of[e];
+    FERRY_CHECK_ARG(s >= 0 && s < cache_rows, "expert %d is not cached (slot %d)", e, s);
+  }
+  if (g_num_cus == 0) {
+    int dev = 0, cus = 0;
+    FERRY_HIP(hipGetDevice(&dev));
+    FERRY_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    g_num_cus = cus > 0 ? cus : 256;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  FfnArgs args;
+  args.cache = (const bf16_t*)cache;
+  args.x = (const bf16_t*)x;
+  args.w = (const bf16_t*)w_sorted;
+  args.starts = starts;
+  args.rows = rows;
+  args.cols = cols;
+  args.act = (bf16_t*)act;
+  args.out = (bf16_t*)out;
+  args.H = hidden;
+  args.I = inter;
+  args.k = topk;
+  args.out_mode = out_mode;
+  // max_rows_per_expert must bound every n_e (rows_in does for a layout from ferry_layout);
+  // the tiled kernels size their work from the device starts, the bound only gates the launch
+  const int64_t maxn = max_rows_per_expert;
+  const int64_t pairs = rows_in * topk;
+  for (int32_t off = 0; off < n_list; off += kListMax) {
+    const int32_t cnt = (n_list - off) < kListMax ? (n_list - off) : kListMax;
+    args.list.n = cnt;
+    for (int32_t i = 0; i < kListMax; ++i) {
+      args.list.expert[i] = (int16_t)(i < cnt ? expert_list[off + i] : 0);
+      args.list.slot[i] = i < cnt ? slot_of[expert_list[off + i]] : 0;
+    }
+    // skinny part (experts with 1..64 rows)
+    hipLaunchKernelGGL(ffn_up_skinny<1>, dim3((unsigned)(inter / 16), cnt), dim3(256), 0, s, args);
+    FERRY_LAUNCHED("ffn_up_skinny");
+    const bool any_big = maxn > kSkinnyMax;
+    int64_t tile_bound = 0;
+    if (any_big) {
+      // M tiles over experts with > 64 rows: sum ceil(n/128) <= pairs/128 + pairs/65
+      tile_bound = pairs / BM + pairs / (kSkinnyMax + 1) + 1;
+      int64_t t1 = tile_bound * (inter / 64);
+      int64_t grid = t1 < (int64_t)g_num_cus * 2 ? t1 : (int64_t)g_num_cus * 2;
+      hipLaunchKernelGGL(ffn_tiled<0>, dim3((unsigned)grid), dim3(256), 0, s, args);
+      FERRY_LAUNCHED("ffn_tiled<up>");
+    }
+    hipLaunchKernelGGL(ffn_down_skinny<4>, dim3((unsigned)(hidden / 64), cnt), dim3(256), 0, s,
+                       args);
+    FERRY_LAUNCHED("ffn_down_skinny");
+    if (any_big) {
+      int64_t t2 = tile_bound * (hidden / BN);
+      int64_t grid = t2 < (int64_t)g_num_cus * 2 ? t2 : (int64_t)g_num_cus * 2;
+      hipLaunchKernelGGL(ffn_tiled<1>, dim3((unsigned)grid), dim3(256), 0, s, args);
+      FERRY_LAUNCHED("ffn_tiled<down>");
+    }
+  }
+  return 0;
+}

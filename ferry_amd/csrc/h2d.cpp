@@ -1,0 +1,177 @@
+// H2D expert fetch engine: pinned host pool rows -> device cache slots on a dedicated stream.
+//
+// Reference: ferry/csrc/expert_ops.cpp:94-142 (H2DEngine).  A copy into a slot first waits
+// (on the copy stream, GPU-side) for the last compute that read the slot (the "used" event of
+// mark_used), then records the slot's copy-done event.  Besides the reference's host wait
+// (wait_host), wait_stream makes a compute stream wait for the copies on the GPU, so that
+// experts that are already resident can run while missing ones are still in flight.
+// The engine owns one stream (default priority) and its events; it allocates no memory.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <memory>
+#include <vector>
+
+#include "../../include/ferry_amd.h"
+
+namespace ferry {
+void set_error(const char* fmt, ...);
+void clear_error();
+}  // namespace ferry
+
+namespace {
+
+struct Event {
+  hipEvent_t e = nullptr;
+  ~Event() {
+    if (e) (void)hipEventDestroy(e);
+  }
+};
+
+}  // namespace
+
+struct ferry_h2d {
+  char* cache = nullptr;
+  const char* pool = nullptr;
+  int64_t cache_rows = 0, pool_rows = 0, row_bytes = 0;
+  int32_t device = 0;
+  hipStream_t stream = nullptr;
+  std::vector<hipEvent_t> copy_done;  // per slot
+  std::vector<int64_t> copy_seq;      // per slot: sequence number of its last copy, -1 if none
+  std::vector<std::shared_ptr<Event>> used;  // per slot: last compute that read it
+  int64_t seq = 0;
+  int64_t copies = 0;
+};
+
+#define H2D_HIP(expr)                                                                     \
+  do {                                                                                    \
+    hipError_t _e = (expr);                                                               \
+    if (_e != hipSuccess) {                                                               \
+      ferry::set_error("%s failed: %s", #expr, hipGetErrorString(_e));                   \
+      return 3;                                                                           \
+    }                                                                                     \
+  } while (0)
+
+extern "C" int ferry_h2d_create(void* cache, int64_t cache_rows, const void* pool,
+                                int64_t pool_rows, int64_t row_bytes, int32_t device,
+                                ferry_h2d** out) {
+  ferry::clear_error();
+  if (!out || !cache || !pool || cache_rows < 0 || pool_rows < 0 || row_bytes <= 0) {
+    ferry::set_error("h2d_create: bad arguments");
+    return 2;
+  }
+  hipPointerAttribute_t attr;
+  if (hipPointerGetAttributes(&attr, pool) != hipSuccess || attr.type != hipMemoryTypeHost) {
+    (void)hipGetLastError();
+    ferry::set_error("h2d_create: the pool must be pinned host memory");
+    return 2;
+  }
+  H2D_HIP(hipSetDevice(device));
+  std::unique_ptr<ferry_h2d> h(new ferry_h2d());
+  h->cache = (char*)cache;
+  h->pool = (const char*)pool;
+  h->cache_rows = cache_rows;
+  h->pool_rows = pool_rows;
+  h->row_bytes = row_bytes;
+  h->device = device;
+  H2D_HIP(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking));
+  h->copy_done.assign((size_t)cache_rows, nullptr);
+  h->copy_seq.assign((size_t)cache_rows, -1);
+  h->used.assign((size_t)cache_rows, nullptr);
+  for (auto& e : h->copy_done) H2D_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+  *out = h.release();
+  return 0;
+}
+
+extern "C" int ferry_h2d_destroy(ferry_h2d* h) {
+  ferry::clear_error();
+  if (!h) return 0;
+  (void)hipStreamSynchronize(h->stream);
+  for (auto e : h->copy_done)
+    if (e) (void)hipEventDestroy(e);
+  h->used.clear();
+  (void)hipStreamDestroy(h->stream);
+  delete h;
+  return 0;
+}
+
+extern "C" int ferry_h2d_fetch(ferry_h2d* h, const int64_t* slots, const int64_t* keys,
+                               int64_t n) {
+  ferry::clear_error();
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t slot = slots[i], key = keys[i];
+    if (slot < 0 || slot >= h->cache_rows || key < 0 || key >= h->pool_rows) {
+      ferry::set_error("h2d_fetch: slot %lld / key %lld out of range", (long long)slot,
+                       (long long)key);
+      return 2;
+    }
+    if (h->used[(size_t)slot]) H2D_HIP(hipStreamWaitEvent(h->stream, h->used[(size_t)slot]->e, 0));
+    H2D_HIP(hipMemcpyAsync(h->cache + slot * h->row_bytes, h->pool + key * h->row_bytes,
+                           (size_t)h->row_bytes, hipMemcpyHostToDevice, h->stream));
+    H2D_HIP(hipEventRecord(h->copy_done[(size_t)slot], h->stream));
+    h->copy_seq[(size_t)slot] = h->seq++;
+    ++h->copies;
+  }
+  return 0;
+}
+
+extern "C" int ferry_h2d_wait_host(ferry_h2d* h, const int64_t* slots, int64_t n) {
+  ferry::clear_error();
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t slot = slots[i];
+    if (slot < 0 || slot >= h->cache_rows) {
+      ferry::set_error("h2d_wait_host: slot %lld out of range", (long long)slot);
+      return 2;
+    }
+    if (h->copy_seq[(size_t)slot] >= 0) H2D_HIP(hipEventSynchronize(h->copy_done[(size_t)slot]));
+  }
+  return 0;
+}
+
+extern "C" int ferry_h2d_wait_stream(ferry_h2d* h, const int64_t* slots, int64_t n,
+                                     void* stream) {
+  ferry::clear_error();
+  // copies complete in issue order on the engine's stream: waiting for the most recently
+  // issued copy among the slots covers all of them
+  int64_t best = -1, best_seq = -1;
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t slot = slots[i];
+    if (slot < 0 || slot >= h->cache_rows) {
+      ferry::set_error("h2d_wait_stream: slot %lld out of range", (long long)slot);
+      return 2;
+    }
+    if (h->copy_seq[(size_t)slot] > best_seq) {
+      best_seq = h->copy_seq[(size_t)slot];
+      best = slot;
+    }
+  }
+  if (best >= 0) H2D_HIP(hipStreamWaitEvent((hipStream_t)stream, h->copy_done[(size_t)best], 0));
+  return 0;
+}
+
+extern "C" int ferry_h2d_mark_used(ferry_h2d* h, const int64_t* slots, int64_t n, void* stream) {
+  ferry::clear_error();
+  if (n == 0) return 0;
+  auto ev = std::make_shared<Event>();
+  H2D_HIP(hipEventCreateWithFlags(&ev->e, hipEventDisableTiming));
+  H2D_HIP(hipEventRecord(ev->e, (hipStream_t)stream));
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t slot = slots[i];
+    if (slot < 0 || slot >= h->cache_rows) {
+      ferry::set_error("h2d_mark_used: slot %lld out of range", (long long)slot);
+      return 2;
+    }
+    h->used[(size_t)slot] = ev;
+  }
+  return 0;
+}
+
+extern "C" int ferry_h2d_synchronize(ferry_h2d* h) {
+  ferry::clear_error();
+  H2D_HIP(hipStreamSynchronize(h->stream));
+  return 0;
+}
+
+extern "C" int64_t ferry_h2d_copies(const ferry_h2d* h) { return h ? h->copies : 0; }
+
+extern "C" void* ferry_h2d_stream(ferry_h2d* h) { return h ? (void*)h->stream : nullptr; }

@@ -1,0 +1,101 @@
+// Selection-frequency history (window W) on the device, plus the uint8 ID payload that the
+// host planner copies back.
+//
+// Reference: ferry/metadata.py:15-38 (GateHistory) fed by RouteGather.collect at world = 1
+// (ferry/metadata.py:169-176): the history rows of a layer call are the one-hot selection
+// indicators of its last min(T, ceil(W / world)) tokens; a batch of >= W rows replaces the
+// window, a shorter one is appended ring-wise; scores = float32(sum(rows) / max(1, count)).
+// Because rows are 0/1, the window sum is the integer count c_e of the last n = min(W, seen)
+// tokens that selected e, so the device keeps per-layer integer counters and a ring of the
+// IDs of the tokens in the window; score = float32(double(c_e) / double(n)) reproduces the
+// reference's float64 mean followed by the float32 cast exactly.
+#include "common.h"
+
+namespace ferry {
+namespace {
+
+constexpr int kMaxE = 512;
+constexpr int kThreads = 256;
+constexpr int kIdsPerBlock = kThreads * 16;
+
+// Block 0 updates the window of `layer`; blocks >= 1 write the uint8 copy of selected.
+__global__ __launch_bounds__(kThreads) void history_kernel(
+    const int64_t* __restrict__ selected, int64_t tokens, int k, int E, int W, int64_t layer,
+    int32_t* __restrict__ ring, int32_t* __restrict__ counts, int32_t* __restrict__ meta,
+    float* __restrict__ scores_out, uint8_t* __restrict__ ids_out) {
+  if (blockIdx.x > 0) {
+    const int64_t n = tokens * k;
+    const int64_t i0 = (int64_t)(blockIdx.x - 1) * kIdsPerBlock;
+    for (int64_t i = i0 + threadIdx.x; i < n && i < i0 + kIdsPerBlock; i += kThreads)
+      ids_out[i] = (uint8_t)selected[i];
+    return;
+  }
+  __shared__ int32_t c[kMaxE];
+  int32_t* lring = ring + layer * (int64_t)W * k;
+  int32_t* lcount = counts + layer * (int64_t)E;
+  const int count = meta[layer * 2 + 0];
+  const int head = meta[layer * 2 + 1];
+  const int tail = (int)(tokens < W ? tokens : W);
+  const bool replace = tail >= W;
+  for (int e = threadIdx.x; e < E; e += kThreads) c[e] = replace ? 0 : lcount[e];
+  __syncthreads();
+  if (replace) {
+    // window := the last W tokens, ring position r = token T - W + r
+    for (int idx = threadIdx.x; idx < W * k; idx += kThreads) {
+      const int r = idx / k, j = idx % k;
+      const int64_t e = selected[(tokens - W + r) * k + j];
+      lring[idx] = (int32_t)e;
+      if (e >= 0 && e < E) atomicAdd(&c[e], 1);
+    }
+  } else {
+    // append ring-wise; position (head + r) % W holds an old row iff r >= W - count
+    for (int idx = threadIdx.x; idx < tail * k; idx += kThreads) {
+      const int r = idx / k, j = idx % k;
+      const int pos = (head + r) % W;
+      if (r >= W - count) {
+        const int32_t old = lring[pos * k + j];
+        if (old >= 0 && old < E) atomicSub(&c[old], 1);
+      }
+      const int64_t e = selected[(tokens - tail + r) * k + j];
+      lring[pos * k + j] = (int32_t)e;
+      if (e >= 0 && e < E) atomicAdd(&c[e], 1);
+    }
+  }
+  __syncthreads();
+  const int new_count = replace ? W : (count + tail < W ? count + tail : W);
+  const int n = new_count > 1 ? new_count : 1;
+  for (int e = threadIdx.x; e < E; e += kThreads) {
+    lcount[e] = c[e];
+    scores_out[e] = (float)((double)c[e] / (double)n);
+  }
+  if (threadIdx.x == 0) {
+    meta[layer * 2 + 0] = new_count;
+    meta[layer * 2 + 1] = replace ? 0 : (head + tail) % W;
+  }
+}
+
+}  // namespace
+}  // namespace ferry
+
+using namespace ferry;
+
+extern "C" int ferry_history_update(const int64_t* selected, int64_t tokens, int64_t topk,
+                                    int64_t experts, int64_t window, int64_t layer,
+                                    int32_t* ring, int32_t* counts, int32_t* meta,
+                                    float* scores_out, uint8_t* ids_out, void* stream) {
+  clear_error();
+  FERRY_CHECK_ARG(tokens >= 0 && topk >= 1 && layer >= 0, "bad sizes");
+  FERRY_CHECK_ARG(experts >= 1 && experts <= kMaxE, "experts must be in [1, %d]", kMaxE);
+  FERRY_CHECK_ARG(experts <= 256 || ids_out == nullptr, "uint8 IDs need experts <= 256");
+  FERRY_CHECK_ARG(window >= 1 && window <= (1 << 20), "window must be in [1, 2^20]");
+  FERRY_CHECK_ARG(ring && counts && meta && scores_out, "null pointer argument");
+  FERRY_CHECK_ARG(tokens == 0 || selected, "null pointer argument");
+  const int64_t nids = ids_out ? tokens * topk : 0;
+  const int64_t grid = 1 + ceil_div(nids, kIdsPerBlock);
+  FERRY_CHECK_ARG(grid < (1 << 30), "too many tokens");
+  hipLaunchKernelGGL(history_kernel, dim3((unsigned)grid), dim3(kThreads), 0, (hipStream_t)stream,
+                     selected, tokens, (int)topk, (int)experts, (int)window, layer, ring, counts,
+                     meta, scores_out, ids_out);
+  FERRY_LAUNCHED("history_kernel");
+  return 0;
+}

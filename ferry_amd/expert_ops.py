@@ -1,0 +1,234 @@
+"""Python face of the HIP kernels (libferry_amd.so) with the reference's native-op names.
+
+Reference: ``expert_ops()`` of ferry/runtime.py:26-31, i.e. the pybind11 module of
+ferry/csrc/expert_ops.cpp:144-157 (execute_experts, pack_dispatch, unpack_dispatch,
+reduce_partials, scatter_returned, H2DEngine).  The same names and argument meanings are kept
+so that call sites written against the reference work unchanged; the fused hot-path entry
+points (router_topk, layout, expert_ffn, combine, history_update) are exposed next to them.
+All tensors are CUDA (HIP) tensors; every op runs on the current stream.
+"""
+import numpy as np
+import torch
+
+from ._lib import check, lib
+from .h2d import H2DEngine
+
+__all__ = ['execute_experts', 'pack_dispatch', 'unpack_dispatch', 'reduce_partials',
+           'scatter_returned', 'H2DEngine', 'router_topk', 'layout', 'expert_ffn', 'combine',
+           'history_update', 'current_stream']
+
+MAX_EXPERTS = 512
+
+
+def current_stream(device=None):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _dev(t, name, dtype=None, contiguous=True):
+    if not isinstance(t, torch.Tensor) or t.device.type != 'cuda':
+        raise RuntimeError(f'{name} must be a CUDA tensor')
+    if dtype is not None and t.dtype != dtype:
+        raise RuntimeError(f'{name} must be {dtype}, got {t.dtype}')
+    if contiguous and not t.is_contiguous():
+        raise RuntimeError(f'{name} must be contiguous')
+    return t.data_ptr()
+
+
+# ------------------------------------------------------------------------------------------
+# Hot-path entry points
+# ------------------------------------------------------------------------------------------
+
+def router_topk(logits, topk, renorm=True, scale=1.0, sorted=True, return_probs=False,
+                tie_counter=None):
+    """Softmax (fp32) + top-k + optional renorm, * scale, cast to bf16.
+
+    Reference: ferry/model.py:141-146 (Qwen3: ``softmax(logits, -1, fp32)``, ``topk(k)``,
+    ``w / w.sum(-1)``, ``.to(bf16)``) and the greedy DeepSeek-V2 gate reaching
+    ferry/model.py:151-157 (``topk(sorted=False)``, ``* routed_scaling_factor``).
+    Returns (weights bf16 [T, k], selected int64 [T, k]) and the fp32 probabilities when
+    ``return_probs``.  Index selection is exactly torch's CPU ``topk``, ties included.
+    """
+    if logits.dim() != 2:
+        raise RuntimeError('logits must be [tokens, experts]')
+    dt = {torch.bfloat16: 0, torch.float32: 1}.get(logits.dtype)
+    if dt is None:
+        raise RuntimeError('logits must be bf16 or fp32')
+    T, E = logits.shape
+    idx = torch.empty((T, topk), dtype=torch.int64, device=logits.device)
+    w = torch.empty((T, topk), dtype=torch.bfloat16, device=logits.device)
+    probs = torch.empty((T, E), dtype=torch.float32, device=logits.device) if return_probs else None
+    check(lib().ferry_router_topk(
+        _dev(logits, 'logits'), dt, T, E, topk, int(bool(renorm)), float(scale), int(bool(sorted)),
+        idx.data_ptr(), w.data_ptr(), probs.data_ptr() if probs is not None else None,
+        _dev(tie_counter, 'tie_counter', torch.int32) if tie_counter is not None else None,
+        current_stream(logits.device)), 'router_topk')
+    return (w, idx, probs) if return_probs else (w, idx)
+
+
+class Layout:
+    """Device layout of one layer call (ferry/layout.py:12-94 at world = 1)."""
+
+    __slots__ = ('tokens', 'topk', 'experts', 'send_ids', 'w_sorted', 'starts', 'rows', 'cols',
+                 'pair_pos', 'workspace')
+
+
+def layout_workspace_bytes(tokens, topk, experts):
+    return int(lib().ferry_layout_workspace_bytes(tokens, topk, experts))
+
+
+def layout(selected, weights, experts, out=None):
+    """Sorted packet IDs/weights, per-expert starts and the stable (rows, cols) permutation."""
+    T, k = selected.shape
+    dev = selected.device
+    lay = out if out is not None else Layout()
+    if out is None:
+        lay.send_ids = torch.empty((T, k), dtype=torch.int64, device=dev)
+        lay.w_sorted = torch.empty((T, k), dtype=torch.bfloat16, device=dev)
+        lay.starts = torch.empty(experts + 1, dtype=torch.int64, device=dev)
+        lay.rows = torch.empty(T * k, dtype=torch.int64, device=dev)
+        lay.cols = torch.empty(T * k, dtype=torch.int64, device=dev)
+        lay.pair_pos = torch.empty(T * k, dtype=torch.int32, device=dev)
+        lay.workspace = torch.empty(layout_workspace_bytes(T, k, experts), dtype=torch.uint8,
+                                    device=dev)
+    lay.tokens, lay.topk, lay.experts = T, k, experts
+    check(lib().ferry_layout(
+        _dev(selected, 'selected', torch.int64),
+        _dev(weights, 'weights', torch.bfloat16) if weights is not None else None,
+        T, k, experts, lay.send_ids.data_ptr(), lay.w_sorted.data_ptr(), lay.starts.data_ptr(),
+        lay.rows.data_ptr(), lay.cols.data_ptr(), lay.pair_pos.data_ptr(),
+        lay.workspace.data_ptr(), lay.workspace.numel(), current_stream(dev)), 'layout')
+    return lay
+
+
+def expert_ffn(cache, x, w_sorted, starts, rows, cols, expert_list, slot_of, hidden,
+               intermediate, act, out, out_mode=0, max_rows=None, experts=None):
+    """Grouped SwiGLU over cache slots for the experts in ``expert_list`` (host ints)."""
+    R, k = w_sorted.shape
+    el = np.ascontiguousarray(expert_list, dtype=np.int32)
+    so = np.ascontiguousarray(slot_of, dtype=np.int32)
+    E = int(experts if experts is not None else len(so))
+    check(lib().ferry_expert_ffn(
+        _dev(cache, 'cache', torch.bfloat16), cache.shape[0], hidden, intermediate,
+        _dev(x, 'x', torch.bfloat16), R, k, _dev(w_sorted, 'w_sorted', torch.bfloat16),
+        _dev(starts, 'starts', torch.int64), _dev(rows, 'rows', torch.int64),
+        _dev(cols, 'cols', torch.int64), el.ctypes.data, len(el), so.ctypes.data, E,
+        int(max_rows if max_rows is not None else R), _dev(act, 'act', torch.bfloat16),
+        _dev(out, 'out', torch.bfloat16), int(out_mode), current_stream(x.device)), 'expert_ffn')
+    return out
+
+
+def combine(part, tokens, topk, hidden, pair_pos=None, out=None):
+    """out[t] = bf16(sum_j fp32(part[src(t, j)])), j ascending (expert_ops.cpp:75-92)."""
+    if out is None:
+        out = torch.empty((tokens, hidden), dtype=torch.bfloat16, device=part.device)
+    check(lib().ferry_combine(
+        _dev(part, 'part', torch.bfloat16),
+        _dev(pair_pos, 'pair_pos', torch.int32) if pair_pos is not None else None,
+        tokens, topk, hidden, _dev(out, 'out', torch.bfloat16), current_stream(part.device)),
+        'combine')
+    return out
+
+
+def history_update(selected, experts, window, layer, ring, counts, meta, scores, ids_out=None):
+    """Device GateHistory update of ``layer`` (ferry/metadata.py:15-38, frequency rows)."""
+    T, k = selected.shape
+    check(lib().ferry_history_update(
+        _dev(selected, 'selected', torch.int64), T, k, experts, window, layer,
+        _dev(ring, 'ring', torch.int32), _dev(counts, 'counts', torch.int32),
+        _dev(meta, 'meta', torch.int32), _dev(scores, 'scores', torch.float32),
+        _dev(ids_out, 'ids_out', torch.uint8) if ids_out is not None else None,
+        current_stream(selected.device)), 'history_update')
+
+
+# ------------------------------------------------------------------------------------------
+# The reference's pybind names (ferry/csrc/expert_ops.cpp:144-157)
+# ------------------------------------------------------------------------------------------
+
+def execute_experts(cache, input, routing_weights, slots, rows, cols, hidden, intermediate):
+    """Routed-expert MLPs of every (slot, rows, cols) group (expert_ops.cpp:16-45).
+
+    Output i is ``down(silu(x Wg^T) * (x Wu^T)) * routing_weights[rows[i], cols[i]]`` for
+    ``x = input[rows[i]]``, one bf16 [len(rows[i]), hidden] tensor per group.
+    """
+    _dev(cache, 'cache', torch.bfloat16)
+    if cache.dim() != 2 or cache.shape[1] != 3 * hidden * intermediate:
+        raise RuntimeError('cache must be [cap, 3 * hidden * intermediate]')
+    if input.dim() != 2 or input.shape[1] != hidden:
+        raise RuntimeError('input must be [rows, hidden]')
+    if routing_weights.dim() != 2 or routing_weights.shape[0] != input.shape[0]:
+        raise RuntimeError('routing_weights must be [rows, topk]')
+    if not (len(slots) == len(rows) == len(cols)):
+        raise RuntimeError('slots, rows and cols must have the same length')
+    G = len(slots)
+    if G == 0:
+        return []
+    if G > MAX_EXPERTS:
+        raise RuntimeError(f'at most {MAX_EXPERTS} groups per call')
+    for s in slots:
+        if not 0 <= int(s) < cache.shape[0]:
+            raise RuntimeError('slot out of range')
+    sizes = [int(r.numel()) for r in rows]
+    dev = input.device
+    starts = torch.tensor(np.concatenate([[0], np.cumsum(sizes)]), dtype=torch.int64, device=dev)
+    rows_cat = torch.cat([r.reshape(-1) for r in rows]).to(torch.int64).contiguous()
+    cols_cat = torch.cat([c.reshape(-1) for c in cols]).to(torch.int64).contiguous()
+    P = int(sum(sizes))
+    act = torch.empty((max(P, 1), intermediate), dtype=torch.bfloat16, device=dev)
+    out = torch.empty((max(P, 1), hidden), dtype=torch.bfloat16, device=dev)
+    expert_ffn(cache, input.contiguous(), routing_weights.contiguous(), starts, rows_cat, cols_cat,
+               np.arange(G), np.asarray(slots, np.int32), hidden, intermediate, act, out,
+               out_mode=1, max_rows=max(sizes) if sizes else 0, experts=G)
+    return list(out[:P].split(sizes))
+
+
+def pack_dispatch(hidden, selected, weights, send_idx, send_ids, experts):
+    """Dispatch packet rows ``[x (2H B) | weights in send_ids order (2k B) | IDs (k B)]``.
+
+    Reference: expert_ops.cpp:50-66.  At world = 1 the packet never leaves the GPU; this
+    builds the same byte format for API compatibility (the fused path reads the routing
+    weights in send_ids order straight from the layout kernel instead).
+    """
+    n, k = send_ids.shape
+    dense = torch.zeros((hidden.shape[0], experts), dtype=torch.float32, device=hidden.device)
+    dense.scatter_add_(1, selected, weights.float())
+    dense = dense.to(torch.bfloat16)
+    valid = send_ids.ge(0)
+    pw = dense[send_idx.unsqueeze(1), send_ids.clamp_min(0)] * valid
+    payload = torch.empty((n, 2 * hidden.shape[1] + 3 * k), dtype=torch.uint8, device=hidden.device)
+    payload[:, :2 * hidden.shape[1]] = hidden.index_select(0, send_idx).view(torch.uint8)
+    payload[:, 2 * hidden.shape[1]:2 * hidden.shape[1] + 2 * k] = pw.contiguous().view(torch.uint8)
+    payload[:, 2 * hidden.shape[1] + 2 * k:] = send_ids.to(torch.uint8)
+    return payload
+
+
+def unpack_dispatch(raw, hidden, topk):
+    """Split packet rows back into bf16 [m, H] hidden states and [m, k] weights (:68-73)."""
+    m = raw.shape[0]
+    x = raw[:, :2 * hidden].contiguous().view(torch.bfloat16).view(m, hidden)
+    w = raw[:, 2 * hidden:2 * hidden + 2 * topk].contiguous().view(torch.bfloat16).view(m, topk)
+    return [x, w]
+
+
+def reduce_partials(parts, rows, received, hidden, like):
+    """fp32 sum of expert outputs per received row, ascending group order, then bf16 (:76-83)."""
+    if len(parts) == 0:
+        return torch.zeros((received, hidden), dtype=torch.bfloat16, device=like.device)
+    part = torch.cat([p.reshape(-1, hidden) for p in parts]).to(torch.bfloat16).contiguous()
+    rows_cat = torch.cat([r.reshape(-1) for r in rows]).to(torch.int64)
+    # the j-th occurrence (in group order) of each row is its j-th term
+    order = torch.argsort(rows_cat, stable=True)
+    counts = torch.bincount(rows_cat, minlength=received)
+    k = max(int(counts.max().item()) if counts.numel() else 1, 1)
+    first = torch.cumsum(counts, 0) - counts
+    rank = torch.arange(order.numel(), device=like.device) - first[rows_cat[order]]
+    pair_pos = torch.full((received * k,), -1, dtype=torch.int32, device=like.device)
+    pair_pos[rows_cat[order] * k + rank] = order.to(torch.int32)
+    return combine(part, received, k, hidden, pair_pos=pair_pos)
+
+
+def scatter_returned(returned, send_idx, tokens):
+    """Add returned rows back to their tokens in fp32 (expert_ops.cpp:86-92)."""
+    output = torch.zeros((tokens, returned.shape[1]), dtype=torch.float32, device=returned.device)
+    if returned.shape[0]:
+        output.index_add_(0, send_idx, returned.float())
+    return output.to(returned.dtype)

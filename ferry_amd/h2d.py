@@ -1,0 +1,79 @@
+"""H2D expert fetch engine (the reference's ``H2DEngine``, ferry/csrc/expert_ops.cpp:94-142).
+
+Copies rows of a pinned host pool into GPU cache slots with ``hipMemcpyAsync`` on the
+engine's own stream.  A copy into a slot waits, on the GPU, for the last compute that read
+that slot (``mark_used``).  ``wait_host`` blocks the host like the reference;
+``wait_stream`` makes a compute stream wait on the GPU instead, which lets resident experts
+run while missing ones are still in flight.
+"""
+import ctypes
+
+import numpy as np
+import torch
+
+from ._lib import check, lib
+
+
+def _i64(values):
+    return np.ascontiguousarray(np.asarray(values, dtype=np.int64).reshape(-1))
+
+
+class H2DEngine:
+    def __init__(self, cache, pool):
+        if not (isinstance(cache, torch.Tensor) and cache.device.type == 'cuda' and cache.is_contiguous()):
+            raise RuntimeError('cache must be a contiguous CUDA tensor')
+        if not (isinstance(pool, torch.Tensor) and pool.is_pinned() and pool.is_contiguous()):
+            raise RuntimeError('pool must be a contiguous pinned host tensor')
+        if pool.dim() != 2 or cache.dim() != 2 or pool.shape[1] != cache.shape[1] or pool.dtype != cache.dtype:
+            raise RuntimeError('pool rows must match cache rows')
+        self._cache, self._pool = cache, pool   # keep both alive, like the reference
+        handle = ctypes.c_void_p()
+        check(lib().ferry_h2d_create(cache.data_ptr(), cache.shape[0], pool.data_ptr(), pool.shape[0],
+                                     cache.shape[1] * cache.element_size(), cache.device.index or 0,
+                                     ctypes.byref(handle)), 'H2DEngine')
+        self._h = handle.value
+
+    def fetch(self, slots, keys):
+        s, k = _i64(slots), _i64(keys)
+        if len(s) != len(k):
+            raise RuntimeError('slots and keys must have the same length')
+        check(lib().ferry_h2d_fetch(self._h, s.ctypes.data, k.ctypes.data, len(s)), 'H2DEngine.fetch')
+
+    def wait_host(self, slots):
+        s = _i64(slots)
+        check(lib().ferry_h2d_wait_host(self._h, s.ctypes.data, len(s)), 'H2DEngine.wait_host')
+
+    def wait_stream(self, slots, stream=None):
+        s = _i64(slots)
+        st = stream if stream is not None else torch.cuda.current_stream(self._cache.device)
+        check(lib().ferry_h2d_wait_stream(self._h, s.ctypes.data, len(s), st.cuda_stream),
+              'H2DEngine.wait_stream')
+
+    def mark_used(self, slots, stream=None):
+        s = _i64(slots)
+        st = stream if stream is not None else torch.cuda.current_stream(self._cache.device)
+        check(lib().ferry_h2d_mark_used(self._h, s.ctypes.data, len(s), st.cuda_stream),
+              'H2DEngine.mark_used')
+
+    def synchronize(self):
+        check(lib().ferry_h2d_synchronize(self._h), 'H2DEngine.synchronize')
+
+    @property
+    def copies(self):
+        return int(lib().ferry_h2d_copies(self._h))
+
+    @property
+    def stream(self):
+        """The engine's copy stream as a torch.cuda.ExternalStream."""
+        return torch.cuda.ExternalStream(lib().ferry_h2d_stream(self._h), device=self._cache.device)
+
+    def close(self):
+        if getattr(self, '_h', None):
+            lib().ferry_h2d_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

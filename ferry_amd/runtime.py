@@ -1,0 +1,202 @@
+"""One-GPU offloading runtime for routed experts (reference: ferry/runtime.py).
+
+Per MoE layer call (world = 1):
+  1. history: the device window counters of the layer are updated from ``selected``; the
+     expert IDs (uint8) and the layer's scores are copied to pinned host memory in one D2H
+     copy -- the host must know the misses to enqueue fetches;
+  2. the layout kernel is enqueued before the host waits for that copy, so it overlaps the
+     host planning;
+  3. the C++ planner picks the misses (ascending expert) and their slots (routing-aware
+     eviction, bit-exact with the reference) and the H2D engine enqueues their copies on its
+     own stream;
+  4. experts already resident run first; the compute stream then waits on the GPU for the
+     copies and runs the fetched experts (``overlap=False`` restores the reference's serial
+     host wait);
+  5. the combine kernel sums each token's k expert rows in fp32 (ascending expert ID).
+"""
+import time
+
+import numpy as np
+import torch
+import torch.distributed as dist
+
+from . import expert_ops as ops
+from .metadata import DeviceGateHistory, GateHistory, RouteGather
+from .policy import Controller, layer_slots
+from .transport import Transport
+
+
+def expert_ops():
+    """The native op module (reference: ferry/runtime.py:26-31)."""
+    return ops
+
+
+class OffloadRuntime:
+    def __init__(self, spec, pool, capacities, policy, topology, history_window=128,
+                 balance_tol_bps=200, salt=1, eviction_score='frequency', overlap=True,
+                 timing=False):
+        if dist.is_available() and dist.is_initialized() and dist.get_world_size() != 1:
+            raise NotImplementedError('this build runs one GPU (world = 1)')
+        if len(capacities) != 1:
+            raise NotImplementedError('this build runs one GPU (world = 1)')
+        self.spec = spec
+        self.pool = pool
+        self.rank, self.world = 0, 1
+        self.capacities = capacities
+        self.cap = capacities[0]
+        self.window = history_window
+        self.overlap = overlap
+        self.timing = timing
+        self.ops = expert_ops()
+        self.device = torch.device('cuda', torch.cuda.current_device())
+        self.cache = torch.empty((self.cap, spec.expert_elements), dtype=torch.bfloat16,
+                                 device=self.device)
+        self.controller = Controller(spec, capacities, policy, topology, balance_tol_bps, salt)
+        self.gather = RouteGather(spec.topk, spec.experts, history_window, eviction_score)
+        self.transport = Transport(self.ops, spec.topk, spec.experts)
+        self._scores_dev = torch.zeros(spec.experts, dtype=torch.float32, device=self.device)
+        self._scores_host = torch.zeros(spec.experts, dtype=torch.float32, pin_memory=True)
+        self._ids_dev = None
+        self._ids_host = None
+        self._bufs = {}
+        self.h2d = None
+        self.reset()
+
+    # -- state -------------------------------------------------------------------------------
+
+    def reset(self):
+        """Empty expert cache and routing history (start of every measured run)."""
+        if self.h2d is not None:
+            self.h2d.synchronize()
+        torch.cuda.synchronize(self.device)
+        self.controller.reset()
+        spec = self.spec
+        self.history = GateHistory(spec.layers, spec.experts, self.window)
+        self.device_history = DeviceGateHistory(spec.layers, spec.experts, spec.topk, self.window,
+                                                self.device)
+        if self.h2d is not None:
+            self.h2d.close()
+        self.h2d = self.ops.H2DEngine(self.cache, self.pool)
+        self.event = 0
+        self.fetches_per_rank = np.zeros(self.world, np.int64)
+        self.decode_fetches_per_rank = np.zeros(self.world, np.int64)
+        self.serial_wait_ns = 0
+        self.timings = []
+
+    def _buffers(self, tokens):
+        b = self._bufs.get(tokens)
+        if b is None:
+            spec, k = self.spec, self.spec.topk
+            b = dict(act=torch.empty((tokens * k, spec.intermediate), dtype=torch.bfloat16,
+                                     device=self.device),
+                     part=torch.empty((tokens * k, spec.hidden), dtype=torch.bfloat16,
+                                      device=self.device),
+                     layout=None)
+            self._bufs[tokens] = b
+        if self._ids_dev is None or self._ids_dev.numel() < tokens * self.spec.topk:
+            n = tokens * self.spec.topk
+            self._ids_dev = torch.empty(n, dtype=torch.uint8, device=self.device)
+            self._ids_host = torch.empty(n, dtype=torch.uint8, pin_memory=True)
+        return b
+
+    # -- one layer call ------------------------------------------------------------------------
+
+    def execute(self, layer, hidden, selected, weights, probs_tail):
+        spec = self.spec
+        T, k = selected.shape
+        E = spec.experts
+        if hidden.dtype != torch.bfloat16 or hidden.dim() != 2 or hidden.shape[1] != spec.hidden:
+            raise RuntimeError('hidden must be bf16 [tokens, hidden]')
+        stream = torch.cuda.current_stream(self.device)
+        buf = self._buffers(T)
+        selected = selected.contiguous()
+        weights = weights.to(torch.bfloat16).contiguous()
+
+        # 1. history + D2H of the IDs (and scores)
+        frequency = self.gather.score == 'frequency'
+        ids_dev = self._ids_dev[:T * k]
+        if frequency:
+            self.device_history.update(layer, selected, self._scores_dev, ids_dev)
+            self._scores_host.copy_(self._scores_dev, non_blocking=True)
+        else:
+            ids_dev.copy_(selected.reshape(-1).to(torch.uint8))
+        ids_host = self._ids_host[:T * k]
+        ids_host.copy_(ids_dev, non_blocking=True)
+        tail_host = None
+        if not frequency:
+            tail = min(T, self.window)
+            tail_host = probs_tail[-tail:].float().to('cpu', non_blocking=True)
+        d2h = torch.cuda.Event()
+        d2h.record(stream)
+
+        # 2. layout (overlaps the host planning)
+        buf['layout'] = self.ops.layout(selected, weights, E, out=buf['layout'])
+        lay = buf['layout']
+
+        # 3. plan + fetch
+        d2h.synchronize()
+        ids = ids_host.numpy().astype(np.int64).reshape(T, k)
+        if frequency:
+            scores = self._scores_host.numpy().copy()
+        else:
+            self.history.update(layer, tail_host.numpy())
+            scores = self.history.scores(layer)
+        origins = np.zeros(T, np.int64)
+        fetches, destinations, counts = self.controller.plan(self.event, layer, ids, origins, scores)
+        self.fetches_per_rank += counts
+        if self.event >= spec.layers:
+            self.decode_fetches_per_rank += counts
+        fetch_slots = fetches[:, 2]
+        timing = self.timing and len(fetch_slots) > 0
+        if timing:
+            copy_stream = self.h2d.stream
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+            ev[0].record(copy_stream)
+        self.h2d.fetch(fetch_slots, fetches[:, 1])
+        if timing:
+            ev[1].record(copy_stream)
+
+        # 4. experts: resident first, then the fetched ones
+        slot_of = layer_slots(self.controller.slots[0], self.cap, layer, E)
+        active = np.zeros(E, bool)
+        active[ids.reshape(-1)] = True
+        missing = np.zeros(E, bool)
+        missing[fetches[:, 1] - layer * E] = True
+        resident_list = np.flatnonzero(active & ~missing)
+        missing_list = np.flatnonzero(missing)
+        slot32 = slot_of.astype(np.int32)
+        common = (self.cache, hidden.contiguous(), lay.w_sorted, lay.starts, lay.rows, lay.cols)
+        if not self.overlap and len(fetch_slots):
+            started = time.perf_counter_ns()
+            self.h2d.wait_host(fetch_slots)
+            self.serial_wait_ns += time.perf_counter_ns() - started
+        if len(resident_list):
+            self.h2d.wait_stream(slot_of[resident_list], stream)
+            self.ops.expert_ffn(*common, resident_list, slot32, spec.hidden, spec.intermediate,
+                                buf['act'], buf['part'], out_mode=0, max_rows=T, experts=E)
+        if len(missing_list):
+            if timing:
+                ev[2].record(stream)
+            self.h2d.wait_stream(fetch_slots, stream)
+            if timing:
+                ev[3].record(stream)
+            self.ops.expert_ffn(*common, missing_list, slot32, spec.hidden, spec.intermediate,
+                                buf['act'], buf['part'], out_mode=0, max_rows=T, experts=E)
+        self.h2d.mark_used(slot_of[np.flatnonzero(active)], stream)
+        if timing:
+            self.timings.append(ev)
+        self.event += 1
+
+        # 5. combine
+        return self.transport.combine(hidden, buf['part'], dict(layout=lay))
+
+    def fetch_timing(self):
+        """(total fetch ms, exposed wait ms) over the layer calls recorded with timing=True."""
+        torch.cuda.synchronize(self.device)
+        fetch = sum(e[0].elapsed_time(e[1]) for e in self.timings)
+        exposed = sum(max(0.0, e[2].elapsed_time(e[3])) for e in self.timings)
+        return fetch, exposed
+
+    def close(self):
+        if self.h2d is not None:
+            self.h2d.synchronize()

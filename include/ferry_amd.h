@@ -1,0 +1,152 @@
+/*
+ * ferry_amd -- C ABI of the MI355X-native per-GPU MoE hot path of FERRY.
+ *
+ * Every entry point takes raw device pointers, int64 sizes and a hipStream_t (passed as
+ * void*), returns 0 on success and a non-zero status on error; ferry_last_error() then
+ * returns a thread-local message.  Apart from the H2D engine handle (which owns one HIP
+ * stream and per-slot events) the library allocates no memory: scratch space is passed in
+ * by the caller.  All index arrays are int64 like the reference's (torch.long) tensors.
+ *
+ * The replaced reference interfaces are cited per entry point (paths are relative to the
+ * FERRY repository).
+ */
+#ifndef FERRY_AMD_H
+#define FERRY_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Thread-local description of the last failure of any entry point. */
+const char* ferry_last_error(void);
+/* ABI version of this library (bumped on any signature change). */
+int32_t ferry_abi_version(void);
+
+enum { FERRY_BF16 = 0, FERRY_F32 = 1 };
+
+/*
+ * Router: fp32 softmax over each row of logits[T, E], top-k, optional renormalisation of the
+ * k weights, multiplication by `scale`, cast to bf16.
+ * Replaces ferry/model.py:141-146 (Qwen3 hook: softmax(dtype=fp32), topk(k) sorted,
+ * w /= w.sum(), .to(bf16)) and the greedy DeepSeek-V2 gate whose outputs reach
+ * ferry/model.py:151-157 (softmax, topk(sorted=False), * routed_scaling_factor, .to(bf16)).
+ * Selection reproduces torch's CPU topk exactly, ties included.  probs_out (nullable)
+ * receives the fp32 probabilities [T, E]; tie_rows (nullable, one int32 counter) counts
+ * rows that took the exact tie-resolution path.
+ */
+int ferry_router_topk(const void* logits, int32_t logits_dtype, int64_t tokens, int64_t experts,
+                      int64_t topk, int32_t renorm, float scale, int32_t sorted,
+                      int64_t* idx_out, void* w_out_bf16, float* probs_out, int32_t* tie_rows,
+                      void* stream);
+
+/*
+ * Dispatch layout at world = 1.  Replaces ferry/layout.py:12-94 (build_layout +
+ * device_layout: sorted packet IDs, per-expert counts, exclusive prefix, stable
+ * (rows, cols) counting sort) and the packet-weight reorder of pack_dispatch
+ * (ferry/csrc/expert_ops.cpp:57-60).  Outputs, all device memory:
+ *   send_ids[T,k]   int64  expert IDs of each token, ascending
+ *   w_sorted[T,k]   bf16   routing weight of send_ids[t,j]
+ *   starts[E+1]     int64  exclusive prefix of the per-expert counts
+ *   rows[T*k]       int64  token of each (expert, rank) entry, ascending token per expert
+ *   cols[T*k]       int64  position of that expert in the token's sorted ID list
+ *   pair_pos[T*k]   int32  inverse map: pair_pos[t*k+j] = grouped position (nullable)
+ * `workspace` must hold ferry_layout_workspace_bytes(T, k, E) bytes of device memory.
+ */
+int64_t ferry_layout_workspace_bytes(int64_t tokens, int64_t topk, int64_t experts);
+int ferry_layout(const int64_t* selected, const void* weights_bf16, int64_t tokens, int64_t topk,
+                 int64_t experts, int64_t* send_ids, void* w_sorted_bf16, int64_t* starts,
+                 int64_t* rows, int64_t* cols, int32_t* pair_pos, void* workspace,
+                 int64_t workspace_bytes, void* stream);
+
+/*
+ * Grouped SwiGLU over resident cache slots.  Replaces ferry/csrc/expert_ops.cpp:13-45
+ * (execute_experts: per expert x = in[rows]; g = x Wg^T; u = x Wu^T; a = silu(g) * u;
+ * y = a Wd^T; out = y * w[rows, cols]) and the silu_mul kernel of
+ * ferry/csrc/expert_ops.cu:6-25.  cache[slot] = [gate I*H | up I*H | down H*I] bf16.
+ * The experts computed are expert_list[0..n_list); slot_of[e] gives the cache slot of
+ * expert e (host arrays, at most FERRY_MAX_EXPERTS entries).  x is bf16 [R, H];
+ * w_sorted bf16 [R, k]; starts/rows/cols come from ferry_layout.  act is bf16 scratch of
+ * [R*k, I] elements.  out_mode 0 writes bf16 rows out[rows[p]*k + cols[p]] (token-major,
+ * the combine input); out_mode 1 writes row p of out (grouped order).
+ * max_rows_per_expert bounds n_e (R is always a valid bound).
+ */
+enum { FERRY_MAX_EXPERTS = 512 };
+int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t hidden, int64_t inter,
+                     const void* x, int64_t rows_in, int64_t topk, const void* w_sorted,
+                     const int64_t* starts, const int64_t* rows, const int64_t* cols,
+                     const int32_t* expert_list, int32_t n_list, const int32_t* slot_of,
+                     int64_t experts, int64_t max_rows_per_expert, void* act, void* out,
+                     int32_t out_mode, void* stream);
+
+/*
+ * Combine: out[t, :] = bf16( sum_{j<k} fp32(part[src(t, j), :]) ), j ascending (= ascending
+ * expert ID).  src(t, j) = pair_pos[t*k+j] when pair_pos is non-null, else t*k+j.
+ * Replaces ferry/csrc/expert_ops.cpp:75-92 (reduce_partials: fp32 index_add_ over experts in
+ * ascending order, then bf16; scatter_returned: identity at world = 1).
+ */
+int ferry_combine(const void* part, const int32_t* pair_pos, int64_t tokens, int64_t topk,
+                  int64_t hidden, void* out, void* stream);
+
+/*
+ * Selection-frequency history on the device.  Replaces ferry/metadata.py:15-38 (GateHistory
+ * update/scores over one-hot rows built by RouteGather.collect, ferry/metadata.py:169-176).
+ * State per layer (device memory, caller-owned, zero-initialised):
+ *   ring[L, W, k] int32, counts[L, E] int32, meta[L, 2] int32 (count, head).
+ * Update with the last min(T, W) tokens of selected[T, k]; then scores_out[E] =
+ * float32(count_e / max(1, n)).  ids_out (nullable) receives selected as uint8 [T*k]
+ * (the D2H payload of the host planner).
+ */
+int ferry_history_update(const int64_t* selected, int64_t tokens, int64_t topk, int64_t experts,
+                         int64_t window, int64_t layer, int32_t* ring, int32_t* counts,
+                         int32_t* meta, float* scores_out, uint8_t* ids_out, void* stream);
+
+/*
+ * Host planner at world = 1.  Replaces ferry/policy.py:130-194 (plan_layer with
+ * FERRY/RANDOM at world = 1, the quota check of ferry/quota.py:63) and :109-127
+ * (_choose_slot).  State arrays are host memory owned by the caller:
+ *   slots[cap], owner[L*E], last[L*E] int64; scores[L*E] float32.
+ * Returns the number of misses m (fetches_out receives m rows of (0, key, slot) in ascending
+ * expert order), or -1 with ferry_last_error() set when the misses exceed the admission
+ * capacity.  destinations_out (nullable) receives owner[layer*E + selected[t,j]].
+ */
+int64_t ferry_plan_layer(int64_t event, int64_t layer, const int64_t* selected, int64_t tokens,
+                         int64_t topk, const float* gate_scores, int64_t* slots, int64_t cap,
+                         int64_t* owner, int64_t* last, float* scores, int64_t experts,
+                         int64_t* fetches_out, int64_t* destinations_out);
+int64_t ferry_choose_slot(int64_t layer, const uint8_t* active, const int64_t* slots,
+                          int64_t cap, const int64_t* last, const float* scores, int64_t experts);
+/* ferry/policy.py:197-205 */
+void ferry_layer_slots(const int64_t* slots, int64_t cap, int64_t layer, int64_t experts,
+                       int64_t* lookup);
+
+/*
+ * H2D expert fetch engine.  Replaces the H2DEngine class of ferry/csrc/expert_ops.cpp:94-142.
+ * The engine copies pool rows (pinned host memory) into cache slots on its own stream; a copy
+ * into a slot first waits (GPU-side) for the last compute that read the slot.
+ */
+typedef struct ferry_h2d ferry_h2d;
+int ferry_h2d_create(void* cache, int64_t cache_rows, const void* pool, int64_t pool_rows,
+                     int64_t row_bytes, int32_t device, ferry_h2d** out);
+int ferry_h2d_destroy(ferry_h2d* h);
+/* expert_ops.cpp:107-117 */
+int ferry_h2d_fetch(ferry_h2d* h, const int64_t* slots, const int64_t* keys, int64_t n);
+/* expert_ops.cpp:119-122: host blocks until the slots' copies are done */
+int ferry_h2d_wait_host(ferry_h2d* h, const int64_t* slots, int64_t n);
+/* GPU-side variant: `stream` waits for the slots' copies without blocking the host */
+int ferry_h2d_wait_stream(ferry_h2d* h, const int64_t* slots, int64_t n, void* stream);
+/* expert_ops.cpp:124-128 */
+int ferry_h2d_mark_used(ferry_h2d* h, const int64_t* slots, int64_t n, void* stream);
+/* expert_ops.cpp:130-133 */
+int ferry_h2d_synchronize(ferry_h2d* h);
+/* expert_ops.cpp:135 */
+int64_t ferry_h2d_copies(const ferry_h2d* h);
+/* the engine's copy stream (for event timing by the caller) */
+void* ferry_h2d_stream(ferry_h2d* h);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FERRY_AMD_H */

@@ -1,0 +1,291 @@
+"""Parity of each HIP kernel (through the C ABI) with the CPU oracle."""
+import numpy as np
+import pytest
+import torch
+
+from oracle.experts import execute_experts_ref, moe_layer_ref, reduce_partials_ref
+from oracle.history import GateHistoryRef, frequency_rows
+from oracle.layout import layout_closed_form
+from oracle.router import deepseek_router, qwen3_router
+
+pytestmark = pytest.mark.gpu
+
+BF16_REL = 2.0 ** -8  # one bf16 ulp, relative
+
+
+def _ops():
+    from ferry_amd import expert_ops
+    return expert_ops
+
+
+def _logits(T, E, dtype, seed, ties=False, zipf=0.0):
+    g = torch.Generator().manual_seed(seed)
+    z = torch.randn((T, E), generator=g)
+    if zipf:
+        r = torch.arange(1, E + 1, dtype=torch.float64)
+        p = r ** -zipf
+        z = z + torch.log(p / p.sum()).float()[torch.randperm(E, generator=g)]
+    if ties:
+        z = torch.round(z * 3) / 3   # few distinct values per row: many ties at every position
+    return z.to(dtype)
+
+
+# ---------------------------------------------------------------------------------------------
+# router
+# ---------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize('E,k', [(128, 8), (64, 6), (16, 4), (256, 8), (32, 1), (8, 8), (200, 3)])
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize('ties', [False, True])
+def test_router_sorted_matches_torch_cpu_topk(device, E, k, dtype, ties):
+    ops = _ops()
+    T = 777
+    logits = _logits(T, E, dtype, seed=E * 31 + k, ties=ties)
+    w_ref, sel_ref, p_ref = qwen3_router(logits, k)
+    counter = torch.zeros(1, dtype=torch.int32, device=device)
+    w, sel, probs = ops.router_topk(logits.to(device), k, renorm=True, return_probs=True,
+                                    tie_counter=counter)
+    torch.cuda.synchronize()
+    assert torch.equal(sel.cpu(), sel_ref), 'routing indices differ from torch.topk on the CPU'
+    torch.testing.assert_close(probs.cpu(), p_ref, rtol=1e-5, atol=1e-7)
+    wd = (w.cpu().float() - w_ref.float()).abs()
+    assert bool((wd <= BF16_REL * w_ref.float().abs() + 1e-7).all())
+    if ties:
+        assert int(counter.item()) > 0, 'the exact tie path was not exercised'
+
+
+@pytest.mark.parametrize('E,k', [(64, 6), (128, 8), (16, 5)])
+@pytest.mark.parametrize('ties', [False, True])
+def test_router_unsorted_deepseek(device, E, k, ties):
+    ops = _ops()
+    T = 500
+    logits = _logits(T, E, torch.float32, seed=7 + E, ties=ties)
+    w_ref, sel_ref, _ = deepseek_router(logits, k, 1.0)
+    w, sel = ops.router_topk(logits.to(device), k, renorm=False, scale=1.0, sorted=False)
+    torch.cuda.synchronize()
+    assert torch.equal(sel.cpu(), sel_ref)
+    wd = (w.cpu().float() - w_ref.float()).abs()
+    assert bool((wd <= BF16_REL * w_ref.float().abs() + 1e-7).all())
+
+
+def test_router_full_size_qwen3_prefill(device):
+    """8192 tokens x 128 experts, Zipf(1.1)-skewed bf16 logits (the prefill shape)."""
+    ops = _ops()
+    logits = _logits(8192, 128, torch.bfloat16, seed=1, zipf=1.1)
+    w_ref, sel_ref, _ = qwen3_router(logits, 8)
+    w, sel = ops.router_topk(logits.to(device), 8)
+    torch.cuda.synchronize()
+    assert torch.equal(sel.cpu(), sel_ref)
+
+
+def test_router_empty_and_errors(device):
+    ops = _ops()
+    w, sel = ops.router_topk(torch.empty((0, 64), dtype=torch.bfloat16, device=device), 6)
+    assert w.shape == (0, 6) and sel.shape == (0, 6)
+    with pytest.raises(RuntimeError):
+        ops.router_topk(torch.zeros((4, 300), dtype=torch.bfloat16, device=device), 8)
+    with pytest.raises(RuntimeError):
+        ops.router_topk(torch.zeros((4, 16), dtype=torch.bfloat16, device=device), 17)
+
+
+# ---------------------------------------------------------------------------------------------
+# layout
+# ---------------------------------------------------------------------------------------------
+
+def _selected(T, E, k, seed, zipf=0.0):
+    logits = _logits(T, E, torch.float32, seed, zipf=zipf)
+    return torch.topk(logits, k, dim=-1).indices.contiguous()
+
+
+@pytest.mark.parametrize('T,E,k', [(1, 8, 2), (16, 128, 8), (1000, 64, 6), (1024, 128, 8),
+                                   (1025, 128, 8), (4097, 512, 16), (65536, 64, 6), (8192, 128, 8)])
+def test_layout_bit_exact(device, T, E, k):
+    ops = _ops()
+    sel = _selected(T, E, k, seed=T + E, zipf=1.1)
+    w = torch.randn((T, k)).to(torch.bfloat16)
+    ref = layout_closed_form(sel.numpy(), E, w.view(torch.int16).numpy())
+    lay = ops.layout(sel.to(device), w.to(device), E)
+    torch.cuda.synchronize()
+    assert np.array_equal(lay.send_ids.cpu().numpy(), ref['send_ids'])
+    assert np.array_equal(lay.w_sorted.cpu().view(torch.int16).numpy(), ref['w_sorted'])
+    assert np.array_equal(lay.starts.cpu().numpy(), ref['starts'])
+    assert np.array_equal(lay.rows.cpu().numpy(), ref['rows'])
+    assert np.array_equal(lay.cols.cpu().numpy(), ref['cols'])
+    assert np.array_equal(lay.pair_pos.cpu().numpy(), ref['pair_pos'])
+
+
+# ---------------------------------------------------------------------------------------------
+# device history
+# ---------------------------------------------------------------------------------------------
+
+def test_device_history_matches_gate_history(device):
+    from ferry_amd.metadata import DeviceGateHistory
+    L, E, k, W = 3, 128, 8, 128
+    hist = DeviceGateHistory(L, E, k, W, device)
+    ref = GateHistoryRef(L, E, W)
+    rng = np.random.default_rng(0)
+    scores = torch.empty(E, dtype=torch.float32, device=device)
+    ids = torch.empty(4096 * k, dtype=torch.uint8, device=device)
+    for step, T in enumerate([1, 16, 64, 200, 3, 127, 128, 129, 16, 16, 500, 5, 1, 64]):
+        layer = step % L
+        sel = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int64)
+        hist.update(layer, torch.from_numpy(sel).to(device), scores, ids[:T * k])
+        ref.update(layer, frequency_rows(sel, E, W))
+        torch.cuda.synchronize()
+        assert np.array_equal(scores.cpu().numpy(), ref.scores(layer)), f'step {step}'
+        assert np.array_equal(ids[:T * k].cpu().numpy(), sel.reshape(-1).astype(np.uint8))
+
+
+# ---------------------------------------------------------------------------------------------
+# expert FFN + combine
+# ---------------------------------------------------------------------------------------------
+
+def _pool(n, H, I, seed):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn((n, 3 * H * I), generator=g) * 0.02).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize('T,E,k,H,I,zipf', [
+    (16, 128, 8, 2048, 768, 1.1),     # decode layer shape (skinny kernels only)
+    (300, 16, 4, 256, 128, 1.5),      # mixed skinny / tiled experts
+    (700, 8, 2, 512, 256, 0.5),       # tiled-heavy
+    (64, 64, 6, 2048, 1408, 0.9),     # DeepSeek-V2-Lite expert shape
+])
+def test_expert_ffn_and_combine_vs_oracle(device, T, E, k, H, I, zipf):
+    ops = _ops()
+    rows_w = _pool(E, H, I, seed=T)
+    g = torch.Generator().manual_seed(T + 1)
+    x = torch.randn((T, H), generator=g).to(torch.bfloat16)
+    sel = _selected(T, E, k, seed=T + 2, zipf=zipf)
+    w = torch.softmax(torch.randn((T, k), generator=g), -1).to(torch.bfloat16)
+    # cache holds the experts in reverse slot order, to exercise slot_of
+    cache = rows_w.flip(0).contiguous().to(device)
+    slot_of = np.arange(E)[::-1].astype(np.int32).copy()
+    lay = ops.layout(sel.to(device), w.to(device), E)
+    act = torch.empty((T * k, I), dtype=torch.bfloat16, device=device)
+    part = torch.empty((T * k, H), dtype=torch.bfloat16, device=device)
+    active = np.unique(sel.numpy())
+    ops.expert_ffn(cache, x.to(device), lay.w_sorted, lay.starts, lay.rows, lay.cols, active, slot_of,
+                   H, I, act, part, out_mode=0)
+    out = ops.combine(part, T, k, H)
+    torch.cuda.synchronize()
+    # per-(token, expert) rows vs the reference op order
+    ref_lay = layout_closed_form(sel.numpy(), E, w.float().numpy())
+    w_sorted = torch.from_numpy(ref_lay['w_sorted']).to(torch.bfloat16)
+    groups = [e for e in range(E) if ref_lay['counts'][e] > 0]
+    rows = [torch.from_numpy(ref_lay['rows'][ref_lay['starts'][e]:ref_lay['starts'][e + 1]]) for e in groups]
+    cols = [torch.from_numpy(ref_lay['cols'][ref_lay['starts'][e]:ref_lay['starts'][e + 1]]) for e in groups]
+    parts = execute_experts_ref([rows_w[e] for e in groups], x, w_sorted, rows, cols, H, I)
+    got_part = part.cpu().float().view(T, k, H)
+    for e, r, c, p in zip(groups, rows, cols, parts):
+        torch.testing.assert_close(got_part[r, c], p.float(), rtol=2e-2, atol=1e-2)
+    ref = reduce_partials_ref(parts, rows, T, H)
+    torch.testing.assert_close(out.cpu().float(), ref.float(), rtol=2e-2, atol=1e-2)
+    # the combine itself is exact: same fp32 additions in the same order as reduce_partials
+    mine = reduce_partials_ref([got_part[r, c].to(torch.bfloat16) for r, c in zip(rows, cols)], rows, T, H)
+    assert torch.equal(out.cpu(), mine)
+
+
+def test_execute_experts_api(device):
+    """The reference's execute_experts signature (expert_ops.cpp:16-45) on groups of any size."""
+    ops = _ops()
+    H, I, cap = 256, 128, 6
+    rows_w = _pool(cap, H, I, seed=3)
+    cache = rows_w.to(device)
+    g = torch.Generator().manual_seed(5)
+    R, k = 150, 3
+    x = torch.randn((R, H), generator=g).to(torch.bfloat16)
+    rw = torch.rand((R, k), generator=g).to(torch.bfloat16)
+    sizes = [1, 70, 0, 150, 33]
+    slots = [4, 0, 2, 5, 1]
+    rows = [torch.randperm(R, generator=g)[:n].sort().values for n in sizes]
+    cols = [torch.randint(0, k, (n,), generator=g) for n in sizes]
+    got = ops.execute_experts(cache, x.to(device), rw.to(device), slots, [r.to(device) for r in rows],
+                              [c.to(device) for c in cols], H, I)
+    ref = execute_experts_ref([rows_w[s] for s in slots], x, rw, rows, cols, H, I)
+    assert [t.shape[0] for t in got] == sizes
+    for a, b in zip(got, ref):
+        torch.testing.assert_close(a.cpu().float(), b.float(), rtol=2e-2, atol=1e-2)
+
+
+def test_full_layer_matches_fp64(device):
+    """bf16 MoE output within rel 2e-2 / abs 1e-2 of the reference's fp32-accumulated result."""
+    ops = _ops()
+    from oracle.experts import moe_fp64
+    T, E, k, H, I = 512, 32, 8, 1024, 256
+    rows_w = _pool(E, H, I, seed=11)
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn((T, H), generator=g).to(torch.bfloat16)
+    logits = _logits(T, E, torch.bfloat16, seed=13, zipf=1.1)
+    w_ref, sel_ref, _ = qwen3_router(logits, k)
+    w, sel = ops.router_topk(logits.to(device), k)
+    lay = ops.layout(sel, w, E)
+    act = torch.empty((T * k, I), dtype=torch.bfloat16, device=device)
+    part = torch.empty((T * k, H), dtype=torch.bfloat16, device=device)
+    ops.expert_ffn(rows_w.to(device), x.to(device), lay.w_sorted, lay.starts, lay.rows, lay.cols,
+                   np.unique(sel_ref.numpy()), np.arange(E, dtype=np.int32), H, I, act, part)
+    out = ops.combine(part, T, k, H).cpu().float()
+    ref = moe_layer_ref(lambda e: rows_w[e], x, sel_ref, w_ref, E, H, I).float()
+    torch.testing.assert_close(out, ref, rtol=2e-2, atol=1e-2)
+    exact = moe_fp64(lambda e: rows_w[e], x, sel_ref, w_ref, H, I).float()
+    torch.testing.assert_close(out, exact, rtol=2e-2, atol=1e-2)
+
+
+# ---------------------------------------------------------------------------------------------
+# H2D engine
+# ---------------------------------------------------------------------------------------------
+
+def test_h2d_fetch_and_counters(device):
+    from ferry_amd.h2d import H2DEngine
+    rows, cap, width = 10, 4, 1 << 16
+    pool = torch.arange(rows * width, dtype=torch.int32).view(rows, width).to(torch.bfloat16).pin_memory()
+    cache = torch.zeros((cap, width), dtype=torch.bfloat16, device=device)
+    eng = H2DEngine(cache, pool)
+    eng.fetch([2, 0, 3], [7, 1, 9])
+    eng.wait_host([2, 0, 3])
+    assert eng.copies == 3
+    assert torch.equal(cache[2].cpu(), pool[7]) and torch.equal(cache[0].cpu(), pool[1])
+    assert torch.equal(cache[3].cpu(), pool[9])
+    s = torch.cuda.current_stream()
+    eng.fetch([1], [4])
+    eng.wait_stream([1], s)
+    snap = cache[1].clone()      # ordered after the copy by the GPU-side wait
+    torch.cuda.synchronize()
+    assert torch.equal(snap.cpu(), pool[4])
+    with pytest.raises(RuntimeError):
+        eng.fetch([cap], [0])
+    with pytest.raises(RuntimeError):
+        H2DEngine(cache, pool.clone())   # not pinned
+    eng.synchronize()
+    eng.close()
+
+
+def test_h2d_copy_waits_for_last_use(device):
+    """A fetch into a slot must not overwrite it before the compute that reads it ends."""
+    ops = _ops()
+    from ferry_amd.h2d import H2DEngine
+    H, I, T, k, E = 2048, 768, 64, 1, 2
+    rows_w = _pool(2, H, I, seed=21)
+    pool = rows_w.pin_memory()
+    cache = torch.zeros((1, 3 * H * I), dtype=torch.bfloat16, device=device)
+    eng = H2DEngine(cache, pool)
+    eng.fetch([0], [0])
+    s = torch.cuda.current_stream()
+    eng.wait_stream([0], s)
+    x = torch.randn((T, H)).to(torch.bfloat16)
+    sel = torch.zeros((T, 1), dtype=torch.int64)
+    w = torch.ones((T, 1), dtype=torch.bfloat16)
+    lay = ops.layout(sel.to(device), w.to(device), E)
+    act = torch.empty((T, I), dtype=torch.bfloat16, device=device)
+    part = torch.empty((T, H), dtype=torch.bfloat16, device=device)
+    for _ in range(20):   # a long read of slot 0 on the compute stream
+        ops.expert_ffn(cache, x.to(device), lay.w_sorted, lay.starts, lay.rows, lay.cols, [0],
+                       np.zeros(E, np.int32), H, I, act, part)
+    eng.mark_used([0], s)
+    eng.fetch([0], [1])          # overwrite slot 0 with expert 1: must wait for the reads
+    torch.cuda.synchronize()
+    eng.synchronize()
+    ref = execute_experts_ref([rows_w[0]], x, w, [torch.arange(T)], [torch.zeros(T, dtype=torch.long)], H, I)[0]
+    torch.testing.assert_close(part.cpu().float(), ref.float(), rtol=2e-2, atol=1e-2)
+    assert torch.equal(cache[0].cpu(), rows_w[1])
+    eng.close()
