@@ -1,0 +1,252 @@
+"""Benchmark of the per-GPU MoE hot path on one MI355X.
+
+Default workload (the headline metric): the Qwen3-30B-A3B-shaped MoE layer in decode --
+16 tokens per step, 128 experts top-8 (renormalised softmax), hidden 2048, SwiGLU
+intermediate 768, bf16, a 38-slot expert cache with the other experts in pinned host memory,
+router logits N(0, 1) + log Zipf(1.1) popularity (seed 1).  One step = one layer call:
+router kernel -> device history + D2H of the IDs -> host planner -> H2D fetch of the misses
+-> layout -> grouped SwiGLU (resident experts first) -> combine.
+
+Also reported on the same line:
+  * roofline: the decode expert FFN phase-1 kernel (ffn_up_skinny: gate/up projection +
+    SwiGLU, 2/3 of the expert bytes), achieved GB/s on its algorithmic bytes vs 8 TB/s,
+    from HIP events around each launch on the compute stream;
+  * prefill: the Qwen3-shaped 8192-token layer (experts resident), tokens/s and MFMA
+    utilisation of the grouped GEMMs vs 2.5 PFLOP/s;
+  * fetch: H2D GB/s of the expert copies and the fraction hidden behind compute;
+  * cpu_baseline: the oracle's torch-CPU restatement of the reference op order on the host
+    cores, on a bounded sample of the same decode stream.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from dataclasses import replace
+from pathlib import Path
+
+import numpy as np
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+PCIE_PEAK_GBS = 64.0
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument('--gpus', type=int, default=1)
+    p.add_argument('--steps', type=int, default=300)
+    p.add_argument('--warmup', type=int, default=30)
+    p.add_argument('--prefill-reps', type=int, default=20)
+    p.add_argument('--no-prefill', action='store_true')
+    p.add_argument('--no-cpu-baseline', action='store_true')
+    p.add_argument('--cpu-seconds', type=float, default=15.0)
+    return p.parse_args()
+
+
+def decode_stream(w, steps, device):
+    """Feasible steps of the seeded decode stream: (logits bf16 [T, E], x bf16 [T, H])."""
+    from ferry_amd import workloads
+    logits_gen = workloads.RouterLogits(w, device)
+    g = torch.Generator(device=device)
+    g.manual_seed(w.seed + 1000)
+    out = []
+    while len(out) < steps:
+        lg = logits_gen.next(0, w.tokens)
+        x = torch.randn((w.tokens, w.spec.hidden), generator=g, device=device).to(torch.bfloat16)
+        if workloads.feasible_topk_sets(lg.float().cpu().numpy(), w.spec.topk, w.cache_slots):
+            out.append((lg, x))
+    return out
+
+
+def run_decode(args, device):
+    from ferry_amd import expert_ops as ops
+    from ferry_amd import workloads
+    from ferry_amd.quota import Topology
+    from ferry_amd.runtime import OffloadRuntime
+    w = workloads.CONFIGS[2]
+    spec = w.spec
+    pool = workloads.make_pool(spec, 1, seed=0)
+    rt = OffloadRuntime(spec, pool, [w.cache_slots], 'ferry', Topology.uniform(1, spec.experts),
+                        timing=False)
+    stream = decode_stream(w, args.warmup + args.steps, device)
+
+    def step(lg, x):
+        wts, sel = ops.router_topk(lg, spec.topk, renorm=True)
+        return rt.execute(0, x, sel, wts, None)
+
+    for lg, x in stream[:args.warmup]:
+        step(lg, x)
+    torch.cuda.synchronize()
+    copies0 = rt.h2d.copies
+    rt.timing = True
+    ops.timing_enable(True)
+    t0 = time.perf_counter()
+    for lg, x in stream[args.warmup:]:
+        step(lg, x)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    rt.h2d.synchronize()
+    copies = rt.h2d.copies - copies0
+    ks = dict(rt.kernel_bytes)
+    ks['up_launches'], ks['up_ms'] = ops.timing_summary('ffn_up_skinny')
+    ks['down_launches'], ks['down_ms'] = ops.timing_summary('ffn_down_skinny')
+    ks['kernels'] = {name: ops.timing_summary(name) for name in
+                     ('router_kernel', 'history_kernel', 'layout_single', 'ffn_up_skinny',
+                      'ffn_down_skinny', 'combine_kernel')}
+    ops.timing_enable(False)
+    fetch_ms, exposed_ms = rt.fetch_timing()
+    elapsed = t1 - t0
+    tokens = w.tokens * args.steps
+    res = dict(workload=w, elapsed=elapsed, tokens=tokens, copies=copies, kernels=ks,
+               fetch_ms=fetch_ms, exposed_ms=exposed_ms, expert_bytes=spec.expert_bytes,
+               samples=stream[args.warmup:])
+    rt.close()
+    del pool
+    return res
+
+
+def run_prefill(args, device):
+    """One Qwen3-shaped prefill layer, 8192 tokens, all 128 experts resident in HBM."""
+    from ferry_amd import expert_ops as ops
+    from ferry_amd import workloads
+    w = workloads.CONFIGS[3]
+    spec = replace(w.spec, moe_layers=(0,))
+    E, k, H, I, T = spec.experts, spec.topk, spec.hidden, spec.intermediate, w.tokens
+    cache = workloads.expert_rows(range(E), spec.expert_elements, seed=0, device=device)
+    logits = workloads.RouterLogits(replace(w, layers=1), device).next(0, T)
+    x = workloads.hidden_states(T, H, seed=w.seed + 7, device=device)
+    act = torch.empty((T * k, I), dtype=torch.bfloat16, device=device)
+    part = torch.empty((T * k, H), dtype=torch.bfloat16, device=device)
+    slot_of = np.arange(E, dtype=np.int32)
+    stream = torch.cuda.current_stream()
+
+    def layer():
+        wts, sel = ops.router_topk(logits, k)
+        lay = ops.layout(sel, wts, E)
+        ops.expert_ffn(cache, x, lay.w_sorted, lay.starts, lay.rows, lay.cols, np.arange(E), slot_of,
+                       H, I, act, part, max_rows=T)
+        return ops.combine(part, T, k, H), sel
+
+    _, sel = layer()
+    torch.cuda.synchronize()
+    counts = np.bincount(sel.cpu().numpy().reshape(-1), minlength=E)
+    ops.timing_enable(True)
+    t0 = time.perf_counter()
+    for _ in range(args.prefill_reps):
+        layer()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    kern = {name: ops.timing_summary(name) for name in
+            ('router_kernel', 'layout_count', 'layout_scan', 'layout_scatter', 'ffn_up_skinny',
+             'ffn_tiled_up', 'ffn_down_skinny', 'ffn_tiled_down', 'combine_kernel')}
+    ops.timing_enable(False)
+    per = lambda name: kern[name][1] / max(1, args.prefill_reps)  # noqa: E731
+    up_ms = per('ffn_up_skinny') + per('ffn_tiled_up')
+    down_ms = per('ffn_down_skinny') + per('ffn_tiled_down')
+    flops = 2 * 3 * H * I * int(counts.sum())
+    gemm_ms = up_ms + down_ms
+    return dict(workload='qwen3_30b_a3b_moe_prefill_t8192_layer_resident', tokens=T,
+                tokens_per_s=T / ((t1 - t0) / args.prefill_reps),
+                gemm_ms=gemm_ms, up_ms=up_ms, down_ms=down_ms,
+                mfma_tflops=flops / (gemm_ms * 1e-3) / 1e12,
+                mfma_util=flops / (gemm_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+                active_experts=int((counts > 0).sum()), max_rows=int(counts.max()),
+                median_rows=float(np.median(counts[counts > 0])),
+                kernel_ms={name: per(name) for name in kern})
+
+
+def cpu_baseline(dec, seconds):
+    """The oracle's torch-CPU restatement of the reference op order on the decode stream."""
+    from oracle.experts import execute_experts_ref, reduce_partials_ref
+    from oracle.history import GateHistoryRef, frequency_rows
+    from oracle.layout import layout_closed_form
+    from oracle.policy import PlannerRef
+    from oracle.router import qwen3_router
+    from ferry_amd import workloads
+    w = dec['workload']
+    spec = w.spec
+    cores = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(cores)
+    E, k, H, I = spec.experts, spec.topk, spec.hidden, spec.intermediate
+    pool = workloads.make_pool(spec, 1, seed=0).cpu()   # same rows as the GPU pool
+    planner = PlannerRef(1, E, w.cache_slots)
+    hist = GateHistoryRef(1, E, 128)
+    samples = [(lg.cpu(), x.cpu()) for lg, x in dec['samples']]
+    steps = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        lg, x = samples[steps % len(samples)]
+        wts, sel, _ = qwen3_router(lg, k)
+        hist.update(0, frequency_rows(sel.numpy(), E, 128))
+        planner.plan(steps, 0, sel.numpy(), hist.scores(0))
+        lay = layout_closed_form(sel.numpy(), E, wts.float().numpy())
+        w_sorted = torch.from_numpy(lay['w_sorted']).to(torch.bfloat16)
+        groups = [e for e in range(E) if lay['counts'][e] > 0]
+        rows = [torch.from_numpy(lay['rows'][lay['starts'][e]:lay['starts'][e + 1]]) for e in groups]
+        cols = [torch.from_numpy(lay['cols'][lay['starts'][e]:lay['starts'][e + 1]]) for e in groups]
+        parts = execute_experts_ref([pool[e] for e in groups], x, w_sorted, rows, cols, H, I)
+        reduce_partials_ref(parts, rows, x.shape[0], H)
+        steps += 1
+    el = time.perf_counter() - t0
+    return dict(value=steps * w.tokens / el, unit='tokens/s', cores=cores, kind='port',
+                sample=f'{steps} decode steps ({steps * w.tokens} tokens) cycling over the same seeded stream, '
+                       f'{el:.1f} s; experts read from host memory (no H2D copy on the CPU path)')
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps(dict(error='this build runs one GPU per process; --gpus must be 1 '
+                                    '(multi-GPU expert parallelism is out of scope)')))
+        sys.exit(2)
+    torch.cuda.set_device(0)
+    device = torch.device('cuda', 0)
+    dec = run_decode(args, device)
+    w = dec['workload']
+    ks = dec['kernels']
+    up_gbs = ks['up'] / (ks['up_ms'] * 1e-3) / 1e9
+    down_gbs = ks['down'] / (ks['down_ms'] * 1e-3) / 1e9
+    ffn_gbs = (ks['up'] + ks['down']) / ((ks['up_ms'] + ks['down_ms']) * 1e-3) / 1e9
+    value = dec['tokens'] / dec['elapsed']
+    fetch_bytes = dec['copies'] * dec['expert_bytes']
+    h2d_gbs = fetch_bytes / (dec['fetch_ms'] * 1e-3) / 1e9 if dec['fetch_ms'] else None
+    hidden = 1.0 - dec['exposed_ms'] / dec['fetch_ms'] if dec['fetch_ms'] else None
+    compute_ms = ks['up_ms'] + ks['down_ms']
+    line = dict(
+        metric='MoE-layer tokens/sec (Qwen3-30B-A3B-shaped decode layer, 16 tok/step, 38/128 cached)',
+        value=value, unit='tokens/s', n_gpus=1, steps=args.steps, warmup=args.warmup,
+        ms_per_step=dec['elapsed'] / args.steps * 1e3, higher_is_better=True, scaling='weak',
+        vs_baseline=None, dtype='bf16', data='synthetic',
+        config=dict(workload=w.name, tokens_per_step=w.tokens, experts=w.spec.experts,
+                    topk=w.spec.topk, hidden=w.spec.hidden, intermediate=w.spec.intermediate,
+                    cache_slots=w.cache_slots, router='N(0,1)+log Zipf(1.1), seed 1',
+                    parallelism='single GPU (one expert-parallel share)'),
+        roofline=dict(kernel='ffn_up_skinny (decode gate/up + SwiGLU)', bound='hbm',
+                      achieved=up_gbs, peak=HBM_PEAK_GBS, unit='GB/s', frac=up_gbs / HBM_PEAK_GBS,
+                      traffic=None, launches=ks['up_launches'],
+                      avg_launch_us=ks['up_ms'] / max(1, ks['up_launches']) * 1e3,
+                      bytes_per_launch=ks['up'] / max(1, ks['up_launches'])),
+        decode=dict(ffn_down_gbs=down_gbs, ffn_gbs=ffn_gbs, ffn_frac=ffn_gbs / HBM_PEAK_GBS,
+                    ffn_ms_per_step=compute_ms / args.steps,
+                    active_experts_per_step=ks['experts'] / args.steps,
+                    misses_per_step=dec['copies'] / args.steps,
+                    h2d_gbs=h2d_gbs, h2d_frac=(h2d_gbs / PCIE_PEAK_GBS) if h2d_gbs else None,
+                    fetch_ms_per_step=dec['fetch_ms'] / args.steps,
+                    fetch_hidden_frac=hidden,
+                    kernel_us_per_step={n: v[1] / args.steps * 1e3 for n, v in ks['kernels'].items()},
+                    hidden_cap=min(1.0, compute_ms / dec['fetch_ms']) if dec['fetch_ms'] else None),
+    )
+    if not args.no_prefill:
+        line['prefill'] = run_prefill(args, device)
+    if not args.no_cpu_baseline:
+        line['cpu_baseline'] = cpu_baseline(dec, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == '__main__':
+    main()

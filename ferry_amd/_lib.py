@@ -26,7 +26,7 @@ SIGNATURES = [
      [_c_p, _c_p, _i64, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _i64, _c_p]),
     ('ferry_expert_ffn', ctypes.c_int,
      [_c_p, _i64, _i64, _i64, _c_p, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _i32, _c_p, _i64,
-      _i64, _c_p, _c_p, _i32, _c_p]),
+      _i64, _c_p, _c_p, _i32, _i32, _c_p]),
     ('ferry_combine', ctypes.c_int, [_c_p, _c_p, _i64, _i64, _i64, _c_p, _c_p]),
     ('ferry_history_update', ctypes.c_int,
      [_c_p, _i64, _i64, _i64, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p]),
@@ -43,6 +43,9 @@ SIGNATURES = [
     ('ferry_h2d_synchronize', ctypes.c_int, [_c_p]),
     ('ferry_h2d_copies', _i64, [_c_p]),
     ('ferry_h2d_stream', _c_p, [_c_p]),
+    ('ferry_timing_enable', ctypes.c_int, [_i32]),
+    ('ferry_timing_summary', ctypes.c_int,
+     [ctypes.c_char_p, ctypes.POINTER(_i64), ctypes.POINTER(ctypes.c_double)]),
 ]
 
 _lib = None

@@ -3,7 +3,10 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cstring>
+#include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/ferry_amd.h"
 
@@ -24,7 +27,62 @@ void set_error(const char* fmt, ...) {
 
 void clear_error() { g_last_error.clear(); }
 
+namespace {
+struct TimedLaunch {
+  const char* name;
+  hipEvent_t start, stop;
+};
+std::mutex g_timing_mu;
+bool g_timing = false;
+std::vector<TimedLaunch> g_launches;
+
+void release_launches() {
+  for (auto& l : g_launches) {
+    (void)hipEventDestroy(l.start);
+    (void)hipEventDestroy(l.stop);
+  }
+  g_launches.clear();
+}
+}  // namespace
+
+bool timing_enabled() { return g_timing; }
+
+void timing_events(const char* name, hipEvent_t* start, hipEvent_t* stop) {
+  std::lock_guard<std::mutex> lock(g_timing_mu);
+  if (hipEventCreate(start) != hipSuccess || hipEventCreate(stop) != hipSuccess) {
+    *start = *stop = nullptr;  // launch untimed
+    return;
+  }
+  g_launches.push_back(TimedLaunch{name, *start, *stop});
+}
+
 }  // namespace ferry
+
+// Turn per-launch kernel timing on (clearing earlier records) or off.
+extern "C" int ferry_timing_enable(int32_t enable) {
+  std::lock_guard<std::mutex> lock(ferry::g_timing_mu);
+  ferry::release_launches();
+  ferry::g_timing = enable != 0;
+  return 0;
+}
+
+// Number of timed launches of `kernel` and their summed duration in ms (waits for them).
+extern "C" int ferry_timing_summary(const char* kernel, int64_t* launches, double* total_ms) {
+  std::lock_guard<std::mutex> lock(ferry::g_timing_mu);
+  int64_t n = 0;
+  double ms = 0.0;
+  for (auto& l : ferry::g_launches) {
+    if (std::strcmp(l.name, kernel) != 0) continue;
+    if (hipEventSynchronize(l.stop) != hipSuccess) return 3;
+    float t = 0.f;
+    if (hipEventElapsedTime(&t, l.start, l.stop) != hipSuccess) return 3;
+    ms += t;
+    ++n;
+  }
+  *launches = n;
+  *total_ms = ms;
+  return 0;
+}
 
 extern "C" const char* ferry_last_error(void) { return ferry::g_last_error.c_str(); }
 

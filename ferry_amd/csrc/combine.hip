@@ -67,7 +67,7 @@ extern "C" int ferry_combine(const void* part, const int32_t* pair_pos, int64_t 
   const int64_t work = tokens * (hidden / kVec);
   int64_t grid = ceil_div(work, kThreads);
   if (grid > 65536) grid = 65536;
-  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)grid), dim3(kThreads), 0, (hipStream_t)stream,
+  launch("combine_kernel", combine_kernel, dim3((unsigned)grid), dim3(kThreads), 0, (hipStream_t)stream,
                      (const bf16_t*)part, pair_pos, tokens, (int)topk, hidden, (bf16_t*)out);
   FERRY_LAUNCHED("combine_kernel");
   return 0;

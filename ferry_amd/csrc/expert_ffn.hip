@@ -68,16 +68,20 @@ __device__ __forceinline__ bf16x8 load8(const bf16_t* p) {
 // Skinny kernels
 // =============================================================================================
 
-// Phase 1, skinny: one workgroup = (expert, 16*NT intermediate columns), K split KS ways.
-template <int NT>
+// Phase 1, skinny: one workgroup = (expert, 16*NT intermediate columns), K split KS = 4/NT
+// ways over its wavefronts.  MT = number of 16-row M tiles (rows of the expert, <= 16*MT).
+// Each lane streams 16-byte weight fragments straight into MFMA B-operand registers; UNR
+// K steps of loads are issued before their MFMAs so ~UNR*32 bytes per lane are in flight.
+template <int NT, int MT>
 __global__ __launch_bounds__(256) void ffn_up_skinny(FfnArgs a) {
   constexpr int KS = 4 / NT;
+  constexpr int UNR = 8;
   const int li = blockIdx.y;
   if (li >= a.list.n) return;
   const int e = a.list.expert[li];
   const int64_t start = a.starts[e];
   const int n = (int)(a.starts[e + 1] - start);
-  if (n == 0 || n > kSkinnyMax) return;
+  if (n == 0 || n > 16 * MT) return;
   const int H = (int)a.H;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nt = wave % NT, ks = wave / NT;
@@ -87,19 +91,18 @@ __global__ __launch_bounds__(256) void ffn_up_skinny(FfnArgs a) {
   const int r16 = lane & 15, kg = (lane >> 4) * 8;
   const bf16_t* pg = wg + (int64_t)(i0 + r16) * H + kg;
   const bf16_t* pu = wu + (int64_t)(i0 + r16) * H + kg;
-  const int MT = (n + 15) / 16;
-  const bf16_t* px[4];
-  bool okx[4];
+  const bf16_t* px[MT];
+  bool okx[MT];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
+  for (int mt = 0; mt < MT; ++mt) {
     const int r = mt * 16 + r16;
     okx[mt] = r < n;
     const int64_t t = okx[mt] ? a.rows[start + r] : 0;
     px[mt] = a.x + t * a.H + kg;
   }
-  floatx4 accg[4], accu[4];
+  floatx4 accg[MT], accu[MT];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
+  for (int mt = 0; mt < MT; ++mt) {
     accg[mt] = floatx4{0, 0, 0, 0};
     accu[mt] = floatx4{0, 0, 0, 0};
   }
@@ -107,52 +110,49 @@ __global__ __launch_bounds__(256) void ffn_up_skinny(FfnArgs a) {
   const int kbeg = ks * kspan, kend = kbeg + kspan;
   const bf16x8 zero8 = {};
   int k0 = kbeg;
-  for (; k0 + 4 * 32 <= kend; k0 += 4 * 32) {
-    bf16x8 bg[4], bu[4];
+  for (; k0 + UNR * 32 <= kend; k0 += UNR * 32) {
+    bf16x8 bg[UNR], bu[UNR], ax[MT][UNR];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < UNR; ++s) {
       bg[s] = load8(pg + k0 + s * 32);
       bu[s] = load8(pu + k0 + s * 32);
     }
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      if (mt < MT) {
-        bf16x8 ax[4];
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int s = 0; s < 4; ++s) ax[s] = okx[mt] ? load8(px[mt] + k0 + s * 32) : zero8;
+      for (int s = 0; s < UNR; ++s) ax[mt][s] = okx[mt] ? load8(px[mt] + k0 + s * 32) : zero8;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          accg[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax[s], bg[s], accg[mt], 0, 0, 0);
-          accu[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax[s], bu[s], accu[mt], 0, 0, 0);
-        }
+    for (int s = 0; s < UNR; ++s)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        accg[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax[mt][s], bg[s], accg[mt], 0, 0, 0);
+        accu[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax[mt][s], bu[s], accu[mt], 0, 0, 0);
       }
-    }
   }
   for (; k0 < kend; k0 += 32) {
     const bf16x8 bg = load8(pg + k0), bu = load8(pu + k0);
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      if (mt < MT) {
-        const bf16x8 ax = okx[mt] ? load8(px[mt] + k0) : zero8;
-        accg[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, bg, accg[mt], 0, 0, 0);
-        accu[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, bu, accu[mt], 0, 0, 0);
-      }
+    for (int mt = 0; mt < MT; ++mt) {
+      const bf16x8 ax = okx[mt] ? load8(px[mt] + k0) : zero8;
+      accg[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, bg, accg[mt], 0, 0, 0);
+      accu[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, bu, accu[mt], 0, 0, 0);
     }
   }
   // cross-wavefront K reduction, fixed order ks = 0..KS-1
-  __shared__ floatx4 red[KS > 1 ? KS : 1][NT][4][2][64];
-  if (KS > 1) {
+  if constexpr (KS > 1) {
+    __shared__ floatx4 red[KS][NT][MT][2][64];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+    for (int mt = 0; mt < MT; ++mt) {
       red[ks][nt][mt][0][lane] = accg[mt];
       red[ks][nt][mt][1][lane] = accu[mt];
     }
     __syncthreads();
     if (ks != 0) return;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+    for (int mt = 0; mt < MT; ++mt) {
       accg[mt] = red[0][nt][mt][0][lane];
       accu[mt] = red[0][nt][mt][1][lane];
+#pragma unroll
       for (int q = 1; q < KS; ++q) {
         accg[mt] += red[q][nt][mt][0][lane];
         accu[mt] += red[q][nt][mt][1][lane];
@@ -162,30 +162,29 @@ __global__ __launch_bounds__(256) void ffn_up_skinny(FfnArgs a) {
   // 16x16 accumulator layout: column = lane & 15, rows (lane >> 4) * 4 + [0, 4)
   const int col = i0 + (lane & 15);
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    if (mt < MT) {
+  for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r = mt * 16 + (lane >> 4) * 4 + q;
-        if (r < n) {
-          const float g = bf16r(accg[mt][q]), u = bf16r(accu[mt][q]);
-          a.act[(start + r) * a.I + col] = f32_to_bf16(silu_mul(g, u));
-        }
+    for (int q = 0; q < 4; ++q) {
+      const int r = mt * 16 + (lane >> 4) * 4 + q;
+      if (r < n) {
+        const float g = bf16r(accg[mt][q]), u = bf16r(accu[mt][q]);
+        a.act[(start + r) * a.I + col] = f32_to_bf16(silu_mul(g, u));
       }
     }
   }
 }
 
-// Phase 2, skinny: one workgroup = (expert, 16*NT hidden rows), K = I split KS ways.
-template <int NT>
+// Phase 2, skinny: one workgroup = (expert, 16*NT hidden rows), K = I split KS = 4/NT ways.
+template <int NT, int MT>
 __global__ __launch_bounds__(256) void ffn_down_skinny(FfnArgs a) {
   constexpr int KS = 4 / NT;
+  constexpr int UNR = 8;
   const int li = blockIdx.y;
   if (li >= a.list.n) return;
   const int e = a.list.expert[li];
   const int64_t start = a.starts[e];
   const int n = (int)(a.starts[e + 1] - start);
-  if (n == 0 || n > kSkinnyMax) return;
+  if (n == 0 || n > 16 * MT) return;
   const int I = (int)a.I;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nt = wave % NT, ks = wave / NT;
@@ -193,75 +192,69 @@ __global__ __launch_bounds__(256) void ffn_down_skinny(FfnArgs a) {
   const bf16_t* wd = a.cache + (int64_t)a.list.slot[li] * 3 * a.H * a.I + 2 * a.H * a.I;
   const int r16 = lane & 15, kg = (lane >> 4) * 8;
   const bf16_t* pd = wd + (int64_t)(h0 + r16) * I + kg;
-  const int MT = (n + 15) / 16;
-  const bf16_t* pa[4];
-  bool oka[4];
+  const bf16_t* pa[MT];
+  bool oka[MT];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
+  for (int mt = 0; mt < MT; ++mt) {
     const int r = mt * 16 + r16;
     oka[mt] = r < n;
     pa[mt] = a.act + (start + (oka[mt] ? r : 0)) * a.I + kg;
   }
-  floatx4 acc[4];
+  floatx4 acc[MT];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) acc[mt] = floatx4{0, 0, 0, 0};
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = floatx4{0, 0, 0, 0};
   const int kspan = I / KS;
   const int kbeg = ks * kspan, kend = kbeg + kspan;
   const bf16x8 zero8 = {};
   int k0 = kbeg;
-  for (; k0 + 4 * 32 <= kend; k0 += 4 * 32) {
-    bf16x8 b[4];
+  for (; k0 + UNR * 32 <= kend; k0 += UNR * 32) {
+    bf16x8 b[UNR], ax[MT][UNR];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) b[s] = load8(pd + k0 + s * 32);
+    for (int s = 0; s < UNR; ++s) b[s] = load8(pd + k0 + s * 32);
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      if (mt < MT) {
-        bf16x8 ax[4];
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int s = 0; s < 4; ++s) ax[s] = oka[mt] ? load8(pa[mt] + k0 + s * 32) : zero8;
+      for (int s = 0; s < UNR; ++s) ax[mt][s] = oka[mt] ? load8(pa[mt] + k0 + s * 32) : zero8;
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-          acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax[s], b[s], acc[mt], 0, 0, 0);
-      }
-    }
+    for (int s = 0; s < UNR; ++s)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax[mt][s], b[s], acc[mt], 0, 0, 0);
   }
   for (; k0 < kend; k0 += 32) {
     const bf16x8 b = load8(pd + k0);
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      if (mt < MT) {
-        const bf16x8 ax = oka[mt] ? load8(pa[mt] + k0) : zero8;
-        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, b, acc[mt], 0, 0, 0);
-      }
+    for (int mt = 0; mt < MT; ++mt) {
+      const bf16x8 ax = oka[mt] ? load8(pa[mt] + k0) : zero8;
+      acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, b, acc[mt], 0, 0, 0);
     }
   }
-  __shared__ floatx4 red[KS > 1 ? KS : 1][NT][4][64];
-  if (KS > 1) {
+  if constexpr (KS > 1) {
+    __shared__ floatx4 red[KS][NT][MT][64];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) red[ks][nt][mt][lane] = acc[mt];
+    for (int mt = 0; mt < MT; ++mt) red[ks][nt][mt][lane] = acc[mt];
     __syncthreads();
     if (ks != 0) return;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+    for (int mt = 0; mt < MT; ++mt) {
       acc[mt] = red[0][nt][mt][lane];
+#pragma unroll
       for (int q = 1; q < KS; ++q) acc[mt] += red[q][nt][mt][lane];
     }
   }
   const int h = h0 + (lane & 15);
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    if (mt < MT) {
+  for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int r = mt * 16 + (lane >> 4) * 4 + q;
-        if (r < n) {
-          const int64_t p = start + r;
-          const int64_t t = a.rows[p], j = a.cols[p];
-          const float wt = bf16_to_f32(a.w[t * a.k + j]);
-          const float y = bf16r(acc[mt][q]);
-          const int64_t orow = a.out_mode == 0 ? t * a.k + j : p;
-          a.out[orow * a.H + h] = f32_to_bf16(y * wt);
-        }
+    for (int q = 0; q < 4; ++q) {
+      const int r = mt * 16 + (lane >> 4) * 4 + q;
+      if (r < n) {
+        const int64_t p = start + r;
+        const int64_t t = a.rows[p], j = a.cols[p];
+        const float wt = bf16_to_f32(a.w[t * a.k + j]);
+        const float y = bf16r(acc[mt][q]);
+        const int64_t orow = a.out_mode == 0 ? t * a.k + j : p;
+        a.out[orow * a.H + h] = f32_to_bf16(y * wt);
       }
     }
   }
@@ -271,7 +264,12 @@ __global__ __launch_bounds__(256) void ffn_down_skinny(FfnArgs a) {
 // Tiled kernels
 // =============================================================================================
 
-constexpr int BM = 128, BN = 128, BK = 64, LDK = BK + 8;  // +8 bf16 of padding per row
+// Output tile 256 x 256 per workgroup, K step 64, four wavefronts of 128 x 128 (2 x 2), each a
+// 4 x 4 grid of 32x32 MFMA accumulators (256 fp32 per lane, held in AGPRs).  Phase 1's 256 B rows
+// are 128 gate rows and the 128 up rows of the same intermediate columns, so every wavefront
+// owns matching gate/up accumulators and the SwiGLU runs in registers.
+constexpr int BM = 256, BN = 256, BK = 64, LDK = BK + 8;  // +8 bf16 of padding per LDS row
+constexpr int kTileLds = 2 * (BM + BN) * LDK;               // bf16 elements (double buffer)
 
 struct TileTable {
   int32_t cum[kListMax + 1];  // cumulative M tiles over list entries
@@ -329,22 +327,29 @@ __device__ __forceinline__ int find_entry(const TileTable& tt, int m) {
   return lo;
 }
 
-// MODE 0: A = gathered x rows (K = H), B rows 0..63 = Wg[i0..], 64..127 = Wu[i0..], out act.
-// MODE 1: A = act rows (K = I), B rows = Wd[h0..], out weighted rows.
+// MODE 0: A = gathered x rows (K = H); B rows 0..127 = Wg[i0 ..], 128..255 = Wu[i0 ..];
+//         epilogue act[p, i0 + c] = bf16(silu(bf16(g)) * bf16(u)).
+// MODE 1: A = activation rows (K = I); B rows = Wd[h0 ..];
+//         epilogue out[row(p), h0 + c] = bf16(bf16(y) * w(p)).
 template <int MODE>
-__global__ __launch_bounds__(256) void ffn_tiled(FfnArgs a) {
+__global__ __launch_bounds__(256, 1) void ffn_tiled(FfnArgs a) {
   __shared__ TileTable tt;
-  __shared__ __attribute__((aligned(16))) bf16_t As[2][BM * LDK];
-  __shared__ __attribute__((aligned(16))) bf16_t Bs[2][BN * LDK];
+  __shared__ __attribute__((aligned(16))) bf16_t smem[kTileLds];
+  __shared__ int64_t orow_s[BM];
+  __shared__ float wt_s[BM];
   build_tile_table(a, tt);
   const int64_t K = MODE == 0 ? a.H : a.I;
-  const int ntn = MODE == 0 ? (int)(a.I / 64) : (int)(a.H / BN);
+  const int ntn = MODE == 0 ? (int)(a.I / 128) : (int)(a.H / BN);
   const int total = tt.total * ntn;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int KT = (int)(K / BK);
+  const int l32 = lane & 31, kh = (lane >> 5) * 8;
+  bf16_t* As = smem;                 // [2][BM][LDK]
+  bf16_t* Bs = smem + 2 * BM * LDK;  // [2][BN][LDK]
 
   for (int tile = blockIdx.x; tile < total; tile += gridDim.x) {
+    // tiles of one expert are consecutive, N fastest: consecutive workgroups share A rows
     const int mt_global = tile / ntn, ntile = tile % ntn;
     const int li = find_entry(tt, mt_global);
     const int e = a.list.expert[li];
@@ -353,64 +358,86 @@ __global__ __launch_bounds__(256) void ffn_tiled(FfnArgs a) {
     const int m0 = (mt_global - tt.cum[li]) * BM;
     const bf16_t* slot = a.cache + (int64_t)a.list.slot[li] * 3 * a.H * a.I;
 
-    // per-thread global load descriptors: 4 chunks of 16 B for A and for B
-    const bf16_t* ga[4];
-    const bf16_t* gb[4];
-    bool oka[4];
-    int lrow[4], lkc[4];
+    // global load descriptors: thread owns 16-byte chunk kc of rows tid/8 + 32*q, q < 8.
+    // A rows are element offsets (32-bit) from a.x / a.act, B rows are affine in q.
+    const int lrow = tid >> 3, lkc = (tid & 7) * 8;
+    uint32_t aoff[8];
+    uint32_t amask = 0;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int c = tid + 256 * q;
-      const int row = c >> 3, kc = (c & 7) * 8;
-      lrow[q] = row;
-      lkc[q] = kc;
-      const int r = m0 + row;
-      oka[q] = r < n;
+    for (int q = 0; q < 8; ++q) {
+      const int r = m0 + lrow + 32 * q;
+      const bool ok = r < n;
+      amask |= ok ? (1u << q) : 0u;
       if (MODE == 0) {
-        const int64_t t = oka[q] ? a.rows[start + r] : 0;
-        ga[q] = a.x + t * a.H + kc;
-        const int i0 = ntile * 64;
-        const bf16_t* wrow = row < 64 ? slot + (int64_t)(i0 + row) * a.H
-                                      : slot + a.H * a.I + (int64_t)(i0 + row - 64) * a.H;
-        gb[q] = wrow + kc;
+        const int64_t t = ok ? a.rows[start + r] : 0;
+        aoff[q] = (uint32_t)(t * a.H + lkc);
       } else {
-        ga[q] = a.act + (start + (oka[q] ? r : 0)) * a.I + kc;
-        const int h0 = ntile * BN;
-        gb[q] = slot + 2 * a.H * a.I + (int64_t)(h0 + row) * a.I + kc;
+        aoff[q] = (uint32_t)((start + (ok ? r : 0)) * a.I + lkc);
       }
     }
-    u32x4 ra[4], rb[4];
+    const bf16_t* abase = MODE == 0 ? a.x : a.act;
+    const int64_t ldb = MODE == 0 ? a.H : a.I;
+    // MODE 0: rows lrow + 32q, q < 4 gate, q >= 4 the matching up rows (offset H*I - 128 rows)
+    const bf16_t* gb = MODE == 0 ? slot + (int64_t)(ntile * 128 + lrow) * a.H + lkc
+                                 : slot + 2 * a.H * a.I + (int64_t)(ntile * BN + lrow) * a.I + lkc;
+    const int64_t bstep = 32 * ldb;                                   // next 32 rows
+    const int64_t bjump = MODE == 0 ? a.H * a.I - 4 * bstep : 0;       // gate -> up block
+    if (MODE == 1) {
+      // per-row output row and routing weight for the epilogue
+      for (int r = tid; r < BM; r += 256) {
+        const int rr = m0 + r;
+        int64_t orow = 0;
+        float wt = 0.f;
+        if (rr < n) {
+          const int64_t p = start + rr;
+          const int64_t t = a.rows[p], j = a.cols[p];
+          wt = bf16_to_f32(a.w[t * a.k + j]);
+          orow = a.out_mode == 0 ? t * a.k + j : p;
+        }
+        orow_s[r] = orow;
+        wt_s[r] = wt;
+      }
+    }
+
+    u32x4 ra[8], rb[8];
     const u32x4 z4 = {0, 0, 0, 0};
     auto gload = [&](int kt) {
-      const int64_t koff = (int64_t)kt * BK;
+      const int koff = kt * BK;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        ra[q] = oka[q] ? *reinterpret_cast<const u32x4*>(ga[q] + koff) : z4;
-        rb[q] = *reinterpret_cast<const u32x4*>(gb[q] + koff);
+      for (int q = 0; q < 8; ++q)
+        ra[q] = (amask >> q) & 1u ? *reinterpret_cast<const u32x4*>(abase + aoff[q] + koff) : z4;
+      const bf16_t* b = gb + koff;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        rb[q] = *reinterpret_cast<const u32x4*>(b);
+        b += (q == 3) ? bstep + bjump : bstep;
       }
     };
     auto lstore = [&](int buf) {
+      bf16_t* as = As + buf * BM * LDK;
+      bf16_t* bs = Bs + buf * BN * LDK;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        *reinterpret_cast<u32x4*>(&As[buf][lrow[q] * LDK + lkc[q]]) = ra[q];
-        *reinterpret_cast<u32x4*>(&Bs[buf][lrow[q] * LDK + lkc[q]]) = rb[q];
+      for (int q = 0; q < 8; ++q) {
+        *reinterpret_cast<u32x4*>(&as[(lrow + 32 * q) * LDK + lkc]) = ra[q];
+        *reinterpret_cast<u32x4*>(&bs[(lrow + 32 * q) * LDK + lkc]) = rb[q];
       }
     };
 
-    floatx16 acc[2][2];
+    floatx16 acc[4][4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-    // B sub-tile rows of this wavefront: MODE 0 -> gate rows wn*32.., up rows 64 + wn*32..;
-    // MODE 1 -> rows wn*64 + [0, 64).
-    const int brow0 = MODE == 0 ? wn * 32 : wn * 64;
-    const int brow1 = MODE == 0 ? 64 + wn * 32 : wn * 64 + 32;
-    const int arow0 = wm * 64;
-    const int l32 = lane & 31, kh = (lane >> 5) * 8;
+    // B sub-tiles of this wavefront.  MODE 0: j = 0, 1 gate rows wn*64 + 32j; j = 2, 3 the
+    // matching up rows 128 + wn*64 + 32(j-2).  MODE 1: rows wn*128 + 32j.
+    int brow[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      brow[j] = MODE == 0 ? (j < 2 ? wn * 64 + 32 * j : 128 + wn * 64 + 32 * (j - 2))
+                          : wn * 128 + 32 * j;
 
     gload(0);
     lstore(0);
@@ -418,49 +445,64 @@ __global__ __launch_bounds__(256) void ffn_tiled(FfnArgs a) {
     for (int kt = 0; kt < KT; ++kt) {
       const int buf = kt & 1;
       if (kt + 1 < KT) gload(kt + 1);
+      const bf16_t* as = As + buf * BM * LDK;
+      const bf16_t* bs = Bs + buf * BN * LDK;
 #pragma unroll
       for (int kk = 0; kk < BK; kk += 16) {
-        bf16x8 af[2], bf[2];
+        bf16x8 af[4], bfr[4];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-          af[i] = *reinterpret_cast<const bf16x8*>(&As[buf][(arow0 + i * 32 + l32) * LDK + kk + kh]);
-        bf[0] = *reinterpret_cast<const bf16x8*>(&Bs[buf][(brow0 + l32) * LDK + kk + kh]);
-        bf[1] = *reinterpret_cast<const bf16x8*>(&Bs[buf][(brow1 + l32) * LDK + kk + kh]);
+        for (int i = 0; i < 4; ++i)
+          af[i] = *reinterpret_cast<const bf16x8*>(&as[(wm * 128 + i * 32 + l32) * LDK + kk + kh]);
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int j = 0; j < 4; ++j)
+          bfr[j] = *reinterpret_cast<const bf16x8*>(&bs[(brow[j] + l32) * LDK + kk + kh]);
 #pragma unroll
-          for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
       }
       if (kt + 1 < KT) lstore(buf ^ 1);
       __syncthreads();
     }
 
-    // epilogue; 32x32 accumulator layout: column = lane & 31,
-    // row(v) = (v / 4) * 8 + (lane / 32) * 4 + v % 4
+    // epilogue: bf16 tile staged in LDS, then 16-byte row stores.
+    // 32x32 accumulator layout: column = lane & 31, row(v) = (v/4)*8 + (lane/32)*4 + v%4
+    constexpr int OC = MODE == 0 ? 128 : 256;  // output columns of the tile
+    constexpr int OLD = OC + 8;
+    bf16_t* os = smem;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < 4; ++i) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int r = m0 + arow0 + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-        if (r >= n) continue;
-        const int64_t p = start + r;
+        const int r = wm * 128 + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
         if (MODE == 0) {
-          const int icol = ntile * 64 + wn * 32 + l32;
-          const float g = bf16r(acc[i][0][v]), u = bf16r(acc[i][1][v]);
-          a.act[p * a.I + icol] = f32_to_bf16(silu_mul(g, u));
-        } else {
-          const int64_t t = a.rows[p], j = a.cols[p];
-          const float wt = bf16_to_f32(a.w[t * a.k + j]);
-          const int64_t orow = a.out_mode == 0 ? t * a.k + j : p;
 #pragma unroll
-          for (int jj = 0; jj < 2; ++jj) {
-            const int h = ntile * BN + wn * 64 + jj * 32 + l32;
-            a.out[orow * a.H + h] = f32_to_bf16(bf16r(acc[i][jj][v]) * wt);
+          for (int jg = 0; jg < 2; ++jg) {
+            const float g = bf16r(acc[i][jg][v]), u = bf16r(acc[i][jg + 2][v]);
+            os[r * OLD + wn * 64 + jg * 32 + l32] = f32_to_bf16(silu_mul(g, u));
           }
+        } else {
+          const float wt = wt_s[r];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            os[r * OLD + wn * 128 + j * 32 + l32] = f32_to_bf16(bf16r(acc[i][j][v]) * wt);
         }
       }
     }
+    __syncthreads();
+    constexpr int CPR = OC / 8;  // 16-byte chunks per row
+    for (int c = tid; c < BM * CPR; c += 256) {
+      const int r = c / CPR, cc = (c % CPR) * 8;
+      if (m0 + r >= n) continue;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(&os[r * OLD + cc]);
+      if (MODE == 0) {
+        *reinterpret_cast<u32x4*>(&a.act[(start + m0 + r) * a.I + ntile * 128 + cc]) = v;
+      } else {
+        *reinterpret_cast<u32x4*>(&a.out[orow_s[r] * a.H + ntile * BN + cc]) = v;
+      }
+    }
+    __syncthreads();
   }
 }
 
@@ -477,8 +519,9 @@ extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t h
                                 const int64_t* cols, const int32_t* expert_list, int32_t n_list,
                                 const int32_t* slot_of, int64_t experts,
                                 int64_t max_rows_per_expert, void* act, void* out,
-                                int32_t out_mode, void* stream) {
+                                int32_t out_mode, int32_t phases, void* stream) {
   clear_error();
+  FERRY_CHECK_ARG(phases >= 1 && phases <= 3, "phases must be 1 (up), 2 (down) or 3 (both)");
   FERRY_CHECK_ARG(hidden > 0 && hidden % 128 == 0, "hidden must be a positive multiple of 128");
   FERRY_CHECK_ARG(inter > 0 && inter % 128 == 0, "intermediate must be a positive multiple of 128");
   FERRY_CHECK_ARG(topk >= 1 && rows_in >= 0 && n_list >= 0 && max_rows_per_expert >= 0,
@@ -487,6 +530,10 @@ extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t h
                   FERRY_MAX_EXPERTS);
   FERRY_CHECK_ARG(out_mode == 0 || out_mode == 1, "out_mode must be 0 or 1");
   FERRY_CHECK_ARG(rows_in * topk < (int64_t)1 << 31, "rows*topk must be < 2^31");
+  // the tiled kernels address A rows with 32-bit element offsets
+  FERRY_CHECK_ARG(rows_in * hidden < ((int64_t)1 << 32) &&
+                      rows_in * topk * inter < ((int64_t)1 << 32),
+                  "x / act must hold fewer than 2^32 elements");
   if (n_list == 0 || rows_in == 0) return 0;
   FERRY_CHECK_ARG(cache && x && w_sorted && starts && rows && cols && expert_list && slot_of &&
                       act && out,
@@ -528,27 +575,41 @@ extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t h
       args.list.expert[i] = (int16_t)(i < cnt ? expert_list[off + i] : 0);
       args.list.slot[i] = i < cnt ? slot_of[expert_list[off + i]] : 0;
     }
-    // skinny part (experts with 1..64 rows)
-    hipLaunchKernelGGL(ffn_up_skinny<1>, dim3((unsigned)(inter / 16), cnt), dim3(256), 0, s, args);
-    FERRY_LAUNCHED("ffn_up_skinny");
     const bool any_big = maxn > kSkinnyMax;
-    int64_t tile_bound = 0;
-    if (any_big) {
-      // M tiles over experts with > 64 rows: sum ceil(n/128) <= pairs/128 + pairs/65
-      tile_bound = pairs / BM + pairs / (kSkinnyMax + 1) + 1;
-      int64_t t1 = tile_bound * (inter / 64);
-      int64_t grid = t1 < (int64_t)g_num_cus * 2 ? t1 : (int64_t)g_num_cus * 2;
-      hipLaunchKernelGGL(ffn_tiled<0>, dim3((unsigned)grid), dim3(256), 0, s, args);
-      FERRY_LAUNCHED("ffn_tiled<up>");
+    // M tiles over experts with > 64 rows: sum ceil(n/128) <= pairs/128 + pairs/65
+    const int64_t tile_bound = pairs / BM + pairs / (kSkinnyMax + 1) + 1;  // >= sum ceil(n/BM)
+    const int64_t grid_cap = (int64_t)g_num_cus;  // one 256x256 workgroup per CU
+    if (phases & 1) {
+      const dim3 g1((unsigned)(inter / 16), cnt);
+      if (maxn <= 16)
+        launch("ffn_up_skinny", ffn_up_skinny<1, 1>, g1, dim3(256), 0, s, args);
+      else if (maxn <= 32)
+        launch("ffn_up_skinny", ffn_up_skinny<1, 2>, g1, dim3(256), 0, s, args);
+      else
+        launch("ffn_up_skinny", ffn_up_skinny<1, 4>, g1, dim3(256), 0, s, args);
+      FERRY_LAUNCHED("ffn_up_skinny");
+      if (any_big) {
+        const int64_t t1 = tile_bound * (inter / 128);
+        launch("ffn_tiled_up", ffn_tiled<0>, dim3((unsigned)(t1 < grid_cap ? t1 : grid_cap)),
+                           dim3(256), 0, s, args);
+        FERRY_LAUNCHED("ffn_tiled<up>");
+      }
     }
-    hipLaunchKernelGGL(ffn_down_skinny<4>, dim3((unsigned)(hidden / 64), cnt), dim3(256), 0, s,
-                       args);
-    FERRY_LAUNCHED("ffn_down_skinny");
-    if (any_big) {
-      int64_t t2 = tile_bound * (hidden / BN);
-      int64_t grid = t2 < (int64_t)g_num_cus * 2 ? t2 : (int64_t)g_num_cus * 2;
-      hipLaunchKernelGGL(ffn_tiled<1>, dim3((unsigned)grid), dim3(256), 0, s, args);
-      FERRY_LAUNCHED("ffn_tiled<down>");
+    if (phases & 2) {
+      const dim3 g2((unsigned)(hidden / 64), cnt);
+      if (maxn <= 16)
+        launch("ffn_down_skinny", ffn_down_skinny<4, 1>, g2, dim3(256), 0, s, args);
+      else if (maxn <= 32)
+        launch("ffn_down_skinny", ffn_down_skinny<4, 2>, g2, dim3(256), 0, s, args);
+      else
+        launch("ffn_down_skinny", ffn_down_skinny<4, 4>, g2, dim3(256), 0, s, args);
+      FERRY_LAUNCHED("ffn_down_skinny");
+      if (any_big) {
+        const int64_t t2 = tile_bound * (hidden / BN);
+        launch("ffn_tiled_down", ffn_tiled<1>, dim3((unsigned)(t2 < grid_cap ? t2 : grid_cap)),
+                           dim3(256), 0, s, args);
+        FERRY_LAUNCHED("ffn_tiled<down>");
+      }
     }
   }
   return 0;

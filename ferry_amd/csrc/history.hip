@@ -93,7 +93,7 @@ extern "C" int ferry_history_update(const int64_t* selected, int64_t tokens, int
   const int64_t nids = ids_out ? tokens * topk : 0;
   const int64_t grid = 1 + ceil_div(nids, kIdsPerBlock);
   FERRY_CHECK_ARG(grid < (1 << 30), "too many tokens");
-  hipLaunchKernelGGL(history_kernel, dim3((unsigned)grid), dim3(kThreads), 0, (hipStream_t)stream,
+  launch("history_kernel", history_kernel, dim3((unsigned)grid), dim3(kThreads), 0, (hipStream_t)stream,
                      selected, tokens, (int)topk, (int)experts, (int)window, layer, ring, counts,
                      meta, scores_out, ids_out);
   FERRY_LAUNCHED("history_kernel");

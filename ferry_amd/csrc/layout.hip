@@ -244,18 +244,18 @@ extern "C" int ferry_layout(const int64_t* selected, const void* weights_bf16, i
   const bf16_t* w = (const bf16_t*)weights_bf16;
   bf16_t* ws = (bf16_t*)w_sorted_bf16;
   if (tokens <= kBlockTokens) {
-    hipLaunchKernelGGL(layout_single, dim3(1), dim3(kBlockTokens), 0, s, selected, w, tokens, k,
+    launch("layout_single", layout_single, dim3(1), dim3(kBlockTokens), 0, s, selected, w, tokens, k,
                        E, send_ids, ws, starts, rows, cols, pair_pos, err);
     FERRY_LAUNCHED("layout_single");
     return 0;
   }
   const int nblk = (int)ceil_div(tokens, kBlockTokens);
-  hipLaunchKernelGGL(layout_count, dim3(nblk), dim3(kBlockTokens), 0, s, selected, tokens, k, E,
+  launch("layout_count", layout_count, dim3(nblk), dim3(kBlockTokens), 0, s, selected, tokens, k, E,
                      hist);
   FERRY_LAUNCHED("layout_count");
-  hipLaunchKernelGGL(layout_scan, dim3(1), dim3(kMaxE), 0, s, hist, nblk, E, starts, err);
+  launch("layout_scan", layout_scan, dim3(1), dim3(kMaxE), 0, s, hist, nblk, E, starts, err);
   FERRY_LAUNCHED("layout_scan");
-  hipLaunchKernelGGL(layout_scatter, dim3(nblk), dim3(kBlockTokens), 0, s, selected, w, tokens, k,
+  launch("layout_scatter", layout_scatter, dim3(nblk), dim3(kBlockTokens), 0, s, selected, w, tokens, k,
                      E, hist, starts, send_ids, ws, rows, cols, pair_pos, err);
   FERRY_LAUNCHED("layout_scatter");
   return 0;

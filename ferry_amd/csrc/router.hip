@@ -3,37 +3,53 @@
 // Reference: ferry/model.py:141-146 (Qwen3 hook) and the greedy DeepSeek-V2 gate feeding
 // ferry/model.py:151-157.  torch.topk there selects on the fp32 probabilities with torch's
 // CPU algorithm (std::nth_element + std::sort of the first k-1 entries when k*64 > E, else
-// std::partial_sort; comparator on values only).  Softmax is strictly increasing in the
-// logit, so the order relation -- ties included -- is that of the logits whenever the
-// probabilities compared are normal fp32 numbers; this kernel therefore selects on the
-// logits themselves, which makes the tie pattern independent of the exp implementation.
+// std::partial_sort; comparator on values only, NaN first).  Softmax is strictly increasing
+// in the logit, so the comparison outcomes -- ties included -- are those of the logits while
+// the probabilities compared are normal fp32 numbers; a row holding a NaN or +inf logit has
+// all-NaN probabilities, i.e. all elements compare equal.  Selection therefore runs on
+// order-preserving uint32 keys of the logits (all equal for such rows), which makes the tie
+// pattern independent of the exp implementation.
 //
-// Fast path (sorted output, all top-k values distinct, k-th > (k+1)-th): the selection is
-// unique and comes out in descending order; it is found with k wavefront arg-max
-// reductions.  Every other row (ties, NaN, or unsorted output, whose order depends on the
-// partition steps) is resolved by lane 0 running the same selection algorithm as the CPU
-// (median-of-3 introselect with insertion sort below 4 elements, heap select after the
-// depth limit, introsort for the final sort) on the row staged in LDS.
+// Fast path (sorted output, nth_element regime, all top-k keys distinct and the k-th above
+// the (k+1)-th): the selection is unique and comes out in descending order; k wavefront
+// arg-max rounds find it.  Every other row replays the CPU algorithm exactly:
+//  * wavefront-parallel introselect: the row is held 4 keys per lane (position
+//    p = 64 * slot + lane); each median-of-3 / Hoare partition step is evaluated in one pass
+//    -- the j-th left stop (ascending position holding a key <= pivot) is exchanged with the
+//    j-th right stop (descending position holding a key >= pivot) while left < right, and
+//    the stops are ranked with ballots -- so a partition costs a few LDS round trips
+//    instead of a serial scan;
+//  * the final std::sort of the first k-1 entries (k - 1 <= 16) is an insertion sort, i.e.
+//    a stable descending sort, computed by ranking;
+//  * the rare remainder (introselect depth limit reached -> heap select; partial_sort regime
+//    k*64 <= n; k - 1 > 16) runs the sequential algorithm on lane 0 over the row in LDS.
 #include "common.h"
 
 namespace ferry {
 namespace {
 
-constexpr int kMaxE = 256;  // 4 values per lane
+constexpr int kMaxE = 256;  // 4 keys per lane
 constexpr int kMaxK = 32;
 constexpr int kWaves = 4;
 
 struct Pair {
-  float v;
+  uint32_t v;  // ordered key: larger key = "before" in the torch comparator
   int32_t i;
 };
 
-__device__ __forceinline__ bool before(const Pair& x, const Pair& y) {
-  const bool xn = x.v != x.v, yn = y.v != y.v;
-  return (xn && !yn) || (x.v > y.v);
+__device__ __forceinline__ bool before(const Pair& x, const Pair& y) { return x.v > y.v; }
+
+// order-preserving key of a float: -0 == +0, NaN above +inf (all NaNs equal)
+__device__ __forceinline__ uint32_t ordered_key(float f) {
+  if (f != f) return 0xffffffffu;
+  if (f == 0.f) f = 0.f;
+  uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// ---- heap primitives ----
+// ---------------------------------------------------------------------------------------------
+// Sequential restatement (lane 0, row in LDS): libstdc++ introselect / introsort / heap select
+// ---------------------------------------------------------------------------------------------
 __device__ void push_heap_(Pair* a, int hole, int top, Pair value) {
   int parent = (hole - 1) / 2;
   while (hole > top && before(a[parent], value)) {
@@ -85,8 +101,6 @@ __device__ void sort_heap_(Pair* a, int len) {
     pop_heap_(a, len, len);
   }
 }
-
-// ---- sorting primitives ----
 __device__ void unguarded_linear_insert_(Pair* a, int last) {
   Pair val = a[last];
   int next = last - 1;
@@ -148,19 +162,19 @@ __device__ int partition_pivot_(Pair* a, int first, int last) {
 }
 __device__ __forceinline__ int lg2_(int n) { return 31 - __clz(n); }
 
-// introsort of a[first, last): partition until ranges of <= 16, then one insertion sort.
-__device__ void sort_(Pair* a, int first, int last) {
-  if (first == last) return;
-  // explicit stack replaces the recursion on the right part
-  int st_first[32], st_last[32], st_depth[32];
+// std::sort of a[first, last): introsort loop down to ranges of 16, then insertion sort.
+// stk holds 3 * kStack ints of LDS for the pending right-hand ranges.
+constexpr int kStack = 16;
+__device__ void sort_(Pair* a, int first, int last, int* stk) {
+  if (last - first <= 1) return;
   int sp = 0;
-  st_first[sp] = first;
-  st_last[sp] = last;
-  st_depth[sp] = lg2_(last - first) * 2;
+  stk[0] = first;
+  stk[1] = last;
+  stk[2] = lg2_(last - first) * 2;
   ++sp;
   while (sp > 0) {
     --sp;
-    int f = st_first[sp], l = st_last[sp], depth = st_depth[sp];
+    int f = stk[3 * sp], l = stk[3 * sp + 1], depth = stk[3 * sp + 2];
     while (l - f > 16) {
       if (depth == 0) {
         heap_select_(a + f, l - f, l - f);
@@ -169,12 +183,15 @@ __device__ void sort_(Pair* a, int first, int last) {
       }
       --depth;
       const int cut = partition_pivot_(a, f, l);
-      // the reference recurses on [cut, l) first, then loops on [f, cut); processing
-      // order does not change the result because the ranges are disjoint.
-      st_first[sp] = cut;
-      st_last[sp] = l;
-      st_depth[sp] = depth;
-      ++sp;
+      // the reference recurses on [cut, l) and loops on [f, cut): disjoint ranges, so the
+      // processing order does not change the result.  Ranges here hold at most kMaxK - 1
+      // elements, so the pending stack stays far below kStack entries.
+      if (sp < kStack) {
+        stk[3 * sp] = cut;
+        stk[3 * sp + 1] = l;
+        stk[3 * sp + 2] = depth;
+        ++sp;
+      }
       l = cut;
     }
   }
@@ -186,35 +203,282 @@ __device__ void sort_(Pair* a, int first, int last) {
   }
 }
 
-__device__ void nth_element_(Pair* a, int nth, int n) {
-  if (n == 0 || nth == n) return;
-  int first = 0, last = n;
-  int depth = lg2_(n) * 2;
-  while (last - first > 3) {
-    if (depth == 0) {
-      heap_select_(a + first, nth + 1 - first, last - first);
-      swap_(a, first, nth);
-      return;
-    }
-    --depth;
-    const int cut = partition_pivot_(a, first, last);
-    if (cut <= nth)
-      first = cut;
-    else
-      last = cut;
-  }
-  insertion_sort_(a, first, last);
+// ---------------------------------------------------------------------------------------------
+// Wavefront-parallel restatement
+// ---------------------------------------------------------------------------------------------
+struct WaveScratch {
+  Pair stage[kMaxE];
+  int16_t lstop[kMaxE];
+  int16_t rstop[kMaxE];
+  float prob[kMaxE];
+  int32_t sel[kMaxK];
+  int32_t stack[3 * kStack];
+};
+
+__device__ __forceinline__ void wave_sync_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
 }
 
-// The full CPU selection on a row staged in LDS; result in a[0..k).
-__device__ void exact_topk_(Pair* a, int n, int k, bool sorted) {
-  if (k * 64 <= n) {
-    heap_select_(a, k, n);
-    sort_heap_(a, k);
-  } else {
-    nth_element_(a, k - 1, n);
-    if (sorted) sort_(a, 0, k - 1);
+// value at uniform position p = 64 * slot + lane: read lane (p & 63) of each of the four
+// registers and select by slot (selecting between register values, not array elements, keeps
+// the arrays out of scratch memory)
+__device__ __forceinline__ uint32_t key_at(const uint32_t (&k)[4], int p) {
+  const int l = p & 63, s = p >> 6;
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)k[0], l);
+  const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)k[1], l);
+  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)k[2], l);
+  const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)k[3], l);
+  return s == 0 ? r0 : s == 1 ? r1 : s == 2 ? r2 : r3;
+}
+__device__ __forceinline__ int32_t idx_at(const int32_t (&ix)[4], int p) {
+  const int l = p & 63, s = p >> 6;
+  const int32_t r0 = __builtin_amdgcn_readlane(ix[0], l);
+  const int32_t r1 = __builtin_amdgcn_readlane(ix[1], l);
+  const int32_t r2 = __builtin_amdgcn_readlane(ix[2], l);
+  const int32_t r3 = __builtin_amdgcn_readlane(ix[3], l);
+  return s == 0 ? r0 : s == 1 ? r1 : s == 2 ? r2 : r3;
+}
+__device__ __forceinline__ void set_at(uint32_t (&k)[4], int32_t (&ix)[4], int p, uint32_t kv,
+                                       int32_t iv, int lane) {
+  const bool mine = lane == (p & 63);
+  const int s = p >> 6;
+  // per-element selects (no indexed store, which would move the arrays to scratch)
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const bool hit = mine && q == s;
+    k[q] = hit ? kv : k[q];
+    ix[q] = hit ? iv : ix[q];
   }
+}
+__device__ __forceinline__ void swap_at(uint32_t (&k)[4], int32_t (&ix)[4], int a, int b,
+                                        int lane) {
+  const uint32_t ka = key_at(k, a), kb = key_at(k, b);
+  const int32_t ia = idx_at(ix, a), ib = idx_at(ix, b);
+  set_at(k, ix, a, kb, ib, lane);
+  set_at(k, ix, b, ka, ia, lane);
+}
+
+// One std::__unguarded_partition_pivot step on [first, last); returns the cut.
+__device__ __forceinline__ int wave_partition_pivot(uint32_t (&k)[4], int32_t (&ix)[4], int first, int last,
+                                    int lane, WaveScratch& ws) {
+  const int mid = first + (last - first) / 2;
+  {
+    // __move_median_to_first(first, first + 1, mid, last - 1)
+    const int a = first + 1, b = mid, c = last - 1;
+    const uint32_t ka = key_at(k, a), kb = key_at(k, b), kc = key_at(k, c);
+    int m;
+    if (ka > kb) {
+      m = (kb > kc) ? b : (ka > kc) ? c : a;
+    } else {
+      m = (ka > kc) ? a : (kb > kc) ? c : b;
+    }
+    swap_at(k, ix, first, m, lane);
+  }
+  const uint32_t piv = key_at(k, first);
+  // left stops: [first+1, last) with key <= pivot; right stops: [first, last) with key >= pivot
+  uint64_t bl[4], bg[4];
+  bool le[4], ge[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int pos = s * 64 + lane;
+    le[s] = pos > first && pos < last && k[s] <= piv;
+    ge[s] = pos >= first && pos < last && k[s] >= piv;
+    bl[s] = __ballot(le[s]);
+    bg[s] = __ballot(ge[s]);
+  }
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  const uint64_t gt_mask = (lane == 63) ? 0ull : (~0ull << (lane + 1));
+  int nl = 0, ng = 0;
+  int rl[4], rg[4];
+  int below_l = 0;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    rl[s] = below_l + __popcll(bl[s] & lt_mask);
+    below_l += __popcll(bl[s]);
+  }
+  nl = below_l;
+  int above_g = 0;
+#pragma unroll
+  for (int s = 3; s >= 0; --s) {
+    rg[s] = above_g + __popcll(bg[s] & gt_mask);
+    above_g += __popcll(bg[s]);
+  }
+  ng = above_g;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int pos = s * 64 + lane;
+    if (le[s]) ws.lstop[rl[s]] = (int16_t)pos;
+    if (ge[s]) ws.rstop[rg[s]] = (int16_t)pos;
+    if (pos < last) ws.stage[pos] = Pair{k[s], ix[s]};
+  }
+  wave_sync_lds();
+  // number of exchanges: prefix of m with lstop[m] < rstop[m]
+  const int mm = nl < ng ? nl : ng;
+  int nswap = 0;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int m = s * 64 + lane;
+    const bool f = m < mm && ws.lstop[m] < ws.rstop[m];
+    nswap += __popcll(__ballot(f));
+  }
+  int cut;
+  if (nswap == 0) {
+    cut = nl > 0 ? ws.lstop[0] : last - 1;
+  } else {
+    const int lnext = nswap < nl ? ws.lstop[nswap] : 0x7fffffff;
+    const int rprev = ws.rstop[nswap - 1];
+    cut = lnext < rprev ? lnext : rprev;
+  }
+  // the median-of-3 pivot guarantees a left stop inside the range, so cut lies in
+  // [first + 1, last - 1]; the clamp only keeps indices in range should that ever fail
+  cut = cut < first + 1 ? first + 1 : (cut > last - 1 ? last - 1 : cut);
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    int src = -1;
+    if (le[s] && rl[s] < nswap) src = ws.rstop[rl[s]];
+    else if (ge[s] && rg[s] < nswap) src = ws.lstop[rg[s]];
+    if (src >= 0) {
+      const Pair p = ws.stage[src];
+      k[s] = p.v;
+      ix[s] = p.i;
+    }
+  }
+  wave_sync_lds();
+  return cut;
+}
+
+// stable descending sort of the uniform positions [first, last) (last - first <= 16):
+// the result of std::__insertion_sort on that range
+__device__ __forceinline__ void wave_insertion_sort(uint32_t (&k)[4], int32_t (&ix)[4], int first, int last,
+                                    int lane, WaveScratch& ws) {
+  const int len = last - first;
+  if (len <= 1) return;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int pos = s * 64 + lane;
+    if (pos >= first && pos < last) ws.stage[pos] = Pair{k[s], ix[s]};
+  }
+  wave_sync_lds();
+  int dest[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int pos = s * 64 + lane;
+    dest[s] = -1;
+    if (pos >= first && pos < last) {
+      int d = first;
+      for (int q = first; q < last; ++q) {
+        const uint32_t kq = ws.stage[q].v;
+        d += (kq > k[s]) || (kq == k[s] && q < pos);
+      }
+      dest[s] = d;
+    }
+  }
+  wave_sync_lds();
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+    if (dest[s] >= 0) ws.stage[dest[s]] = Pair{k[s], ix[s]};
+  wave_sync_lds();
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int pos = s * 64 + lane;
+    if (pos >= first && pos < last) {
+      k[s] = ws.stage[pos].v;
+      ix[s] = ws.stage[pos].i;
+    }
+  }
+  wave_sync_lds();
+}
+
+// Exact CPU top-k selection of the row (n keys, position p = 64*s + lane); the chosen indices
+// are written to ws.sel[0..k).
+__device__ __forceinline__ void exact_select(uint32_t (&k)[4], int32_t (&ix)[4], int n, int kk, bool sorted,
+                             int lane, WaveScratch& ws) {
+  bool serial = kk * 64 <= n || (sorted && kk - 1 > 16);
+  if (!serial) {
+    // std::nth_element(first, first + kk - 1, last)
+    const int nth = kk - 1;
+    int first = 0, last = n;
+    int depth = lg2_(n) * 2;
+    if (nth != n) {
+      while (last - first > 3) {
+        if (depth == 0) {
+          serial = true;  // heap select from this state on lane 0
+          break;
+        }
+        --depth;
+        const int cut = wave_partition_pivot(k, ix, first, last, lane, ws);
+        if (cut <= nth)
+          first = cut;
+        else
+          last = cut;
+      }
+      if (!serial) wave_insertion_sort(k, ix, first, last, lane, ws);
+    }
+    if (serial) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int pos = s * 64 + lane;
+        if (pos < n) ws.stage[pos] = Pair{k[s], ix[s]};
+      }
+      wave_sync_lds();
+      if (lane == 0) {
+        heap_select_(ws.stage + first, nth + 1 - first, last - first);
+        swap_(ws.stage, first, nth);
+        if (sorted) sort_(ws.stage, 0, kk - 1, ws.stack);
+        for (int j = 0; j < kk; ++j) ws.sel[j] = ws.stage[j].i;
+      }
+      wave_sync_lds();
+      return;
+    }
+    if (sorted) wave_insertion_sort(k, ix, 0, kk - 1, lane, ws);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int pos = s * 64 + lane;
+      if (pos < kk) ws.sel[pos] = ix[s];
+    }
+    wave_sync_lds();
+    return;
+  }
+  // partial_sort regime, or a final sort longer than 16: sequential on lane 0
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int pos = s * 64 + lane;
+    if (pos < n) ws.stage[pos] = Pair{k[s], ix[s]};
+  }
+  wave_sync_lds();
+  if (lane == 0) {
+    Pair* a = ws.stage;
+    if (kk * 64 <= n) {
+      heap_select_(a, kk, n);
+      sort_heap_(a, kk);
+    } else {
+      int first = 0, last = n, depth = lg2_(n) * 2;
+      const int nth = kk - 1;
+      bool done = false;
+      if (nth != n) {
+        while (last - first > 3) {
+          if (depth == 0) {
+            heap_select_(a + first, nth + 1 - first, last - first);
+            swap_(a, first, nth);
+            done = true;
+            break;
+          }
+          --depth;
+          const int cut = partition_pivot_(a, first, last);
+          if (cut <= nth)
+            first = cut;
+          else
+            last = cut;
+        }
+        if (!done) insertion_sort_(a, first, last);
+      }
+      if (sorted) sort_(a, 0, kk - 1, ws.stack);
+    }
+    for (int j = 0; j < kk; ++j) ws.sel[j] = a[j].i;
+  }
+  wave_sync_lds();
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -227,22 +491,13 @@ __device__ __forceinline__ float wave_sum(float v) {
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
   return v;
 }
-__device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
-// arg-max with the torch comparator on values; equal values -> lower index
-__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
-    float ov = __shfl_xor(v, off, 64);
-    int oi = __shfl_xor(i, off, 64);
-    if (ov > v || (ov == v && oi < i)) {
-      v = ov;
-      i = oi;
-    }
+    const uint32_t o = (uint32_t)__shfl_xor((int)v, off, 64);
+    v = o > v ? o : v;
   }
+  return v;
 }
 
 template <typename T>
@@ -258,108 +513,102 @@ __device__ __forceinline__ float load_logit<bf16_t>(const bf16_t* p) {
 
 template <typename T>
 __global__ __launch_bounds__(64 * kWaves) void router_kernel(
-    const T* __restrict__ logits, int64_t tokens, int n, int k, int renorm, float scale,
+    const T* __restrict__ logits, int64_t tokens, int n, int kk, int renorm, float scale,
     int sorted, int64_t* __restrict__ idx_out, bf16_t* __restrict__ w_out,
     float* __restrict__ probs_out, int32_t* __restrict__ tie_rows) {
-  __shared__ Pair stage[kWaves][kMaxE];
-  __shared__ float prob_lds[kWaves][kMaxE];
-  __shared__ int sel[kWaves][kMaxK];
+  __shared__ WaveScratch scratch[kWaves];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const float NEG = -INFINITY;
+  WaveScratch& ws = scratch[wave];
   for (int64_t row = (int64_t)blockIdx.x * kWaves + wave; row < tokens;
        row += (int64_t)gridDim.x * kWaves) {
     const T* src = logits + row * n;
     float x[4];
-    bool has_nan = false;
+    bool bad = false;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const int e = lane + 64 * s;
-      x[s] = e < n ? load_logit<T>(src + e) : NEG;
-      has_nan |= (e < n) && (x[s] != x[s]);
+      const int e = s * 64 + lane;
+      x[s] = e < n ? load_logit<T>(src + e) : -INFINITY;
+      bad |= (e < n) && (x[s] != x[s] || x[s] == INFINITY);
     }
+    const bool row_bad = __any(bad);  // softmax of this row is all NaN
     // softmax in fp32
     float m = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
     m = wave_max(m);
     float ex[4], part = 0.f;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const int e = lane + 64 * s;
+      const int e = s * 64 + lane;
       ex[s] = e < n ? expf(x[s] - m) : 0.f;
       part += ex[s];
     }
-    const float inv = 1.0f / wave_sum(part);
+    const float sum = wave_sum(part);
+    const float inv = 1.0f / sum;
+    uint32_t key[4];
+    int32_t ix[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const int e = lane + 64 * s;
+      const int e = s * 64 + lane;
+      const float p = row_bad ? __builtin_nanf("") : ex[s] * inv;
       if (e < n) {
-        const float p = ex[s] * inv;
-        prob_lds[wave][e] = p;
+        ws.prob[e] = p;
         if (probs_out) probs_out[row * n + e] = p;
       }
+      key[s] = e < n ? (row_bad ? 0xffffffffu : ordered_key(x[s])) : 0u;
+      ix[s] = e;
     }
-    // fast path: k arg-max rounds; any repeated value among the top k (or at the k-th /
-    // (k+1)-th boundary) sends the row to the exact path.
-    bool exact = !sorted || __any(has_nan);
-    if (!exact && k * 64 > n) {
-      float cur[4];
+    // fast path: kk arg-max rounds on distinct keys (nth_element regime, sorted output)
+    bool exact = !sorted || row_bad || kk * 64 <= n;
+    if (!exact) {
+      uint32_t cur[4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) cur[s] = x[s];
-      for (int r = 0; r < k && !exact; ++r) {
-        float bv = NEG;
-        int bi = 1 << 30;
+      for (int s = 0; s < 4; ++s) cur[s] = (s * 64 + lane < n) ? key[s] : 0u;
+      for (int r = 0; r < kk; ++r) {
+        uint32_t lm = cur[0];
+#pragma unroll
+        for (int s = 1; s < 4; ++s) lm = cur[s] > lm ? cur[s] : lm;
+        const uint32_t best = wave_max_u(lm);
+        int eq = 0, where = 0;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-          const int e = lane + 64 * s;
-          if (e < n && (cur[s] > bv || (cur[s] == bv && e < bi)) && cur[s] != NEG) {
-            bv = cur[s];
-            bi = e;
-          }
+          const bool hit = (s * 64 + lane < n) && cur[s] == best;
+          eq += hit;
+          if (hit) where = s * 64 + lane;
         }
-        wave_argmax(bv, bi);
-        int eq = 0;
+        const uint64_t hits = __ballot(eq > 0);
+        const int total = __popcll(hits) == 1 ? __shfl(eq, __ffsll((long long)hits) - 1, 64) : 2;
+        if (total != 1 || best == 0u) {
+          exact = true;  // a tie decides membership or order
+          break;
+        }
+        const int owner = __ffsll((long long)hits) - 1;
+        const int pos = __shfl(where, owner, 64);
+        if (lane == 0) ws.sel[r] = pos;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) eq += (lane + 64 * s < n) && (cur[s] == bv);
-        eq = wave_sum_i(eq);
-        if (eq != 1 || bv == NEG) {
-          exact = true;  // a tie (or -inf values) decides membership or order
-        } else {
-          if (lane == (bi & 63)) cur[bi >> 6] = NEG;
-          if (lane == 0) sel[wave][r] = bi;
-        }
+        for (int s = 0; s < 4; ++s) cur[s] = (lane == owner && s == (pos >> 6)) ? 0u : cur[s];
       }
-    } else if (!exact) {
-      exact = true;  // partial-sort regime (k*64 <= n): run the CPU algorithm
+      wave_sync_lds();
     }
     if (exact) {
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int e = lane + 64 * s;
-        if (e < n) stage[wave][e] = Pair{x[s], e};
-      }
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      if (lane == 0) {
-        exact_topk_(stage[wave], n, k, sorted != 0);
-        for (int j = 0; j < k; ++j) sel[wave][j] = stage[wave][j].i;
-        if (tie_rows) atomicAdd(tie_rows, 1);
-      }
+      exact_select(key, ix, n, kk, sorted != 0, lane, ws);
+      if (lane == 0 && tie_rows) atomicAdd(tie_rows, 1);
     }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    if (lane == 0) {
-      float sum = 0.f;
-      for (int j = 0; j < k; ++j) sum += prob_lds[wave][sel[wave][j]];
-      for (int j = 0; j < k; ++j) {
-        const int e = sel[wave][j];
-        float w = prob_lds[wave][e];
-        if (renorm) w = w / sum;
-        w = w * scale;
-        idx_out[row * k + j] = e;
-        w_out[row * k + j] = f32_to_bf16(w);
-      }
+    wave_sync_lds();
+    // weights: lanes 0..kk-1 each own one selected expert
+    float wv = 0.f;
+    int e = 0;
+    if (lane < kk) {
+      e = ws.sel[lane];
+      wv = ws.prob[e];
     }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    float tot = 0.f;
+    for (int j = 0; j < kk; ++j) tot += __shfl(wv, j, 64);  // j-ascending like the reference sum
+    if (lane < kk) {
+      float w = renorm ? wv / tot : wv;
+      w = w * scale;
+      idx_out[row * kk + lane] = e;
+      w_out[row * kk + lane] = f32_to_bf16(w);
+    }
+    wave_sync_lds();
   }
 }
 
@@ -386,11 +635,11 @@ extern "C" int ferry_router_topk(const void* logits, int32_t logits_dtype, int64
   const int grid = (int)(want < 65535 ? want : 65535);
   hipStream_t s = (hipStream_t)stream;
   if (logits_dtype == FERRY_BF16) {
-    hipLaunchKernelGGL(router_kernel<bf16_t>, dim3(grid), dim3(64 * kWaves), 0, s,
+    launch("router_kernel", router_kernel<bf16_t>, dim3(grid), dim3(64 * kWaves), 0, s,
                        (const bf16_t*)logits, tokens, (int)experts, (int)topk, renorm, scale,
                        sorted, idx_out, (bf16_t*)w_out_bf16, probs_out, tie_rows);
   } else {
-    hipLaunchKernelGGL(router_kernel<float>, dim3(grid), dim3(64 * kWaves), 0, s,
+    launch("router_kernel", router_kernel<float>, dim3(grid), dim3(64 * kWaves), 0, s,
                        (const float*)logits, tokens, (int)experts, (int)topk, renorm, scale,
                        sorted, idx_out, (bf16_t*)w_out_bf16, probs_out, tie_rows);
   }

@@ -15,9 +15,25 @@ from .h2d import H2DEngine
 
 __all__ = ['execute_experts', 'pack_dispatch', 'unpack_dispatch', 'reduce_partials',
            'scatter_returned', 'H2DEngine', 'router_topk', 'layout', 'expert_ffn', 'combine',
-           'history_update', 'current_stream']
+           'history_update', 'current_stream', 'PHASE_UP', 'PHASE_DOWN', 'PHASE_BOTH']
 
 MAX_EXPERTS = 512
+
+
+def timing_enable(on=True):
+    """Per-launch kernel timing: every kernel launch of the library gets a start/stop HIP event
+    pair bracketing exactly that dispatch (hipExtLaunchKernel).  Turning it on clears the log."""
+    check(lib().ferry_timing_enable(int(bool(on))), 'timing_enable')
+
+
+def timing_summary(kernel):
+    """(launches, total ms) of the timed launches of ``kernel`` (e.g. 'ffn_up_skinny')."""
+    import ctypes
+    n = ctypes.c_int64()
+    ms = ctypes.c_double()
+    check(lib().ferry_timing_summary(kernel.encode(), ctypes.byref(n), ctypes.byref(ms)),
+          'timing_summary')
+    return int(n.value), float(ms.value)
 
 
 def current_stream(device=None):
@@ -100,9 +116,16 @@ def layout(selected, weights, experts, out=None):
     return lay
 
 
+PHASE_UP, PHASE_DOWN, PHASE_BOTH = 1, 2, 3
+
+
 def expert_ffn(cache, x, w_sorted, starts, rows, cols, expert_list, slot_of, hidden,
-               intermediate, act, out, out_mode=0, max_rows=None, experts=None):
-    """Grouped SwiGLU over cache slots for the experts in ``expert_list`` (host ints)."""
+               intermediate, act, out, out_mode=0, max_rows=None, experts=None, phases=PHASE_BOTH):
+    """Grouped SwiGLU over cache slots for the experts in ``expert_list`` (host ints).
+
+    phases: PHASE_UP (gate/up + SwiGLU into ``act``), PHASE_DOWN (down + routing weight from
+    ``act`` into ``out``) or PHASE_BOTH.
+    """
     R, k = w_sorted.shape
     el = np.ascontiguousarray(expert_list, dtype=np.int32)
     so = np.ascontiguousarray(slot_of, dtype=np.int32)
@@ -113,7 +136,8 @@ def expert_ffn(cache, x, w_sorted, starts, rows, cols, expert_list, slot_of, hid
         _dev(starts, 'starts', torch.int64), _dev(rows, 'rows', torch.int64),
         _dev(cols, 'cols', torch.int64), el.ctypes.data, len(el), so.ctypes.data, E,
         int(max_rows if max_rows is not None else R), _dev(act, 'act', torch.bfloat16),
-        _dev(out, 'out', torch.bfloat16), int(out_mode), current_stream(x.device)), 'expert_ffn')
+        _dev(out, 'out', torch.bfloat16), int(out_mode), int(phases), current_stream(x.device)),
+        'expert_ffn')
     return out
 
 

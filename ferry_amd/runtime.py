@@ -54,10 +54,8 @@ class OffloadRuntime:
         self.controller = Controller(spec, capacities, policy, topology, balance_tol_bps, salt)
         self.gather = RouteGather(spec.topk, spec.experts, history_window, eviction_score)
         self.transport = Transport(self.ops, spec.topk, spec.experts)
-        self._scores_dev = torch.zeros(spec.experts, dtype=torch.float32, device=self.device)
-        self._scores_host = torch.zeros(spec.experts, dtype=torch.float32, pin_memory=True)
-        self._ids_dev = None
-        self._ids_host = None
+        self._stage_dev = None   # [scores fp32 E | IDs uint8 T*k]: one D2H copy per call
+        self._stage_host = None
         self._bufs = {}
         self.h2d = None
         self.reset()
@@ -82,6 +80,7 @@ class OffloadRuntime:
         self.decode_fetches_per_rank = np.zeros(self.world, np.int64)
         self.serial_wait_ns = 0
         self.timings = []
+        self.kernel_bytes = dict(up=0, down=0, flops=0, experts=0, launches=0)
 
     def _buffers(self, tokens):
         b = self._bufs.get(tokens)
@@ -93,10 +92,10 @@ class OffloadRuntime:
                                       device=self.device),
                      layout=None)
             self._bufs[tokens] = b
-        if self._ids_dev is None or self._ids_dev.numel() < tokens * self.spec.topk:
-            n = tokens * self.spec.topk
-            self._ids_dev = torch.empty(n, dtype=torch.uint8, device=self.device)
-            self._ids_host = torch.empty(n, dtype=torch.uint8, pin_memory=True)
+        n = 4 * self.spec.experts + tokens * self.spec.topk
+        if self._stage_dev is None or self._stage_dev.numel() < n:
+            self._stage_dev = torch.zeros(n, dtype=torch.uint8, device=self.device)
+            self._stage_host = torch.zeros(n, dtype=torch.uint8, pin_memory=True)
         return b
 
     # -- one layer call ------------------------------------------------------------------------
@@ -114,14 +113,15 @@ class OffloadRuntime:
 
         # 1. history + D2H of the IDs (and scores)
         frequency = self.gather.score == 'frequency'
-        ids_dev = self._ids_dev[:T * k]
+        nbytes = 4 * E + T * k
+        scores_dev = self._stage_dev[:4 * E].view(torch.float32)
+        ids_dev = self._stage_dev[4 * E:nbytes]
         if frequency:
-            self.device_history.update(layer, selected, self._scores_dev, ids_dev)
-            self._scores_host.copy_(self._scores_dev, non_blocking=True)
+            self.device_history.update(layer, selected, scores_dev, ids_dev)
         else:
             ids_dev.copy_(selected.reshape(-1).to(torch.uint8))
-        ids_host = self._ids_host[:T * k]
-        ids_host.copy_(ids_dev, non_blocking=True)
+        stage_host = self._stage_host[:nbytes]
+        stage_host.copy_(self._stage_dev[:nbytes], non_blocking=True)
         tail_host = None
         if not frequency:
             tail = min(T, self.window)
@@ -135,9 +135,10 @@ class OffloadRuntime:
 
         # 3. plan + fetch
         d2h.synchronize()
-        ids = ids_host.numpy().astype(np.int64).reshape(T, k)
+        host = stage_host.numpy()
+        ids = host[4 * E:].astype(np.int64).reshape(T, k)
         if frequency:
-            scores = self._scores_host.numpy().copy()
+            scores = host[:4 * E].view(np.float32).copy()
         else:
             self.history.update(layer, tail_host.numpy())
             scores = self.history.scores(layer)
@@ -165,6 +166,7 @@ class OffloadRuntime:
         resident_list = np.flatnonzero(active & ~missing)
         missing_list = np.flatnonzero(missing)
         slot32 = slot_of.astype(np.int32)
+        counts_e = np.bincount(ids.reshape(-1), minlength=E) if self.timing else None
         common = (self.cache, hidden.contiguous(), lay.w_sorted, lay.starts, lay.rows, lay.cols)
         if not self.overlap and len(fetch_slots):
             started = time.perf_counter_ns()
@@ -172,16 +174,14 @@ class OffloadRuntime:
             self.serial_wait_ns += time.perf_counter_ns() - started
         if len(resident_list):
             self.h2d.wait_stream(slot_of[resident_list], stream)
-            self.ops.expert_ffn(*common, resident_list, slot32, spec.hidden, spec.intermediate,
-                                buf['act'], buf['part'], out_mode=0, max_rows=T, experts=E)
+            self._ffn(common, resident_list, slot32, buf, T, stream, counts_e)
         if len(missing_list):
             if timing:
                 ev[2].record(stream)
             self.h2d.wait_stream(fetch_slots, stream)
             if timing:
                 ev[3].record(stream)
-            self.ops.expert_ffn(*common, missing_list, slot32, spec.hidden, spec.intermediate,
-                                buf['act'], buf['part'], out_mode=0, max_rows=T, experts=E)
+            self._ffn(common, missing_list, slot32, buf, T, stream, counts_e)
         self.h2d.mark_used(slot_of[np.flatnonzero(active)], stream)
         if timing:
             self.timings.append(ev)
@@ -189,6 +189,22 @@ class OffloadRuntime:
 
         # 5. combine
         return self.transport.combine(hidden, buf['part'], dict(layout=lay))
+
+    def _ffn(self, common, expert_list, slot32, buf, T, stream, counts_e):
+        """Phase 1 (gate/up + SwiGLU) and phase 2 (down + weight) for ``expert_list``."""
+        spec = self.spec
+        self.ops.expert_ffn(*common, expert_list, slot32, spec.hidden, spec.intermediate,
+                            buf['act'], buf['part'], out_mode=0, max_rows=T, experts=spec.experts)
+        if self.timing:
+            H, I = spec.hidden, spec.intermediate
+            rows = int(counts_e[expert_list].sum())
+            d = len(expert_list)
+            # algorithmic bytes: weights read once, x / activation rows read, outputs written
+            self.kernel_bytes['up'] += d * 2 * I * H * 2 + rows * (H * 2 + I * 2)
+            self.kernel_bytes['down'] += d * H * I * 2 + rows * (I * 2 + H * 2 + 2)
+            self.kernel_bytes['flops'] += 2 * 3 * H * I * rows
+            self.kernel_bytes['experts'] += d
+            self.kernel_bytes['launches'] += 1
 
     def fetch_timing(self):
         """(total fetch ms, exposed wait ms) over the layer calls recorded with timing=True."""

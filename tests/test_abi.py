@@ -1,0 +1,184 @@
+"""CPU tier: the C ABI library loads and exports every declared symbol; the host-side product
+code (C++ planner, Python API mirror) matches the oracle.  No GPU compute is called here."""
+import ctypes
+import re
+from dataclasses import dataclass
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle.history import GateHistoryRef, frequency_rows
+from oracle.policy import PlannerRef
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared_symbols():
+    text = (ROOT / 'include' / 'ferry_amd.h').read_text()
+    text = re.sub(r'/\*.*?\*/', '', text, flags=re.S)
+    return sorted(set(re.findall(r'\b(ferry_[a-z0-9_]+)\s*\(', text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from ferry_amd._lib import LIB_PATH, SIGNATURES
+    handle = ctypes.CDLL(str(LIB_PATH))
+    declared = _declared_symbols()
+    assert len(declared) >= 20
+    for name in declared:
+        assert hasattr(handle, name), f'{name} declared in include/ferry_amd.h but not exported'
+    bound = {n for n, _, _ in SIGNATURES}
+    assert set(declared) <= bound | {'ferry_timing_enable', 'ferry_timing_summary'}, \
+        sorted(set(declared) - bound)
+
+
+def test_abi_version_and_errors():
+    from ferry_amd._lib import last_error, lib
+    L = lib()
+    assert L.ferry_abi_version() == 1
+    # argument validation fails before any device work
+    assert L.ferry_router_topk(None, 0, 4, 300, 8, 1, 1.0, 1, None, None, None, None, None) != 0
+    assert 'experts' in last_error()
+    assert L.ferry_layout(None, None, 4, 20, 8, None, None, None, None, None, None, None, 0, None) != 0
+    assert L.ferry_combine(None, None, 1, 1, 12, None, None) != 0
+    assert 'hidden' in last_error()
+    assert L.ferry_expert_ffn(None, 1, 100, 128, None, 1, 1, None, None, None, None, None, 0, None,
+                              1, 1, None, None, 0, 3, None) != 0
+
+
+@dataclass(frozen=True)
+class _Spec:
+    layers: int
+    experts: int
+
+
+def test_product_planner_matches_oracle_traces():
+    from ferry_amd.policy import Controller, _choose_slot, layer_slots
+    from ferry_amd.quota import Topology
+    rng = np.random.default_rng(1)
+    for trial in range(12):
+        L, E = int(rng.integers(1, 5)), int(rng.integers(2, 40))
+        cap = int(rng.integers(1, 2 * E))
+        ctl = Controller(_Spec(L, E), [cap], 'ferry', Topology.uniform(1, E))
+        ref = PlannerRef(L, E, cap)
+        for ev in range(80):
+            layer = int(rng.integers(0, L))
+            k = int(rng.integers(1, min(E, 8) + 1))
+            T = int(rng.integers(1, 6))
+            sel = np.stack([rng.choice(E, k, replace=False) for _ in range(T)])
+            gs = (rng.integers(0, 5, E) / 4).astype(np.float32)
+            try:
+                f_ref, d_ref = ref.plan(ev, layer, sel, gs)
+            except AssertionError:
+                f_ref = None
+            try:
+                f, d, counts = ctl.plan(ev, layer, sel, np.zeros(T, np.int64), gs)
+            except AssertionError:
+                f = None
+            assert (f is None) == (f_ref is None)
+            if f is None:
+                break
+            assert np.array_equal(f, f_ref) and np.array_equal(d, d_ref)
+            assert counts.tolist() == [len(f)]
+            assert np.array_equal(ctl.slots[0], ref.slots)
+            assert np.array_equal(ctl.owner, ref.owner) and np.array_equal(ctl.last, ref.last)
+            assert np.array_equal(layer_slots(ctl.slots[0], cap, layer, E), ref.layer_slots(layer))
+            active = np.zeros(E, np.uint8)
+            active[np.unique(sel)] = 1
+            from oracle.native import lib as olib
+            want = olib().oracle_choose_slot(layer, active.ctypes.data, ref.slots.ctypes.data, cap,
+                                             ref.last.ctypes.data, ref.scores.ctypes.data, E)
+            assert _choose_slot(0, layer, active, ctl.slots, [cap], ctl.last, ctl.scores, E) == want
+
+
+def test_product_planner_golden_trace():
+    from ferry_amd.policy import Controller
+    from ferry_amd.quota import Topology
+    d = np.load(ROOT / 'tests' / 'golden' / 'planner.npz')
+    L, E, cap = int(d['layers']), int(d['experts']), int(d['cap'])
+    ctl = Controller(_Spec(L, E), [cap], 'ferry', Topology.uniform(1, E))
+    off = foff = 0
+    for ev, T in enumerate(d['sizes']):
+        sel = d['selected'][off:off + T]
+        off += T
+        f, _, _ = ctl.plan(ev, ev % L, sel, np.zeros(T, np.int64), d['gate_scores'][ev])
+        n = int(d['nfetch'][ev])
+        assert np.array_equal(f, d['fetches'][foff:foff + n])
+        foff += n
+    assert np.array_equal(ctl.slots[0], d['final_slots'])
+
+
+def test_product_planner_overflow_raises_assertion():
+    from ferry_amd.policy import Controller
+    from ferry_amd.quota import Topology
+    ctl = Controller(_Spec(1, 8), [2], 'ferry', Topology.uniform(1, 8))
+    with pytest.raises(AssertionError, match='admission capacity'):
+        ctl.plan(0, 0, np.array([[0, 1, 2]]), np.zeros(1, np.int64), np.zeros(8, np.float32))
+
+
+def test_world_gt_1_rejected():
+    from ferry_amd.policy import Controller
+    from ferry_amd.quota import Topology
+    with pytest.raises(NotImplementedError):
+        Topology.uniform(2, 8)
+    with pytest.raises(NotImplementedError):
+        Controller(_Spec(1, 8), [2, 2], 'ferry', Topology.uniform(1, 8))
+
+
+def test_host_gate_history_matches_oracle():
+    from ferry_amd.metadata import GateHistory
+    from ferry_amd.metadata import frequency_rows as rows_product
+    rng = np.random.default_rng(4)
+    L, E, W = 2, 24, 32
+    a, b = GateHistory(L, E, W), GateHistoryRef(L, E, W)
+    for step in range(40):
+        layer = step % L
+        T = int(rng.integers(1, 50))
+        sel = np.stack([rng.choice(E, 3, replace=False) for _ in range(T)])
+        assert np.array_equal(rows_product(sel, E, W), frequency_rows(sel, E, W))
+        a.update(layer, rows_product(sel, E, W))
+        b.update(layer, frequency_rows(sel, E, W))
+        assert np.array_equal(a.scores(layer), b.scores(layer))
+    # probability rows (the reference's Eq. 12 score) go through the same ring
+    p = rng.random((7, E)).astype(np.float32)
+    a.update(0, p)
+    b.update(0, p.astype(np.float64))
+    assert np.array_equal(a.scores(0), b.scores(0))
+
+
+def test_model_spec_cache_budget_and_read_spec(tmp_path):
+    import json
+    from ferry_amd.model import DEEPSEEK_V2_LITE, QWEN3_30B_A3B, read_spec
+    assert QWEN3_30B_A3B.cache_slots(0.30, 1) == [1843]
+    assert DEEPSEEK_V2_LITE.cache_slots(0.30, 1) == [499]
+    assert QWEN3_30B_A3B.expert_bytes == 9437184 and DEEPSEEK_V2_LITE.expert_bytes == 17301504
+    cfg = dict(model_type='qwen3_moe', num_hidden_layers=48, num_experts=128, num_experts_per_tok=8,
+               hidden_size=2048, moe_intermediate_size=768, decoder_sparse_step=1, mlp_only_layers=[])
+    (tmp_path / 'config.json').write_text(json.dumps(cfg))
+    assert read_spec(tmp_path) == QWEN3_30B_A3B
+    cfg = dict(model_type='deepseek_v2', num_hidden_layers=27, n_routed_experts=64, num_experts_per_tok=6,
+               hidden_size=2048, moe_intermediate_size=1408, first_k_dense_replace=1, moe_layer_freq=1)
+    (tmp_path / 'config.json').write_text(json.dumps(cfg))
+    assert read_spec(tmp_path) == DEEPSEEK_V2_LITE
+
+
+def test_workload_generators_are_seeded():
+    from ferry_amd import workloads
+    a = workloads.zipf_log_bias(128, 1.1, np.random.default_rng(1))
+    b = workloads.zipf_log_bias(128, 1.1, np.random.default_rng(1))
+    assert np.array_equal(a, b)
+    p = np.exp(a.astype(np.float64))
+    assert abs(p.sum() - 1) < 1e-5 and np.isclose(p.max() / p.min(), 128 ** 1.1, rtol=1e-3)
+    w = workloads.CONFIGS[5]
+    sel, logits = workloads.temporal_routing(w, steps=3, tokens=4, seed=0)
+    assert sel.shape == (3, 48, 4, 8)
+    for row in sel.reshape(-1, 8):
+        assert len(set(row.tolist())) == 8
+
+
+def test_bench_rejects_more_than_one_gpu():
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, str(ROOT / 'bench.py'), '--gpus', '2'], capture_output=True,
+                       text=True, timeout=300)
+    assert r.returncode == 2 and 'one GPU' in r.stdout

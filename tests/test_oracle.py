@@ -1,0 +1,280 @@
+"""CPU tier: the oracle pinned against libraries, closed forms, hand-derived answers and the
+committed golden fixtures (no GPU)."""
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.experts import (execute_experts_ref, moe_fp64, moe_layer_ref, reduce_partials_ref,
+                            silu_mul_ref)
+from oracle.history import GateHistoryRef, closed_form_scores, frequency_rows
+from oracle.layout import layout_closed_form, layout_loops
+from oracle.native import topk as emulated_topk
+from oracle.policy import PlannerRef, plan_layer_sorted
+from oracle.router import deepseek_router, qwen3_router
+
+GOLDEN = Path(__file__).resolve().parent / 'golden'
+
+
+# ---------------------------------------------------------------------------------------------
+# top-k restatement vs torch.topk on the CPU (the library the reference router calls)
+# ---------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize('n,k', [(128, 8), (64, 6), (128, 1), (16, 3), (300, 4), (4096, 8), (64, 32),
+                                 (128, 40), (8, 8), (256, 2)])
+@pytest.mark.parametrize('sorted_', [True, False])
+@pytest.mark.parametrize('quant', [None, 'bf16', 'coarse'])
+def test_topk_restatement_matches_torch(n, k, sorted_, quant):
+    rng = np.random.default_rng(n * 7 + k)
+    x = rng.standard_normal((400, n)).astype(np.float32)
+    if quant == 'bf16':
+        x = torch.from_numpy(x).bfloat16().float().numpy()
+    elif quant == 'coarse':
+        x = np.round(x * 4) / 4
+    p = torch.softmax(torch.from_numpy(x), -1)
+    for largest in (True, False):
+        tv, ti = torch.topk(p, k, largest=largest, sorted=sorted_)
+        ov, oi = emulated_topk(p.numpy(), k, largest, sorted_)
+        assert np.array_equal(ti.numpy(), oi)
+        assert np.array_equal(tv.numpy(), ov)
+
+
+def test_topk_nan_rows_match_torch():
+    x = torch.randn((64, 128))
+    x[::3, 5] = float('nan')
+    x[1::3] = float('nan')
+    for sorted_ in (True, False):
+        tv, ti = torch.topk(x, 8, sorted=sorted_)
+        _, oi = emulated_topk(x.numpy(), 8, True, sorted_)
+        assert np.array_equal(ti.numpy(), oi)
+
+
+def test_router_oracle_against_golden():
+    d = np.load(GOLDEN / 'topk_qwen3_bf16.npz')
+    logits = torch.from_numpy(d['logits']).view(torch.bfloat16)
+    w, idx, probs = qwen3_router(logits, int(d['k']))
+    assert np.array_equal(idx.numpy(), d['idx'])
+    assert np.array_equal(w.view(torch.int16).numpy(), d['w'])
+    _, oi = emulated_topk(probs.numpy(), int(d['k']), True, True)
+    assert np.array_equal(oi, d['idx'])
+    d = np.load(GOLDEN / 'topk_deepseek_fp32_unsorted.npz')
+    w, idx, probs = deepseek_router(torch.from_numpy(d['logits']), int(d['k']))
+    assert np.array_equal(idx.numpy(), d['idx'])
+    _, oi = emulated_topk(probs.numpy(), int(d['k']), True, False)
+    assert np.array_equal(oi, d['idx'])
+
+
+def test_router_renorm_closed_form():
+    logits = torch.randn((100, 128)).bfloat16()
+    w, idx, probs = qwen3_router(logits, 8)
+    top = torch.gather(probs, 1, idx)
+    torch.testing.assert_close(w.float(), (top / top.sum(-1, keepdim=True)), rtol=2 ** -8, atol=0)
+    # selection on logits = selection on probabilities (softmax is increasing)
+    assert torch.equal(torch.topk(logits.float(), 8).indices.sort(1).values, idx.sort(1).values)
+
+
+# ---------------------------------------------------------------------------------------------
+# history
+# ---------------------------------------------------------------------------------------------
+
+def test_fp32_division_equals_float64_mean_cast():
+    """score = float32(c / n) in fp32 equals the reference's float64 mean cast to float32."""
+    for n in range(1, 129):
+        c = np.arange(0, n + 1)
+        a = (c.astype(np.float64) / n).astype(np.float32)
+        b = c.astype(np.float32) / np.float32(n)
+        assert np.array_equal(a, b), n
+
+
+def test_history_ring_vs_closed_form():
+    rng = np.random.default_rng(3)
+    L, E, k, W = 3, 40, 5, 128
+    h = GateHistoryRef(L, E, W)
+    seen = [[] for _ in range(L)]
+    for step in range(80):
+        layer = step % L
+        T = int(rng.choice([1, 2, 16, 64, 127, 128, 129, 300]))
+        sel = np.stack([rng.choice(E, k, replace=False) for _ in range(T)])
+        h.update(layer, frequency_rows(sel, E, W))
+        seen[layer].extend(list(sel))
+        assert np.array_equal(h.scores(layer), closed_form_scores(seen[layer], E, W))
+
+
+def test_history_golden():
+    d = np.load(GOLDEN / 'history.npz')
+    L, E, k, W = int(d['layers']), int(d['experts']), int(d['topk']), int(d['window'])
+    h = GateHistoryRef(L, E, W)
+    off = 0
+    for i, T in enumerate(d['sizes']):
+        sel = d['selected'][off:off + T]
+        off += T
+        h.update(i % L, frequency_rows(sel, E, W))
+        assert np.array_equal(h.scores(i % L), d['scores'][i])
+
+
+def test_history_empty_scores_zero():
+    h = GateHistoryRef(1, 8, 128)
+    assert np.array_equal(h.scores(0), np.zeros(8, np.float32))
+
+
+# ---------------------------------------------------------------------------------------------
+# planner
+# ---------------------------------------------------------------------------------------------
+
+def test_planner_known_answer():
+    """Hand-derived trace (E = 4, two layers, three slots)."""
+    p = PlannerRef(2, 4, 3)
+    f, dest = p.plan(0, 0, np.array([[0, 1]]), np.array([.5, .5, 0, 0], np.float32))
+    assert f.tolist() == [[0, 0, 0], [0, 1, 1]] and dest.tolist() == [[0, 0]]
+    # first empty slot for key 6; then the min (score, last, key) over keys 0 and 1 -> key 0
+    f, _ = p.plan(1, 1, np.array([[2, 3]]), np.array([0, 0, .3, .3], np.float32))
+    assert f.tolist() == [[0, 6, 2], [0, 7, 0]]
+    # key 1 is protected (active in layer 0); keys 6 and 7 tie on (score, last) -> key 6
+    f, _ = p.plan(2, 0, np.array([[1, 2]]), np.array([0, .25, .75, 0], np.float32))
+    assert f.tolist() == [[0, 2, 2]]
+    assert p.slots.tolist() == [7, 1, 2]
+    assert p.last[[1, 2]].tolist() == [3, 3] and p.last[7] == 2
+    # LRU: equal scores, older last use is evicted (key 7 last=2 vs key 1 last=3)
+    f, _ = p.plan(3, 1, np.array([[0]]), np.array([0, 0, 0, 0], np.float32))
+    assert f.tolist() == [[0, 4, 0]]   # key 7 (score 0 now, last 2) < key 2 (score .75)
+
+
+def test_planner_scores_of_other_layers_are_stale():
+    """The eviction key uses the score last planned for the victim's own layer."""
+    p = PlannerRef(2, 2, 2)
+    p.plan(0, 0, np.array([[0]]), np.array([.9, 0], np.float32))
+    p.plan(1, 1, np.array([[0]]), np.array([.1, 0], np.float32))
+    # layer-0 key 0 keeps score .9, layer-1 key 2 has .1 -> evict key 2
+    f, _ = p.plan(2, 0, np.array([[1]]), np.array([.9, 0], np.float32))
+    assert f.tolist() == [[0, 1, 1]]
+
+
+def test_planner_overflow_asserts():
+    p = PlannerRef(1, 8, 2)
+    with pytest.raises(AssertionError):
+        p.plan(0, 0, np.array([[0, 1, 2]]), np.zeros(8, np.float32))
+    p = PlannerRef(1, 8, 3)
+    p.plan(0, 0, np.array([[0, 1, 2]]), np.zeros(8, np.float32))
+    with pytest.raises(AssertionError):   # all slots hold protected experts
+        p.plan(1, 0, np.array([[0, 1, 2, 3]]), np.zeros(8, np.float32))
+
+
+def test_planner_c_vs_sorted_formulation_random():
+    rng = np.random.default_rng(0)
+    for trial in range(20):
+        L, E = int(rng.integers(1, 4)), int(rng.integers(2, 20))
+        cap = int(rng.integers(1, 2 * E))
+        ref = PlannerRef(L, E, cap)
+        st = dict(slots=np.full(cap, -1, np.int64), owner=np.full(L * E, -1, np.int64),
+                  last=np.zeros(L * E, np.int64), scores=np.zeros((L, E), np.float32))
+        for ev in range(60):
+            layer = int(rng.integers(0, L))
+            k = int(rng.integers(1, min(E, 4) + 1))
+            T = int(rng.integers(1, 5))
+            sel = np.stack([rng.choice(E, k, replace=False) for _ in range(T)])
+            gs = (rng.integers(0, 3, E) / 2).astype(np.float32)
+            try:
+                f1, dest = ref.plan(ev, layer, sel, gs)
+            except AssertionError:
+                f1 = None
+            try:
+                f2 = plan_layer_sorted(st, ev, layer, sel, gs)
+            except AssertionError:
+                f2 = None
+            assert (f1 is None) == (f2 is None)
+            if f1 is None:
+                break
+            assert np.array_equal(f1, f2)
+            # invariants: misses ascending, every active expert resident, no duplicate keys
+            assert list(f1[:, 1]) == sorted(f1[:, 1])
+            live = ref.slots[ref.slots >= 0]
+            assert len(set(live.tolist())) == len(live)
+            for e in np.unique(sel):
+                assert layer * E + e in live
+            assert np.array_equal(dest, np.zeros_like(dest))
+
+
+def test_planner_golden_trace():
+    d = np.load(GOLDEN / 'planner.npz')
+    L, E, cap = int(d['layers']), int(d['experts']), int(d['cap'])
+    p = PlannerRef(L, E, cap)
+    off = foff = 0
+    for ev, T in enumerate(d['sizes']):
+        sel = d['selected'][off:off + T]
+        off += T
+        f, _ = p.plan(ev, ev % L, sel, d['gate_scores'][ev])
+        n = int(d['nfetch'][ev])
+        assert np.array_equal(f, d['fetches'][foff:foff + n])
+        foff += n
+    assert np.array_equal(p.slots, d['final_slots'])
+    assert np.array_equal(p.last, d['final_last'])
+
+
+# ---------------------------------------------------------------------------------------------
+# layout
+# ---------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize('T,E,k', [(1, 4, 1), (7, 8, 8), (100, 64, 6), (513, 128, 8)])
+def test_layout_closed_form_vs_loops(T, E, k):
+    rng = np.random.default_rng(T)
+    sel = np.stack([rng.choice(E, k, replace=False) for _ in range(T)])
+    a, b = layout_closed_form(sel, E), layout_loops(sel, E)
+    for key in ('send_ids', 'starts', 'rows', 'cols'):
+        assert np.array_equal(a[key], b[key])
+    # pair_pos is the inverse permutation
+    assert np.array_equal(a['rows'][a['pair_pos']], np.repeat(np.arange(T), k))
+
+
+def test_layout_golden():
+    d = np.load(GOLDEN / 'layout.npz')
+    a = layout_closed_form(d['selected'], int(d['experts']))
+    for key in ('send_ids', 'starts', 'rows', 'cols', 'pair_pos'):
+        assert np.array_equal(a[key], d[key])
+
+
+# ---------------------------------------------------------------------------------------------
+# expert FFN and combine
+# ---------------------------------------------------------------------------------------------
+
+def test_silu_mul_closed_form():
+    g = torch.tensor([0.0, 1.0, -1.0, 3.5]).bfloat16()
+    u = torch.tensor([2.0, 1.0, 1.0, -2.0]).bfloat16()
+    want = torch.tensor([0.0, 1 / (1 + np.exp(-1)), -1 / (1 + np.exp(1)), -7.0 / (1 + np.exp(-3.5))])
+    torch.testing.assert_close(silu_mul_ref(g, u).float(), want.float(), rtol=2 ** -8, atol=0)
+
+
+def test_moe_oracle_vs_fp64():
+    g = torch.Generator().manual_seed(1)
+    T, E, k, H, I = 40, 8, 2, 64, 32
+    rows_w = (torch.randn((E, 3 * H * I), generator=g) * 0.05).bfloat16()
+    x = torch.randn((T, H), generator=g).bfloat16()
+    logits = torch.randn((T, E), generator=g).bfloat16()
+    w, sel, _ = qwen3_router(logits, k)
+    out = moe_layer_ref(lambda e: rows_w[e], x, sel, w, E, H, I).float()
+    exact = moe_fp64(lambda e: rows_w[e], x, sel, w, H, I).float()
+    torch.testing.assert_close(out, exact, rtol=2e-2, atol=1e-2)
+
+
+def test_reduce_partials_is_ascending_fp32_sum():
+    g = torch.Generator().manual_seed(2)
+    parts = [torch.randn((3, 8), generator=g).bfloat16() for _ in range(3)]
+    rows = [torch.tensor([0, 2, 4]), torch.tensor([2, 3, 4]), torch.tensor([4, 0, 1])]
+    got = reduce_partials_ref(parts, rows, 5, 8)
+    acc = torch.zeros((5, 8))
+    for p, r in zip(parts, rows):
+        for i, t in enumerate(r.tolist()):
+            acc[t] += p[i].float()
+    assert torch.equal(got, acc.bfloat16())
+
+
+def test_execute_experts_ref_weights_rows_cols():
+    g = torch.Generator().manual_seed(3)
+    H, I = 32, 16
+    row = (torch.randn(3 * H * I, generator=g) * 0.1).bfloat16()
+    x = torch.randn((4, H), generator=g).bfloat16()
+    rw = torch.tensor([[0.5, 0.25], [1.0, 2.0], [0.0, 1.0], [1.0, 1.0]]).bfloat16()
+    r, c = torch.tensor([1, 3]), torch.tensor([1, 0])
+    out = execute_experts_ref([row], x, rw, [r], [c], H, I)[0]
+    unit = execute_experts_ref([row], x, torch.ones_like(rw), [r], [c], H, I)[0]
+    torch.testing.assert_close(out.float(), (unit.float() * torch.tensor([[2.0], [1.0]])).bfloat16().float())
