@@ -20,6 +20,8 @@
 // Phase 1 ("up") computes the gate and up projections together and applies silu(g)*u in the
 // epilogue; phase 2 ("down") applies the routing weight in the epilogue and writes the
 // per-(token, expert) row that the combine kernel sums.
+#include <type_traits>
+
 #include "common.h"
 
 namespace ferry {
@@ -264,12 +266,23 @@ __global__ __launch_bounds__(256) void ffn_down_skinny(FfnArgs a) {
 // Tiled kernels
 // =============================================================================================
 
-// Output tile 256 x 256 per workgroup, K step 64, four wavefronts of 128 x 128 (2 x 2), each a
-// 4 x 4 grid of 32x32 MFMA accumulators (256 fp32 per lane, held in AGPRs).  Phase 1's 256 B rows
-// are 128 gate rows and the 128 up rows of the same intermediate columns, so every wavefront
-// owns matching gate/up accumulators and the SwiGLU runs in registers.
-constexpr int BM = 256, BN = 256, BK = 64, LDK = BK + 8;  // +8 bf16 of padding per LDS row
-constexpr int kTileLds = 2 * (BM + BN) * LDK;               // bf16 elements (double buffer)
+// Output tile 256 x 256 per workgroup, four wavefronts of 128 x 128 (2 x 2), each a 4 x 4 grid
+// of 32x32 MFMA accumulators (256 fp32 per lane, in AGPRs).  Phase 1's 256 B rows are 128 gate
+// rows and the 128 up rows of the same intermediate columns, so every wavefront owns matching
+// gate/up accumulators and the SwiGLU runs in registers.
+//
+// Operand staging: global -> LDS direct loads (global_load_lds_dwordx4, no VGPR round trip).
+// A stage holds BK = 64 columns of K: 256 A rows and 256 B rows of 128 bytes.  One direct
+// load moves 8 full rows (64 lanes x 16 B, lane l -> row l / 8, LDS slot l % 8), which keeps
+// the global side fully coalesced.  Inside a row the 16-byte chunk c is stored at slot
+// c ^ ((row >> 1) & 7): the MFMA fragment read (32 rows x one chunk per half-wavefront) then
+// touches 16 distinct 16-byte bank groups in every 16 lanes, i.e. no LDS bank conflicts.
+// Two stages (2 x 64 KiB): the loads of stage kt+1 run while stage kt is multiplied.
+constexpr int BM = 256, BN = 256, BK = 64, STAGES = 2;
+constexpr int kRowBytes = BK * 2;                                // 128
+constexpr int kOperandBytes = 256 * kRowBytes;                   // 32 KiB per operand tile
+constexpr int kStageBytes = 2 * kOperandBytes;                   // A then B
+constexpr int kTileLds = STAGES * kStageBytes / 2;               // bf16 elements (128 KiB)
 
 struct TileTable {
   int32_t cum[kListMax + 1];  // cumulative M tiles over list entries
@@ -327,6 +340,34 @@ __device__ __forceinline__ int find_entry(const TileTable& tt, int m) {
   return lo;
 }
 
+// wait until at most N of this wavefront's vector-memory operations are outstanding
+__device__ __forceinline__ void wait_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+typedef __attribute__((address_space(3))) char lds_char;
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(lds_char*)p;
+}
+// LDS fragment read issued as inline asm: the compiler cannot see that it reads memory that
+// the in-flight direct loads write, so it does not insert a vmcnt(0) drain in front of it.
+// Completion is awaited explicitly with lds_wait, which also ties the fragment registers.
+template <int OFF>
+__device__ __forceinline__ void ds_read16(bf16x8& v, uint32_t addr) {
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
+}
+__device__ __forceinline__ void lds_wait(bf16x8 (&a)[4], bf16x8 (&b)[4]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]),
+                 "+v"(b[2]), "+v"(b[3])
+               :
+               : "memory");
+}
+// workgroup barrier without the release/acquire fence of __syncthreads (which would drain
+// the direct loads of the later stages); LDS visibility is established by the explicit waits
+__device__ __forceinline__ void wg_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
 // MODE 0: A = gathered x rows (K = H); B rows 0..127 = Wg[i0 ..], 128..255 = Wu[i0 ..];
 //         epilogue act[p, i0 + c] = bf16(silu(bf16(g)) * bf16(u)).
 // MODE 1: A = activation rows (K = I); B rows = Wd[h0 ..];
@@ -334,7 +375,7 @@ __device__ __forceinline__ int find_entry(const TileTable& tt, int m) {
 template <int MODE>
 __global__ __launch_bounds__(256, 1) void ffn_tiled(FfnArgs a) {
   __shared__ TileTable tt;
-  __shared__ __attribute__((aligned(16))) bf16_t smem[kTileLds];
+  __shared__ __attribute__((aligned(1024))) bf16_t smem[kTileLds];
   __shared__ int64_t orow_s[BM];
   __shared__ float wt_s[BM];
   build_tile_table(a, tt);
@@ -345,11 +386,14 @@ __global__ __launch_bounds__(256, 1) void ffn_tiled(FfnArgs a) {
   const int wm = wave >> 1, wn = wave & 1;
   const int KT = (int)(K / BK);
   const int l32 = lane & 31, kh = (lane >> 5) * 8;
-  bf16_t* As = smem;                 // [2][BM][LDK]
-  bf16_t* Bs = smem + 2 * BM * LDK;  // [2][BN][LDK]
 
-  for (int tile = blockIdx.x; tile < total; tile += gridDim.x) {
-    // tiles of one expert are consecutive, N fastest: consecutive workgroups share A rows
+  // XCD-aware order: workgroup b runs on XCD b % 8 (round-robin dispatch), so in each round
+  // of gridDim tiles the workgroups of one XCD take a contiguous run of tiles.  Tiles of one
+  // expert are consecutive with N fastest, so a run covers a compact block of M x N tiles whose
+  // A and B slices are shared in that XCD's L2.
+  const int per_xcd = gridDim.x % 8 == 0 ? (int)gridDim.x / 8 : 0;
+  const int lslot = per_xcd ? (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+  for (int tile = lslot; tile < total; tile += gridDim.x) {
     const int mt_global = tile / ntn, ntile = tile % ntn;
     const int li = find_entry(tt, mt_global);
     const int e = a.list.expert[li];
@@ -358,30 +402,51 @@ __global__ __launch_bounds__(256, 1) void ffn_tiled(FfnArgs a) {
     const int m0 = (mt_global - tt.cum[li]) * BM;
     const bf16_t* slot = a.cache + (int64_t)a.list.slot[li] * 3 * a.H * a.I;
 
-    // global load descriptors: thread owns 16-byte chunk kc of rows tid/8 + 32*q, q < 8.
-    // A rows are element offsets (32-bit) from a.x / a.act, B rows are affine in q.
-    const int lrow = tid >> 3, lkc = (tid & 7) * 8;
-    uint32_t aoff[8];
-    uint32_t amask = 0;
+    // Direct loads: this wavefront moves tile rows 64*wave + 8*q + lane/8 (q < 8) of A and of
+    // B, lane slot lane % 8 holding chunk (lane % 8) ^ ((row >> 1) & 7).  Rows past the
+    // expert's last row load a valid row instead: each output row depends only on its own A
+    // row, and those rows are never stored.
+    const int r8 = lane >> 3, slot8 = lane & 7;
+    uint32_t aoff[8];                    // element offsets of the A rows (+ chunk)
+    const bf16_t* abase = MODE == 0 ? a.x : a.act;
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
-      const int r = m0 + lrow + 32 * q;
+      const int row = 64 * wave + 8 * q + r8;
+      const int chunk = slot8 ^ ((row >> 1) & 7);
+      const int r = m0 + row;
       const bool ok = r < n;
-      amask |= ok ? (1u << q) : 0u;
       if (MODE == 0) {
-        const int64_t t = ok ? a.rows[start + r] : 0;
-        aoff[q] = (uint32_t)(t * a.H + lkc);
+        const int64_t t = a.rows[start + (ok ? r : 0)];
+        aoff[q] = (uint32_t)(t * a.H + chunk * 8);
       } else {
-        aoff[q] = (uint32_t)((start + (ok ? r : 0)) * a.I + lkc);
+        aoff[q] = (uint32_t)((start + (ok ? r : 0)) * a.I + chunk * 8);
       }
     }
-    const bf16_t* abase = MODE == 0 ? a.x : a.act;
+    // B rows of this wavefront: 64*wave .. +64 (MODE 0: waves 0, 1 gate rows, 2, 3 up rows)
     const int64_t ldb = MODE == 0 ? a.H : a.I;
-    // MODE 0: rows lrow + 32q, q < 4 gate, q >= 4 the matching up rows (offset H*I - 128 rows)
-    const bf16_t* gb = MODE == 0 ? slot + (int64_t)(ntile * 128 + lrow) * a.H + lkc
-                                 : slot + 2 * a.H * a.I + (int64_t)(ntile * BN + lrow) * a.I + lkc;
-    const int64_t bstep = 32 * ldb;                                   // next 32 rows
-    const int64_t bjump = MODE == 0 ? a.H * a.I - 4 * bstep : 0;       // gate -> up block
+    const int brow0 = 64 * wave;
+    const bf16_t* bbase =
+        MODE == 0 ? slot + (brow0 < 128 ? (int64_t)(ntile * 128 + brow0) * a.H
+                                        : a.H * a.I + (int64_t)(ntile * 128 + brow0 - 128) * a.H)
+                  : slot + 2 * a.H * a.I + (int64_t)(ntile * BN + brow0) * a.I;
+    uint32_t boff[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int row = brow0 + 8 * q + r8;
+      boff[q] = (uint32_t)((8 * q + r8) * ldb + (slot8 ^ ((row >> 1) & 7)) * 8);
+    }
+    auto issue = [&](int kt) {
+      bf16_t* st = smem + (kt % STAGES) * (kStageBytes / 2);
+      const int k0 = kt * BK;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        __builtin_amdgcn_global_load_lds(abase + aoff[q] + k0, st + (64 * wave + 8 * q) * (kRowBytes / 2),
+                                         16, 0, 0);
+        __builtin_amdgcn_global_load_lds(bbase + boff[q] + k0,
+                                         st + kOperandBytes / 2 + (64 * wave + 8 * q) * (kRowBytes / 2),
+                                         16, 0, 0);
+      }
+    };
     if (MODE == 1) {
       // per-row output row and routing weight for the epilogue
       for (int r = tid; r < BM; r += 256) {
@@ -399,30 +464,6 @@ __global__ __launch_bounds__(256, 1) void ffn_tiled(FfnArgs a) {
       }
     }
 
-    u32x4 ra[8], rb[8];
-    const u32x4 z4 = {0, 0, 0, 0};
-    auto gload = [&](int kt) {
-      const int koff = kt * BK;
-#pragma unroll
-      for (int q = 0; q < 8; ++q)
-        ra[q] = (amask >> q) & 1u ? *reinterpret_cast<const u32x4*>(abase + aoff[q] + koff) : z4;
-      const bf16_t* b = gb + koff;
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        rb[q] = *reinterpret_cast<const u32x4*>(b);
-        b += (q == 3) ? bstep + bjump : bstep;
-      }
-    };
-    auto lstore = [&](int buf) {
-      bf16_t* as = As + buf * BM * LDK;
-      bf16_t* bs = Bs + buf * BN * LDK;
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        *reinterpret_cast<u32x4*>(&as[(lrow + 32 * q) * LDK + lkc]) = ra[q];
-        *reinterpret_cast<u32x4*>(&bs[(lrow + 32 * q) * LDK + lkc]) = rb[q];
-      }
-    };
-
     floatx16 acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -431,78 +472,127 @@ __global__ __launch_bounds__(256, 1) void ffn_tiled(FfnArgs a) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-    // B sub-tiles of this wavefront.  MODE 0: j = 0, 1 gate rows wn*64 + 32j; j = 2, 3 the
-    // matching up rows 128 + wn*64 + 32(j-2).  MODE 1: rows wn*128 + 32j.
-    int brow[4];
+    // Fragment addresses.  Lane l reads row (first row of the fragment) + l % 32, chunk
+    // 2*sub + l / 32, at byte row*128 + ((chunk ^ ((row >> 1) & 7)) << 4); fragment rows are
+    // multiples of 32 apart, so the swizzle term only depends on the lane and the sub-step.
+    // A fragments i: rows wm*128 + 32 i.  B fragments j: MODE 0 gate rows wn*64 + 32 j (j < 2)
+    // and up rows 128 + wn*64 + 32 (j - 2); MODE 1 rows wn*128 + 32 j.
+    const uint32_t smem_base = lds_addr(smem);
+    const int swz = (l32 >> 1) & 7, half = lane >> 5;
+    uint32_t a_addr[4], b_addr[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      brow[j] = MODE == 0 ? (j < 2 ? wn * 64 + 32 * j : 128 + wn * 64 + 32 * (j - 2))
-                          : wn * 128 + 32 * j;
-
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    for (int kt = 0; kt < KT; ++kt) {
-      const int buf = kt & 1;
-      if (kt + 1 < KT) gload(kt + 1);
-      const bf16_t* as = As + buf * BM * LDK;
-      const bf16_t* bs = Bs + buf * BN * LDK;
+    for (int sub = 0; sub < 4; ++sub) {
+      const uint32_t slotb = (uint32_t)((((2 * sub + half) ^ swz)) << 4);
+      a_addr[sub] = smem_base + (uint32_t)((wm * 128 + l32) * kRowBytes) + slotb;
+      b_addr[sub] = smem_base + kOperandBytes + (uint32_t)(((MODE == 0 ? wn * 64 : wn * 128) + l32) * kRowBytes) + slotb;
+    }
+    auto rd = [&](int kt, int sub, bf16x8 (&fa)[4], bf16x8 (&fb)[4]) {
+      const uint32_t so = (uint32_t)((kt % STAGES) * kStageBytes);
+      const uint32_t ab = a_addr[sub] + so, bb = b_addr[sub] + so;
+      ds_read16<0 * 4096>(fa[0], ab);
+      ds_read16<1 * 4096>(fa[1], ab);
+      ds_read16<2 * 4096>(fa[2], ab);
+      ds_read16<3 * 4096>(fa[3], ab);
+      if constexpr (MODE == 0) {
+        ds_read16<0>(fb[0], bb);
+        ds_read16<4096>(fb[1], bb);
+        ds_read16<16384>(fb[2], bb);
+        ds_read16<16384 + 4096>(fb[3], bb);
+      } else {
+        ds_read16<0 * 4096>(fb[0], bb);
+        ds_read16<1 * 4096>(fb[1], bb);
+        ds_read16<2 * 4096>(fb[2], bb);
+        ds_read16<3 * 4096>(fb[3], bb);
+      }
+    };
+    auto mma = [&](const bf16x8 (&fa)[4], const bf16x8 (&fb)[4]) {
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int kk = 0; kk < BK; kk += 16) {
-        bf16x8 af[4], bfr[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          af[i] = *reinterpret_cast<const bf16x8*>(&as[(wm * 128 + i * 32 + l32) * LDK + kk + kh]);
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          bfr[j] = *reinterpret_cast<const bf16x8*>(&bs[(brow[j] + l32) * LDK + kk + kh]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
-      }
-      if (kt + 1 < KT) lstore(buf ^ 1);
-      __syncthreads();
-    }
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    };
 
-    // epilogue: bf16 tile staged in LDS, then 16-byte row stores.
-    // 32x32 accumulator layout: column = lane & 31, row(v) = (v/4)*8 + (lane/32)*4 + v%4
+    // pipeline: stage kt+1 streams in while stage kt is multiplied; the fragments of the next
+    // sub-step are read while the MFMAs of the current one run
+    bf16x8 f0a[4], f0b[4], f1a[4], f1b[4];
+    issue(0);
+    wait_vmcnt0();
+    wg_barrier();
+    if (1 < KT) issue(1);
+    rd(0, 0, f0a, f0b);
+    lds_wait(f0a, f0b);
+    for (int kt = 0; kt < KT; ++kt) {
+      rd(kt, 1, f1a, f1b);
+      mma(f0a, f0b);
+      lds_wait(f1a, f1b);
+      rd(kt, 2, f0a, f0b);
+      mma(f1a, f1b);
+      lds_wait(f0a, f0b);
+      rd(kt, 3, f1a, f1b);
+      mma(f0a, f0b);
+      lds_wait(f1a, f1b);  // stage kt fully read by this wavefront
+      const bool more = kt + 1 < KT;
+      if (more) {
+        wait_vmcnt0();   // this wavefront's loads of stage kt+1 landed
+        wg_barrier();    // ... everyone's; and stage kt is no longer read by anyone
+        if (kt + 2 < KT) issue(kt + 2);
+        rd(kt + 1, 0, f0a, f0b);
+      }
+      mma(f1a, f1b);
+      if (more) lds_wait(f0a, f0b);
+    }
+    __syncthreads();  // all fragment reads done before the staging area is reused
+
+    // epilogue: bf16 tile staged in LDS (in two halves of 128 rows for phase 2), then
+    // 16-byte row stores.  32x32 accumulator layout: column = lane & 31,
+    // row(v) = (v / 4) * 8 + (lane / 32) * 4 + v % 4.
     constexpr int OC = MODE == 0 ? 128 : 256;  // output columns of the tile
     constexpr int OLD = OC + 8;
+    constexpr int HALVES = MODE == 0 ? 1 : 2;
+    constexpr int HROWS = BM / HALVES;
+    constexpr int CPR = OC / 8;  // 16-byte chunks per row
     bf16_t* os = smem;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int half = 0; half < HALVES; ++half) {
+      if (HALVES == 1 || wm == half) {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int r = wm * 128 + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-        if (MODE == 0) {
+        for (int i = 0; i < 4; ++i) {
 #pragma unroll
-          for (int jg = 0; jg < 2; ++jg) {
-            const float g = bf16r(acc[i][jg][v]), u = bf16r(acc[i][jg + 2][v]);
-            os[r * OLD + wn * 64 + jg * 32 + l32] = f32_to_bf16(silu_mul(g, u));
+          for (int v = 0; v < 16; ++v) {
+            const int r = wm * 128 + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+            const int rs = r - half * HROWS;
+            if (MODE == 0) {
+#pragma unroll
+              for (int jg = 0; jg < 2; ++jg) {
+                const float g = bf16r(acc[i][jg][v]), u = bf16r(acc[i][jg + 2][v]);
+                os[rs * OLD + wn * 64 + jg * 32 + l32] = f32_to_bf16(silu_mul(g, u));
+              }
+            } else {
+              const float wt = wt_s[r];
+#pragma unroll
+              for (int j = 0; j < 4; ++j)
+                os[rs * OLD + wn * 128 + j * 32 + l32] = f32_to_bf16(bf16r(acc[i][j][v]) * wt);
+            }
           }
-        } else {
-          const float wt = wt_s[r];
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            os[r * OLD + wn * 128 + j * 32 + l32] = f32_to_bf16(bf16r(acc[i][j][v]) * wt);
         }
       }
-    }
-    __syncthreads();
-    constexpr int CPR = OC / 8;  // 16-byte chunks per row
-    for (int c = tid; c < BM * CPR; c += 256) {
-      const int r = c / CPR, cc = (c % CPR) * 8;
-      if (m0 + r >= n) continue;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(&os[r * OLD + cc]);
-      if (MODE == 0) {
-        *reinterpret_cast<u32x4*>(&a.act[(start + m0 + r) * a.I + ntile * 128 + cc]) = v;
-      } else {
-        *reinterpret_cast<u32x4*>(&a.out[orow_s[r] * a.H + ntile * BN + cc]) = v;
+      __syncthreads();
+      for (int c = tid; c < HROWS * CPR; c += 256) {
+        const int rs = c / CPR, cc = (c % CPR) * 8;
+        const int r = rs + half * HROWS;
+        if (m0 + r >= n) continue;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(&os[rs * OLD + cc]);
+        if (MODE == 0) {
+          *reinterpret_cast<u32x4*>(&a.act[(start + m0 + r) * a.I + ntile * 128 + cc]) = v;
+        } else {
+          *reinterpret_cast<u32x4*>(&a.out[orow_s[r] * a.H + ntile * BN + cc]) = v;
+        }
       }
+      __syncthreads();
     }
-    __syncthreads();
   }
 }
 
