@@ -36,6 +36,21 @@ BF16_PEAK_TFLOPS = 2500.0
 PCIE_PEAK_GBS = 64.0
 
 
+TRAFFIC_PROFILE = ROOT / 'profiles' / 'ffn_up_skinny_decode_qwen3_t16_hbm_traffic.md'
+
+
+def traffic_ratio():
+    """HBM traffic / algorithmic bytes of ffn_up_skinny, from the committed counter profile
+    (FETCH_SIZE + WRITE_SIZE, each scaled by a copy kernel of known size), or None."""
+    try:
+        for line in TRAFFIC_PROFILE.read_text().splitlines():
+            if line.startswith('traffic_over_algorithmic'):
+                return float(line.split('=')[1])
+    except OSError:
+        pass
+    return None
+
+
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument('--gpus', type=int, default=1)
@@ -45,6 +60,10 @@ def parse():
     p.add_argument('--no-prefill', action='store_true')
     p.add_argument('--no-cpu-baseline', action='store_true')
     p.add_argument('--cpu-seconds', type=float, default=15.0)
+    p.add_argument('--copy-calibration-mib', type=int, default=0,
+                   help='run one plain device copy kernel of this many MiB (read and written) '
+                        'before the decode loop: the reference dispatch for scaling HBM byte '
+                        'counters (FETCH_SIZE / WRITE_SIZE) in profiler runs')
     return p.parse_args()
 
 
@@ -201,11 +220,19 @@ def cpu_baseline(dec, seconds):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps(dict(error='this build runs one GPU per process; --gpus must be 1 '
+        print(json.dumps(dict(error='ferry_amd runs on one GPU per process; --gpus must be 1 '
                                     '(multi-GPU expert parallelism is out of scope)')))
         sys.exit(2)
     torch.cuda.set_device(0)
     device = torch.device('cuda', 0)
+    if args.copy_calibration_mib:
+        n = args.copy_calibration_mib << 18   # int32 words
+        src = torch.zeros(n, dtype=torch.int32, device=device)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        torch.bitwise_not(src, out=dst)       # reads n*4 bytes, writes n*4 bytes
+        torch.cuda.synchronize()
+        del src, dst
     dec = run_decode(args, device)
     w = dec['workload']
     ks = dec['kernels']
@@ -217,6 +244,8 @@ def main():
     h2d_gbs = fetch_bytes / (dec['fetch_ms'] * 1e-3) / 1e9 if dec['fetch_ms'] else None
     hidden = 1.0 - dec['exposed_ms'] / dec['fetch_ms'] if dec['fetch_ms'] else None
     compute_ms = ks['up_ms'] + ks['down_ms']
+    ratio = traffic_ratio()
+    bytes_per_launch = ks['up'] / max(1, ks['up_launches'])
     line = dict(
         metric='MoE-layer tokens/sec (Qwen3-30B-A3B-shaped decode layer, 16 tok/step, 38/128 cached)',
         value=value, unit='tokens/s', n_gpus=1, steps=args.steps, warmup=args.warmup,
@@ -228,9 +257,12 @@ def main():
                     parallelism='single GPU (one expert-parallel share)'),
         roofline=dict(kernel='ffn_up_skinny (decode gate/up + SwiGLU)', bound='hbm',
                       achieved=up_gbs, peak=HBM_PEAK_GBS, unit='GB/s', frac=up_gbs / HBM_PEAK_GBS,
-                      traffic=None, launches=ks['up_launches'],
+                      traffic=bytes_per_launch * ratio if ratio else None,
+                      traffic_over_algorithmic=ratio,
+                      traffic_source=TRAFFIC_PROFILE.name if ratio else None,
+                      launches=ks['up_launches'],
                       avg_launch_us=ks['up_ms'] / max(1, ks['up_launches']) * 1e3,
-                      bytes_per_launch=ks['up'] / max(1, ks['up_launches'])),
+                      bytes_per_launch=bytes_per_launch),
         decode=dict(ffn_down_gbs=down_gbs, ffn_gbs=ffn_gbs, ffn_frac=ffn_gbs / HBM_PEAK_GBS,
                     ffn_ms_per_step=compute_ms / args.steps,
                     active_experts_per_step=ks['experts'] / args.steps,

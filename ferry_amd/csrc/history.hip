@@ -2,7 +2,7 @@
 // host planner copies back.
 //
 // Reference: ferry/metadata.py:15-38 (GateHistory) fed by RouteGather.collect at world = 1
-// (ferry/metadata.py:169-176): the history rows of a layer call are the one-hot selection
+// (ferry/metadata.py:67-83): the history rows of a layer call are the one-hot selection
 // indicators of its last min(T, ceil(W / world)) tokens; a batch of >= W rows replaces the
 // window, a shorter one is appended ring-wise; scores = float32(sum(rows) / max(1, count)).
 // Because rows are 0/1, the window sum is the integer count c_e of the last n = min(W, seen)

@@ -19,14 +19,14 @@ def device_layout(selected, destinations, tokens_per_rank, rank, experts, slot_o
     ``layout`` object that the fused path consumes.
     """
     if rank != 0:
-        raise NotImplementedError('this build runs one GPU (world = 1)')
+        raise NotImplementedError('ferry_amd runs on one GPU (world = 1)')
     if isinstance(selected, torch.Tensor):
         sel = selected.to('cuda', torch.int64).contiguous()
     else:
         sel = torch.from_numpy(np.ascontiguousarray(selected, dtype=np.int64)).to('cuda')
     T, k = sel.shape
     if T != tokens_per_rank:
-        raise NotImplementedError('this build runs one GPU (world = 1)')
+        raise NotImplementedError('ferry_amd runs on one GPU (world = 1)')
     if destinations is not None and np.any(np.asarray(destinations) != 0):
         raise AssertionError('expert scheduled on this rank is not cached here')
     lay = ops.layout(sel, weights, experts)

@@ -56,7 +56,7 @@ class DeviceGateHistory:
 
 
 def frequency_rows(expert_ids, experts, window, world=1):
-    """One-hot history rows of the last ceil(W / world) tokens (metadata.py:148-176, world = 1)."""
+    """One-hot history rows of the last ceil(W / world) tokens (metadata.py:55-83, world = 1)."""
     ids = np.asarray(expert_ids, np.int64)
     tail = min(len(ids), -(-window // world))
     recent = ids[len(ids) - tail:]
@@ -67,7 +67,7 @@ def frequency_rows(expert_ids, experts, window, world=1):
 
 
 class RouteGather:
-    """World-1 route gather: the D2H copy of the expert IDs (metadata.py:134-176).
+    """World-1 route gather: the D2H copy of the expert IDs (metadata.py:41-83).
 
     The all-gather is the identity at world = 1; ``collect`` returns (expert_ids int64 [T, k],
     origins int64 [T] (all 0), history rows).  The fused runtime path uses the device history

@@ -24,7 +24,7 @@ def _choose_slot(rank, layer, active, slots, capacities, last, scores, experts):
     """Step 4: an empty slot, else the lowest eviction score, then least-recently used
     (ferry/policy.py:109-127)."""
     if rank != 0 or len(capacities) != 1:
-        raise NotImplementedError('this build runs one GPU (world = 1)')
+        raise NotImplementedError('ferry_amd runs on one GPU (world = 1)')
     act = np.ascontiguousarray(active, dtype=np.uint8)
     row = np.ascontiguousarray(slots[rank], dtype=np.int64)
     return int(lib().ferry_choose_slot(layer, act.ctypes.data, row.ctypes.data, int(capacities[rank]),
@@ -38,7 +38,7 @@ def plan_layer(event, layer, selected, origins, gate_scores, policy, slots, capa
     Returns fetches[m, 3] = (rank, key, slot), destinations [T, k] and per-rank fetch counts.
     """
     if len(capacities) != 1:
-        raise NotImplementedError('this build runs one GPU (world = 1)')
+        raise NotImplementedError('ferry_amd runs on one GPU (world = 1)')
     sel = np.ascontiguousarray(selected, dtype=np.int64)
     tokens, topk = sel.shape
     experts = scores.shape[1]
@@ -72,7 +72,7 @@ class Controller:
         self.policy = POLICIES[policy]
         self.capacities = np.asarray(capacities, np.int64)
         if len(self.capacities) != 1:
-            raise NotImplementedError('this build runs one GPU (world = 1)')
+            raise NotImplementedError('ferry_amd runs on one GPU (world = 1)')
         self.balance_tol_bps = int(balance_tol_bps)
         self.salt = int(salt)
         self.masks, self.seconds, self.lut = topology.masks, topology.seconds, topology.lut

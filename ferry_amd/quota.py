@@ -19,7 +19,7 @@ class Topology:
         if data['world'] != world:
             raise ValueError(f"topology file is for {data['world']} GPUs, runtime has {world}")
         if world != 1:
-            raise NotImplementedError('this build runs one GPU (world = 1)')
+            raise NotImplementedError('ferry_amd runs on one GPU (world = 1)')
         self.masks = np.asarray([d['mask'] for d in data['domains']], np.int64)
         self.seconds = np.asarray([1.0 / d['gib_per_s'] for d in data['domains']], np.float64)
         self.lut = np.asarray(data['quota_lut'], np.int64)
@@ -31,7 +31,7 @@ class Topology:
     @classmethod
     def uniform(cls, world, experts):
         if world != 1:
-            raise NotImplementedError('this build runs one GPU (world = 1)')
+            raise NotImplementedError('ferry_amd runs on one GPU (world = 1)')
         self = cls.__new__(cls)
         self.masks = np.asarray([1], np.int64)
         self.seconds = np.ones(1, np.float64)

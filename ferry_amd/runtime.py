@@ -36,9 +36,9 @@ class OffloadRuntime:
                  balance_tol_bps=200, salt=1, eviction_score='frequency', overlap=True,
                  timing=False):
         if dist.is_available() and dist.is_initialized() and dist.get_world_size() != 1:
-            raise NotImplementedError('this build runs one GPU (world = 1)')
+            raise NotImplementedError('ferry_amd runs on one GPU (world = 1)')
         if len(capacities) != 1:
-            raise NotImplementedError('this build runs one GPU (world = 1)')
+            raise NotImplementedError('ferry_amd runs on one GPU (world = 1)')
         self.spec = spec
         self.pool = pool
         self.rank, self.world = 0, 1

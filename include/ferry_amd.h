@@ -93,7 +93,7 @@ int ferry_combine(const void* part, const int32_t* pair_pos, int64_t tokens, int
 
 /*
  * Selection-frequency history on the device.  Replaces ferry/metadata.py:15-38 (GateHistory
- * update/scores over one-hot rows built by RouteGather.collect, ferry/metadata.py:169-176).
+ * update/scores over one-hot rows built by RouteGather.collect, ferry/metadata.py:67-83).
  * State per layer (device memory, caller-owned, zero-initialised):
  *   ring[L, W, k] int32, counts[L, E] int32, meta[L, 2] int32 (count, head).
  * Update with the last min(T, W) tokens of selected[T, k]; then scores_out[E] =

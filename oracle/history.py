@@ -1,7 +1,7 @@
 """GateHistory oracle (test infrastructure).
 
 Restates ferry/metadata.py:15-38 (the ring of W float64 rows per layer) and the frequency
-rows of RouteGather.collect at world = 1 (ferry/metadata.py:169-176), plus the closed form the
+rows of RouteGather.collect at world = 1 (ferry/metadata.py:67-83), plus the closed form the
 device counters implement.
 """
 import numpy as np
@@ -34,7 +34,7 @@ class GateHistoryRef:
 
 
 def frequency_rows(expert_ids, experts, window, world=1):
-    """One-hot rows of the last min(T, ceil(W / world)) tokens (metadata.py:150, :173-175)."""
+    """One-hot rows of the last min(T, ceil(W / world)) tokens (metadata.py:57, :80-82)."""
     ids = np.asarray(expert_ids, np.int64)
     tail = min(len(ids), -(-window // world))
     recent = ids[len(ids) - tail:]
