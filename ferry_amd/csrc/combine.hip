@@ -6,6 +6,11 @@
 // round trip of that bf16 tensor, i.e. the identity.  A token's k entries are stored in
 // ascending-ID order, so summing j = 0..k-1 reproduces the reference order exactly.
 //
+// DeepSeek-V2 adds the shared experts' bf16 output to the routed bf16 output
+// (transformers modeling_deepseek_v2.py:136, `hidden_states + self.shared_experts(residuals)`):
+// with `addend` the bf16 combine result is added to it in fp32 and rounded again, which is
+// torch's bf16 addition.
+//
 // One block per token row chunk: each thread owns 8 consecutive hidden elements (one 16-byte
 // load per entry), so a token row of H = 2048 is one 256-thread block.
 #include "common.h"
@@ -20,6 +25,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 __global__ __launch_bounds__(kThreads) void combine_kernel(const bf16_t* __restrict__ part,
                                                            const int32_t* __restrict__ pair_pos,
+                                                           const bf16_t* __restrict__ addend,
                                                            int64_t tokens, int k, int64_t H,
                                                            bf16_t* __restrict__ out) {
   const int64_t chunks_per_row = H / kVec;
@@ -41,6 +47,14 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(const bf16_t* __restr
         acc[2 * i + 1] += bf16_to_f32((bf16_t)(v[i] >> 16));
       }
     }
+    if (addend) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(addend + t * H + h0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] = bf16r(acc[2 * i]) + bf16_to_f32((bf16_t)(v[i] & 0xffffu));
+        acc[2 * i + 1] = bf16r(acc[2 * i + 1]) + bf16_to_f32((bf16_t)(v[i] >> 16));
+      }
+    }
     u32x4 o;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -54,21 +68,40 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(const bf16_t* __restr
 
 using namespace ferry;
 
-extern "C" int ferry_combine(const void* part, const int32_t* pair_pos, int64_t tokens,
-                             int64_t topk, int64_t hidden, void* out, void* stream) {
+namespace {
+int combine_impl(const void* part, const int32_t* pair_pos, int64_t tokens, int64_t topk,
+                 int64_t hidden, const void* addend, void* out, void* stream) {
   clear_error();
   FERRY_CHECK_ARG(tokens >= 0 && topk >= 1, "bad sizes");
   FERRY_CHECK_ARG(hidden > 0 && hidden % kVec == 0, "hidden must be a positive multiple of %d",
                   kVec);
   FERRY_CHECK_ARG(tokens == 0 || (part && out), "null pointer argument");
-  FERRY_CHECK_ARG(((uintptr_t)part % 16) == 0 && ((uintptr_t)out % 16) == 0,
-                  "part/out must be 16-byte aligned");
+  FERRY_CHECK_ARG(((uintptr_t)part % 16) == 0 && ((uintptr_t)out % 16) == 0 &&
+                      ((uintptr_t)addend % 16) == 0,
+                  "part/addend/out must be 16-byte aligned");
   if (tokens == 0) return 0;
   const int64_t work = tokens * (hidden / kVec);
   int64_t grid = ceil_div(work, kThreads);
   if (grid > 65536) grid = 65536;
   launch("combine_kernel", combine_kernel, dim3((unsigned)grid), dim3(kThreads), 0, (hipStream_t)stream,
-                     (const bf16_t*)part, pair_pos, tokens, (int)topk, hidden, (bf16_t*)out);
+                     (const bf16_t*)part, pair_pos, (const bf16_t*)addend, tokens, (int)topk, hidden,
+                     (bf16_t*)out);
   FERRY_LAUNCHED("combine_kernel");
   return 0;
+}
+}  // namespace
+
+extern "C" int ferry_combine(const void* part, const int32_t* pair_pos, int64_t tokens,
+                             int64_t topk, int64_t hidden, void* out, void* stream) {
+  return combine_impl(part, pair_pos, tokens, topk, hidden, nullptr, out, stream);
+}
+
+extern "C" int ferry_combine_add(const void* part, const int32_t* pair_pos, int64_t tokens,
+                                 int64_t topk, int64_t hidden, const void* addend, void* out,
+                                 void* stream) {
+  if (!addend && tokens > 0) {
+    clear_error();
+    FERRY_CHECK_ARG(false, "addend must not be null");
+  }
+  return combine_impl(part, pair_pos, tokens, topk, hidden, addend, out, stream);
 }

@@ -68,6 +68,9 @@ __host__ __device__ inline bf16_t f32_to_bf16(float f) {
 #endif
 }
 
+// the float value of v rounded to bf16
+__host__ __device__ inline float bf16r(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Per-launch kernel timing (ferry_timing_enable): when on, kernels are launched with

@@ -55,7 +55,6 @@ struct FfnArgs {
   ExpertList list;
 };
 
-__device__ __forceinline__ float bf16r(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
 __device__ __forceinline__ float silu_mul(float g, float u) {
   // silu(g) * u in fp32 on the bf16-rounded GEMM outputs
@@ -385,7 +384,7 @@ __global__ __launch_bounds__(256, 1) void ffn_tiled(FfnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int KT = (int)(K / BK);
-  const int l32 = lane & 31, kh = (lane >> 5) * 8;
+  const int l32 = lane & 31;
 
   // XCD-aware order: workgroup b runs on XCD b % 8 (round-robin dispatch), so in each round
   // of gridDim tiles the workgroups of one XCD take a contiguous run of tiles.  Tiles of one
@@ -619,6 +618,10 @@ extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t h
   FERRY_CHECK_ARG(experts >= 1 && experts <= FERRY_MAX_EXPERTS, "experts must be in [1, %d]",
                   FERRY_MAX_EXPERTS);
   FERRY_CHECK_ARG(out_mode == 0 || out_mode == 1, "out_mode must be 0 or 1");
+  // the tiled down projection covers the hidden dimension in 256-column tiles
+  FERRY_CHECK_ARG(hidden % 256 == 0 || max_rows_per_expert <= kSkinnyMax,
+                  "hidden must be a multiple of 256 when an expert has more than %d rows",
+                  kSkinnyMax);
   FERRY_CHECK_ARG(rows_in * topk < (int64_t)1 << 31, "rows*topk must be < 2^31");
   // the tiled kernels address A rows with 32-bit element offsets
   FERRY_CHECK_ARG(rows_in * hidden < ((int64_t)1 << 32) &&

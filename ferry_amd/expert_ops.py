@@ -15,6 +15,7 @@ from .h2d import H2DEngine
 
 __all__ = ['execute_experts', 'pack_dispatch', 'unpack_dispatch', 'reduce_partials',
            'scatter_returned', 'H2DEngine', 'router_topk', 'layout', 'expert_ffn', 'combine',
+           'SharedExpert',
            'history_update', 'current_stream', 'PHASE_UP', 'PHASE_DOWN', 'PHASE_BOTH']
 
 MAX_EXPERTS = 512
@@ -141,16 +142,69 @@ def expert_ffn(cache, x, w_sorted, starts, rows, cols, expert_list, slot_of, hid
     return out
 
 
-def combine(part, tokens, topk, hidden, pair_pos=None, out=None):
-    """out[t] = bf16(sum_j fp32(part[src(t, j)])), j ascending (expert_ops.cpp:75-92)."""
+def combine(part, tokens, topk, hidden, pair_pos=None, out=None, addend=None):
+    """out[t] = bf16(sum_j fp32(part[src(t, j)])), j ascending (expert_ops.cpp:75-92).
+
+    With ``addend`` (bf16 [tokens, hidden]) the result is bf16(fp32(out[t]) + fp32(addend[t])),
+    the bf16 addition of the DeepSeek-V2 shared-expert output.
+    """
     if out is None:
         out = torch.empty((tokens, hidden), dtype=torch.bfloat16, device=part.device)
-    check(lib().ferry_combine(
-        _dev(part, 'part', torch.bfloat16),
-        _dev(pair_pos, 'pair_pos', torch.int32) if pair_pos is not None else None,
-        tokens, topk, hidden, _dev(out, 'out', torch.bfloat16), current_stream(part.device)),
-        'combine')
+    pp = _dev(pair_pos, 'pair_pos', torch.int32) if pair_pos is not None else None
+    stream = current_stream(part.device)
+    if addend is None:
+        check(lib().ferry_combine(_dev(part, 'part', torch.bfloat16), pp, tokens, topk, hidden,
+                                  _dev(out, 'out', torch.bfloat16), stream), 'combine')
+    else:
+        if addend.shape != (tokens, hidden):
+            raise RuntimeError('addend must be bf16 [tokens, hidden]')
+        check(lib().ferry_combine_add(_dev(part, 'part', torch.bfloat16), pp, tokens, topk, hidden,
+                                      _dev(addend, 'addend', torch.bfloat16),
+                                      _dev(out, 'out', torch.bfloat16), stream), 'combine_add')
     return out
+
+
+class SharedExpert:
+    """Always-on SwiGLU expert applied to every token (DeepSeek-V2 shared experts).
+
+    Not in the reference runtime: HF's DeepseekV2MoE adds ``shared_experts(residuals)``
+    (a DeepseekV2MLP of intermediate n_shared * moe_intermediate, bf16 nn.Linear layers) to
+    the routed output (transformers 4.57 modeling_deepseek_v2; installed analogue
+    modeling_deepseek_v2.py:126-151).  Here the MLP runs on the grouped SwiGLU kernels as one
+    expert whose rows are all tokens with routing weight 1, from one weight row
+    ``[gate I*H | up I*H | down H*I]`` (the cache row format) resident in HBM.  The SwiGLU
+    rounding is the routed experts' (silu(g) * u in fp32, one bf16 rounding).
+    """
+
+    def __init__(self, row, hidden, intermediate):
+        if row.dtype != torch.bfloat16 or row.numel() != 3 * hidden * intermediate:
+            raise RuntimeError('shared expert row must be bf16 [3 * intermediate * hidden]')
+        self.row = row.reshape(1, -1).contiguous()
+        self.hidden, self.intermediate = hidden, intermediate
+        self._bufs = {}
+
+    def _buffers(self, T, device):
+        b = self._bufs.get(T)
+        if b is None:
+            b = dict(starts=torch.tensor([0, T], dtype=torch.int64, device=device),
+                     rows=torch.arange(T, dtype=torch.int64, device=device),
+                     cols=torch.zeros(T, dtype=torch.int64, device=device),
+                     w=torch.ones((T, 1), dtype=torch.bfloat16, device=device),
+                     act=torch.empty((T, self.intermediate), dtype=torch.bfloat16, device=device))
+            self._bufs[T] = b
+        return b
+
+    def __call__(self, x, out=None):
+        """bf16 [T, H] -> bf16 [T, H] = down(silu(x Wg^T) * (x Wu^T))."""
+        T = x.shape[0]
+        if out is None:
+            out = torch.empty((T, self.hidden), dtype=torch.bfloat16, device=x.device)
+        if T == 0:
+            return out
+        b = self._buffers(T, x.device)
+        return expert_ffn(self.row, x.contiguous(), b['w'], b['starts'], b['rows'], b['cols'], [0],
+                          np.zeros(1, np.int32), self.hidden, self.intermediate, b['act'], out,
+                          out_mode=1, max_rows=T, experts=1)
 
 
 def history_update(selected, experts, window, layer, ring, counts, meta, scores, ids_out=None):

@@ -86,6 +86,24 @@ def qwen3_moe(rt, layer, flat, gate_weight, topk, norm_topk_prob=True, window=12
     return rt.execute(layer, flat, selected, weights, tail), logits
 
 
+def deepseek_moe(rt, layer, flat, gate_weight, topk, shared=None, routed_scaling_factor=1.0,
+                 window=128):
+    """DeepSeek-V2 MoE block on [T, H] bf16 hidden states, greedy gate.
+
+    logits = fp32(x) @ fp32(gate)^T (PyTorch fp32 GEMM, as the HF gate), then the router kernel
+    (fp32 softmax, top-k sorted=False, * routed_scaling_factor, bf16 -- the HF gate plus the cast
+    of ferry/model.py:157), the runtime, and the shared experts (``expert_ops.SharedExpert``)
+    added in bf16 inside the combine.  Returns (out [T, H], logits).
+    """
+    logits = flat.float() @ gate_weight.float().t()
+    want_probs = getattr(rt.gather, 'score', 'frequency') == 'probability'
+    res = ops.router_topk(logits, topk, renorm=False, scale=routed_scaling_factor, sorted=False,
+                          return_probs=want_probs)
+    weights, selected = res[0], res[1]
+    tail = res[2][-window:] if want_probs else None
+    return rt.execute(layer, flat, selected, weights, tail, shared=shared), logits
+
+
 def _qwen3_forward(rt, layer, spec, window):
     def forward(module, hidden_states):
         shape = hidden_states.shape

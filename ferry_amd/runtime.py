@@ -100,7 +100,10 @@ class OffloadRuntime:
 
     # -- one layer call ------------------------------------------------------------------------
 
-    def execute(self, layer, hidden, selected, weights, probs_tail):
+    def execute(self, layer, hidden, selected, weights, probs_tail, shared=None):
+        """One MoE layer call (runtime.py:64-89).  ``shared`` (an ``expert_ops.SharedExpert``,
+        not a reference argument) adds an always-on expert's output to every token, as
+        DeepSeek-V2's block does after the routed experts; it runs while the misses copy."""
         spec = self.spec
         T, k = selected.shape
         E = spec.experts
@@ -175,6 +178,7 @@ class OffloadRuntime:
         if len(resident_list):
             self.h2d.wait_stream(slot_of[resident_list], stream)
             self._ffn(common, resident_list, slot32, buf, T, stream, counts_e)
+        shared_out = shared(common[1], out=self._shared_out(T)) if shared is not None else None
         if len(missing_list):
             if timing:
                 ev[2].record(stream)
@@ -187,8 +191,15 @@ class OffloadRuntime:
             self.timings.append(ev)
         self.event += 1
 
-        # 5. combine
-        return self.transport.combine(hidden, buf['part'], dict(layout=lay))
+        # 5. combine (+ the shared experts' output)
+        return self.transport.combine(hidden, buf['part'], dict(layout=lay), addend=shared_out)
+
+    def _shared_out(self, tokens):
+        b = self._bufs[tokens]
+        if 'shared' not in b:
+            b['shared'] = torch.empty((tokens, self.spec.hidden), dtype=torch.bfloat16,
+                                      device=self.device)
+        return b['shared']
 
     def _ffn(self, common, expert_list, slot32, buf, T, stream, counts_e):
         """Phase 1 (gate/up + SwiGLU) and phase 2 (down + weight) for ``expert_list``."""

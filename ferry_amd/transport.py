@@ -17,7 +17,7 @@ class Transport:
         lay = layout['layout']
         return hidden, lay.w_sorted
 
-    def combine(self, hidden, parts, layout):
-        """``parts`` is the token-major [T*k, H] bf16 output of the expert FFN."""
-        lay = layout['layout']
-        return ops.combine(parts, hidden.shape[0], self.topk, hidden.shape[1])
+    def combine(self, hidden, parts, layout, addend=None):
+        """``parts`` is the token-major [T*k, H] bf16 output of the expert FFN; ``addend``
+        (bf16 [T, H], optional) is added to the bf16 result in fp32."""
+        return ops.combine(parts, hidden.shape[0], self.topk, hidden.shape[1], addend=addend)

@@ -94,6 +94,23 @@ def expert_rows(keys, elements, seed, device='cuda', std=0.02):
     return out
 
 
+SHARED_KEY0 = 1 << 20   # seed keys of the shared-expert rows, disjoint from the pool keys
+
+
+def shared_rows(layers, hidden, intermediate, seed, device='cuda'):
+    """bf16 [layers, 3 H I] shared-expert rows ([gate | up | down], ~N(0, 0.02))."""
+    return expert_rows(range(SHARED_KEY0, SHARED_KEY0 + layers), 3 * hidden * intermediate, seed,
+                       device)
+
+
+def router_gates(spec, layers, seed, device='cuda', std=0.02):
+    """bf16 [E, H] router (gate) weights of each layer, ~N(0, std)."""
+    g = torch.Generator(device=device)
+    g.manual_seed(seed * 1_000_003 + 7)
+    return [(torch.randn((spec.experts, spec.hidden), generator=g, device=device) * std)
+            .to(torch.bfloat16) for _ in range(layers)]
+
+
 def make_pool(spec, layers, seed=0, device='cuda', chunk=32):
     """Pinned host pool [layers * E, 3 H I] bf16 of ~N(0, 0.02) rows (model.py:86-106 format)."""
     n = layers * spec.experts

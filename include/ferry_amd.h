@@ -90,6 +90,15 @@ int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t hidden, int6
  */
 int ferry_combine(const void* part, const int32_t* pair_pos, int64_t tokens, int64_t topk,
                   int64_t hidden, void* out, void* stream);
+/*
+ * Combine plus a bf16 addend: out[t, :] = bf16( fp32(combine(t, :)) + fp32(addend[t, :]) ).
+ * Replaces the DeepSeek-V2 block's `hidden_states + self.shared_experts(residuals)` (HF
+ * transformers 4.57 DeepseekV2MoE, reached through ferry/model.py:150-157; the installed
+ * analogue is transformers/models/deepseek_v2/modeling_deepseek_v2.py:130-137), fused into the
+ * routed combine.  addend is bf16 [tokens, hidden].
+ */
+int ferry_combine_add(const void* part, const int32_t* pair_pos, int64_t tokens, int64_t topk,
+                      int64_t hidden, const void* addend, void* out, void* stream);
 
 /*
  * Selection-frequency history on the device.  Replaces ferry/metadata.py:15-38 (GateHistory

@@ -18,4 +18,7 @@ How each function is pinned (beyond restating the reference):
                              pure-Python restatement of build_layout's loops.
   experts / combine      -- torch-CPU op order of execute_experts / reduce_partials, checked
                              against an fp64 SwiGLU and exact fp32 sums.
+  shared experts         -- HF DeepseekV2MLP op order in torch-CPU bf16, checked against an
+                             fp64 SwiGLU (the HF code itself is not the reference and is only
+                             restated).
 """

@@ -73,3 +73,29 @@ def moe_fp64(weight_rows_of, x, selected, weights, hidden, inter):
         y = ((g / (1 + torch.exp(-g))) * u) @ down.t()
         out.index_add_(0, tok, y * w.unsqueeze(1))
     return out
+
+
+def shared_mlp_ref(row, x, hidden, inter):
+    """DeepSeek-V2 shared experts (HF DeepseekV2MLP, transformers modeling_deepseek_v2.py:140-153
+    installed analogue): bf16 nn.Linear layers on the CPU, down(act(gate(x)) * up(x)) with the
+    SiLU output and the product each rounded to bf16.  ``row`` is [gate | up | down]."""
+    gate, up, down = slot_weights(row, hidden, inter)
+    g = x @ gate.t()
+    u = x @ up.t()
+    a = torch.nn.functional.silu(g) * u
+    return a @ down.t()
+
+
+def shared_mlp_fp64(row, x, hidden, inter):
+    gate, up, down = (w.double() for w in slot_weights(row, hidden, inter))
+    g = x.double() @ gate.t()
+    u = x.double() @ up.t()
+    return ((g / (1 + torch.exp(-g))) * u) @ down.t()
+
+
+def deepseek_layer_ref(weight_rows_of, shared_row, x, selected, weights, experts, hidden, inter,
+                       shared_inter):
+    """Routed experts through the reference's runtime order (moe_layer_ref), then the HF block's
+    bf16 addition of the shared experts (modeling_deepseek_v2.py:136 installed analogue)."""
+    routed = moe_layer_ref(weight_rows_of, x, selected, weights, experts, hidden, inter)
+    return routed + shared_mlp_ref(shared_row, x, hidden, shared_inter)

@@ -44,6 +44,12 @@ def test_abi_version_and_errors():
     assert 'hidden' in last_error()
     assert L.ferry_expert_ffn(None, 1, 100, 128, None, 1, 1, None, None, None, None, None, 0, None,
                               1, 1, None, None, 0, 3, None) != 0
+    # the tiled down projection needs hidden % 256 == 0 once an expert exceeds the skinny size
+    assert L.ferry_expert_ffn(None, 1, 384, 128, None, 100, 1, None, None, None, None, None, 1, None,
+                              1, 100, None, None, 0, 3, None) != 0
+    assert 'multiple of 256' in last_error()
+    assert L.ferry_combine_add(None, None, 4, 2, 64, None, None, None) != 0
+    assert 'addend' in last_error()
 
 
 @dataclass(frozen=True)

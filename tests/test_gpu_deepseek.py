@@ -1,0 +1,103 @@
+"""DeepSeek-V2-Lite-shaped layer on the HIP path: shared experts, the fused bf16 addition in the
+combine, and the single-layer parity case (T = 256, 64 experts top-6, intermediate 1408, plus
+the 2 shared experts, all experts resident): routing indices and permutation bit-exact, output
+within rel 2e-2 / abs 1e-2 of the reference's result and of an fp64 SwiGLU."""
+import numpy as np
+import pytest
+import torch
+
+from oracle.experts import (deepseek_layer_ref, moe_fp64, reduce_partials_ref, shared_mlp_fp64,
+                            shared_mlp_ref)
+from oracle.layout import layout_closed_form
+from oracle.router import deepseek_router
+
+pytestmark = pytest.mark.gpu
+
+
+def _ops():
+    from ferry_amd import expert_ops
+    return expert_ops
+
+
+@pytest.mark.parametrize('T,H,I', [
+    (16, 2048, 2816),     # decode: skinny kernels
+    (256, 2048, 2816),    # the single-layer case: tiled kernels
+    (97, 512, 384),       # ragged: one partial M tile
+    (0, 256, 128),        # empty
+])
+def test_shared_expert_vs_hf_mlp(device, T, H, I):
+    from ferry_amd import workloads
+    ops = _ops()
+    row = workloads.shared_rows(1, H, I, seed=3, device=device)[0]
+    g = torch.Generator().manual_seed(T + 5)
+    x = torch.randn((T, H), generator=g).to(torch.bfloat16)
+    shared = ops.SharedExpert(row, H, I)
+    out = shared(x.to(device))
+    torch.cuda.synchronize()
+    assert out.shape == (T, H) and out.dtype == torch.bfloat16
+    if T == 0:
+        return
+    row_c = row.cpu()
+    ref = shared_mlp_ref(row_c, x, H, I)
+    torch.testing.assert_close(out.cpu().float(), ref.float(), rtol=2e-2, atol=1e-2)
+    exact = shared_mlp_fp64(row_c, x, H, I).float()
+    torch.testing.assert_close(out.cpu().float(), exact, rtol=2e-2, atol=1e-2)
+
+
+def test_combine_add_is_bf16_addition(device):
+    """bf16(fp32(bf16(sum_j part)) + fp32(addend)): bit-exact with torch's bf16 add on the CPU."""
+    ops = _ops()
+    T, k, H = 300, 6, 2048
+    g = torch.Generator().manual_seed(9)
+    part = torch.randn((T * k, H), generator=g).to(torch.bfloat16)
+    addend = (torch.randn((T, H), generator=g) * 3).to(torch.bfloat16)
+    perm = torch.randperm(T * k, generator=g)
+    pair_pos = perm.to(torch.int32)
+    out = ops.combine(part.to(device), T, k, H, pair_pos=pair_pos.to(device), addend=addend.to(device))
+    routed = reduce_partials_ref([part[perm[j::k]] for j in range(k)],
+                                 [torch.arange(T)] * k, T, H)
+    assert torch.equal(out.cpu(), routed + addend)
+    # without addend the plain combine is unchanged
+    plain = ops.combine(part.to(device), T, k, H, pair_pos=pair_pos.to(device))
+    assert torch.equal(plain.cpu(), routed)
+
+
+def test_deepseek_layer_t256_all_resident(device):
+    """One DeepSeek-V2-Lite MoE layer, 256 tokens, every expert resident (64 slots)."""
+    from ferry_amd import expert_ops as ops
+    from ferry_amd import workloads
+    from ferry_amd.model import deepseek_moe
+    from ferry_amd.quota import Topology
+    from ferry_amd.runtime import OffloadRuntime
+    w = workloads.CONFIGS[1]
+    spec = w.spec
+    E, k, H, I, T = spec.experts, spec.topk, spec.hidden, spec.intermediate, w.tokens
+    pool = workloads.make_pool(spec, 1, seed=w.seed)
+    gate = workloads.router_gates(spec, 1, seed=w.seed, device=device)[0]
+    srow = workloads.shared_rows(1, H, w.shared_intermediate, seed=w.seed, device=device)[0]
+    x = workloads.hidden_states(T, H, seed=w.seed + 7, device=device)
+    rt = OffloadRuntime(spec, pool, [w.cache_slots], 'ferry', Topology.uniform(1, E))
+    shared = ops.SharedExpert(srow, H, w.shared_intermediate)
+    out, logits = deepseek_moe(rt, 0, x, gate, k, shared=shared)
+    torch.cuda.synchronize()
+    # routing: the oracle on the identical fp32 logits (the GEMM is not part of the parity claim)
+    lg = logits.cpu()
+    w_ref, sel_ref, _ = deepseek_router(lg, k)
+    wts, sel = ops.router_topk(logits, k, renorm=False, sorted=False)
+    assert torch.equal(sel.cpu(), sel_ref)
+    assert torch.equal(wts.cpu(), w_ref)
+    # permutation
+    lay = ops.layout(sel, wts, E)
+    ref_lay = layout_closed_form(sel_ref.numpy(), E, w_ref.float().numpy())
+    for key in ('send_ids', 'starts', 'rows', 'cols'):
+        assert np.array_equal(getattr(lay, key).cpu().numpy(), ref_lay[key]), key
+    # every routed expert was fetched once into the empty cache, none evicted
+    assert rt.h2d.copies == len(np.unique(sel_ref.numpy()))
+    # output
+    ref = deepseek_layer_ref(lambda e: pool[e], srow.cpu(), x.cpu(), sel_ref, w_ref, E, H, I,
+                             w.shared_intermediate)
+    torch.testing.assert_close(out.cpu().float(), ref.float(), rtol=2e-2, atol=1e-2)
+    exact = (moe_fp64(lambda e: pool[e], x.cpu(), sel_ref, w_ref, H, I)
+             + shared_mlp_fp64(srow.cpu(), x.cpu(), H, w.shared_intermediate)).float()
+    torch.testing.assert_close(out.cpu().float(), exact, rtol=2e-2, atol=1e-2)
+    rt.close()

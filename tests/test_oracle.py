@@ -256,6 +256,24 @@ def test_moe_oracle_vs_fp64():
     torch.testing.assert_close(out, exact, rtol=2e-2, atol=1e-2)
 
 
+def test_shared_mlp_oracle_pinned():
+    """HF DeepseekV2MLP restatement: a diagonal special case reduces it to the elementwise
+    silu(2x) * (x / 2) (torch.nn.functional.silu); random weights agree with the fp64 SwiGLU."""
+    from oracle.experts import shared_mlp_fp64, shared_mlp_ref
+    H = I = 64
+    eye = torch.eye(H)
+    row = torch.cat([(2 * eye).reshape(-1), (0.5 * eye).reshape(-1), eye.reshape(-1)]).bfloat16()
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn((10, H), generator=g).bfloat16()
+    want = (torch.nn.functional.silu(2 * x) * (0.5 * x)).bfloat16()
+    assert torch.equal(shared_mlp_ref(row, x, H, I), want)
+    H, I = 128, 96
+    row = (torch.randn(3 * H * I, generator=g) * 0.05).bfloat16()
+    x = torch.randn((20, H), generator=g).bfloat16()
+    torch.testing.assert_close(shared_mlp_ref(row, x, H, I).float(), shared_mlp_fp64(row, x, H, I).float(),
+                               rtol=2e-2, atol=1e-2)
+
+
 def test_reduce_partials_is_ascending_fp32_sum():
     g = torch.Generator().manual_seed(2)
     parts = [torch.randn((3, 8), generator=g).bfloat16() for _ in range(3)]
