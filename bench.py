@@ -60,6 +60,10 @@ def parse():
     p.add_argument('--no-prefill', action='store_true')
     p.add_argument('--no-cpu-baseline', action='store_true')
     p.add_argument('--cpu-seconds', type=float, default=15.0)
+    p.add_argument('--decode-loop', action='store_true',
+                   help='also run the 48-layer decode loop (1024-token prefill, then 64-token '
+                        'steps; pooled 30%% cache, W = 128 eviction; a 58 GB pinned pool)')
+    p.add_argument('--loop-steps', type=int, default=64)
     p.add_argument('--copy-calibration-mib', type=int, default=0,
                    help='run one plain device copy kernel of this many MiB (read and written) '
                         'before the decode loop: the reference dispatch for scaling HBM byte '
@@ -179,6 +183,71 @@ def run_prefill(args, device):
                 kernel_ms={name: per(name) for name in kern})
 
 
+def run_decode_loop(args, device):
+    """Qwen3-30B-A3B decode loop over all 48 MoE layers: a 1024-token prefill layer pass, then
+    ``loop_steps`` steps of 64 tokens, routing from the seeded temporal-locality process, a pooled
+    cache of 1,843 slots with GateHistory W = 128 eviction."""
+    import hashlib
+    from ferry_amd import workloads
+    from ferry_amd.quota import Topology
+    from ferry_amd.runtime import OffloadRuntime
+    w = workloads.CONFIGS[5]
+    spec = w.spec
+    L, E, k, H, I = w.layers, spec.experts, spec.topk, spec.hidden, spec.intermediate
+    t0 = time.perf_counter()
+    routing = workloads.decode_loop_routing(w, steps=args.loop_steps)
+    pool = workloads.make_pool(spec, L, seed=w.seed)
+    setup_s = time.perf_counter() - t0
+    rt = OffloadRuntime(spec, pool, [w.cache_slots], 'ferry', Topology.uniform(1, E))
+    g = torch.Generator(device=device)
+    g.manual_seed(w.seed)
+    xs = {T: torch.randn((T, H), generator=g, device=device).to(torch.bfloat16)
+          for T in (w.prefill_tokens, w.tokens)}
+    digest = hashlib.sha1()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for layer in range(L):
+        sel = torch.from_numpy(routing['prefill'][layer]).to(device)
+        rt.execute(layer, xs[w.prefill_tokens], sel, routing['prefill_weights'][layer].to(device), None)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    prefill_copies = rt.h2d.copies
+    rt.timing = True
+    from ferry_amd import expert_ops as ops_timing
+    ops_timing.timing_enable(True)
+    t2 = time.perf_counter()
+    for s in range(args.loop_steps):
+        for layer in range(L):
+            sel = torch.from_numpy(routing['decode'][s, layer]).to(device)
+            rt.execute(layer, xs[w.tokens], sel, routing['decode_weights'][s, layer].to(device), None)
+        digest.update(rt.controller.slots[0].tobytes())
+    torch.cuda.synchronize()
+    t3 = time.perf_counter()
+    up = ops_timing.timing_summary('ffn_up_skinny')[1] + ops_timing.timing_summary('ffn_tiled_up')[1]
+    down = (ops_timing.timing_summary('ffn_down_skinny')[1]
+            + ops_timing.timing_summary('ffn_tiled_down')[1])
+    ops_timing.timing_enable(False)
+    fetch_ms, exposed_ms = rt.fetch_timing()
+    copies = rt.h2d.copies - prefill_copies
+    calls = args.loop_steps * L
+    res = dict(
+        workload=w.name, layers=L, steps=args.loop_steps, tokens_per_step=w.tokens,
+        cache_slots=w.cache_slots, setup_s=setup_s,
+        prefill_ms_per_layer=(t1 - t0) / L * 1e3, prefill_fetches=prefill_copies,
+        decode_tokens_per_s=w.tokens * args.loop_steps / (t3 - t2),
+        decode_ms_per_layer_step=(t3 - t2) / calls * 1e3,
+        misses_per_layer_step=copies / calls,
+        h2d_gbs=copies * spec.expert_bytes / (fetch_ms * 1e-3) / 1e9 if fetch_ms else None,
+        fetch_ms_per_layer_step=fetch_ms / calls,
+        fetch_hidden_frac=1.0 - exposed_ms / fetch_ms if fetch_ms else None,
+        ffn_ms_per_layer_step=(up + down) / calls,
+        hidden_cap=min(1.0, (up + down) / fetch_ms) if fetch_ms else None,
+        eviction_state_sha1=digest.hexdigest())
+    rt.close()
+    del pool
+    return res
+
+
 def cpu_baseline(dec, seconds):
     """The oracle's torch-CPU restatement of the reference op order on the decode stream."""
     from oracle.experts import execute_experts_ref, reduce_partials_ref
@@ -275,6 +344,8 @@ def main():
     )
     if not args.no_prefill:
         line['prefill'] = run_prefill(args, device)
+    if args.decode_loop:
+        line['decode_loop'] = run_decode_loop(args, device)
     if not args.no_cpu_baseline:
         line['cpu_baseline'] = cpu_baseline(dec, args.cpu_seconds)
     print(json.dumps(line), flush=True)

@@ -113,8 +113,9 @@ def router_gates(spec, layers, seed, device='cuda', std=0.02):
 
 def make_pool(spec, layers, seed=0, device='cuda', chunk=32):
     """Pinned host pool [layers * E, 3 H I] bf16 of ~N(0, 0.02) rows (model.py:86-106 format)."""
+    from .h2d import pinned_empty
     n = layers * spec.experts
-    pool = torch.empty((n, spec.expert_elements), dtype=torch.bfloat16, pin_memory=True)
+    pool = pinned_empty((n, spec.expert_elements), torch.bfloat16)
     for k0 in range(0, n, chunk):
         keys = range(k0, min(n, k0 + chunk))
         pool[k0:k0 + len(keys)].copy_(expert_rows(keys, spec.expert_elements, seed, device))
@@ -131,6 +132,33 @@ def feasible_topk_sets(logits_np, k, cap):
     """
     top = np.argsort(-logits_np, axis=1, kind='stable')[:, :k]
     return len(np.unique(top)) <= cap - 1
+
+
+def decode_loop_routing(workload, seed=None, steps=None, keep=0.8):
+    """Routing of the decode loop: a synthetic prefill of ``prefill_tokens`` tokens per layer
+    (independent Zipf(s) draws without duplicates), then ``steps`` decode steps of ``tokens``
+    tokens from the temporal-locality process of ``temporal_routing``.  Returns a dict with
+    prefill int64 [L, P, k], decode int64 [S, L, T, k] and bf16 weights of both (renormalised
+    softmax of seeded N(0, 1) logits over each chosen set)."""
+    w = workload
+    seed = w.seed if seed is None else seed
+    steps = w.steps if steps is None else steps
+    E, k, L, P = w.spec.experts, w.spec.topk, w.layers, w.prefill_tokens
+    rng = np.random.default_rng(seed + 7919)
+    pre = np.empty((L, P, k), np.int64)
+    for layer in range(L):
+        p = np.exp(zipf_log_bias(E, w.zipf_s, rng).astype(np.float64))
+        p /= p.sum()
+        for t in range(P):
+            pre[layer, t] = rng.choice(E, size=k, replace=False, p=p)
+    pre_logits = rng.standard_normal((L, P, k)).astype(np.float32)
+    sel, logits = temporal_routing(w, steps, w.tokens, seed, keep)
+
+    def weights(z):
+        return torch.softmax(torch.from_numpy(z), dim=-1).to(torch.bfloat16)
+
+    return dict(prefill=pre, prefill_weights=weights(pre_logits), decode=sel,
+                decode_weights=weights(logits))
 
 
 def temporal_routing(workload, steps, tokens, seed, keep=0.8):

@@ -1,0 +1,63 @@
+"""The Qwen3-30B-A3B decode loop (48 MoE layers, a 1024-token prefill, then 64 steps of 64
+tokens; pooled cache of 30% = 1,843 slots; GateHistory W = 128 selection frequency with LRU
+tie-break) through OffloadRuntime: the whole fetch / eviction sequence must equal the oracle
+planner's, call by call.  The sequence depends only on the routing, so the experts are kept
+small (H = 256, I = 128) to bound the pool; the routing process is the full-size one."""
+from dataclasses import replace
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.experts import moe_layer_ref
+from oracle.history import GateHistoryRef, frequency_rows
+from oracle.policy import PlannerRef
+
+pytestmark = pytest.mark.gpu
+
+
+def test_decode_loop_eviction_sequence_bit_exact(device):
+    from ferry_amd import workloads
+    from ferry_amd.quota import Topology
+    from ferry_amd.runtime import OffloadRuntime
+    w = workloads.CONFIGS[5]
+    spec = replace(w.spec, hidden=256, intermediate=128)
+    L, E, k = w.layers, spec.experts, spec.topk
+    cap = w.cache_slots
+    assert (L, E, k, cap, w.tokens, w.prefill_tokens, w.steps) == (48, 128, 8, 1843, 64, 1024, 64)
+    routing = workloads.decode_loop_routing(w)
+    pool = workloads.make_pool(spec, L, seed=w.seed)
+    rt = OffloadRuntime(spec, pool, [cap], 'ferry', Topology.uniform(1, E))
+    planner = PlannerRef(L, E, cap)
+    hist = GateHistoryRef(L, E, 128)
+    g = torch.Generator(device=device)
+    g.manual_seed(w.seed)
+    xs = {T: torch.randn((T, spec.hidden), generator=g, device=device).to(torch.bfloat16)
+          for T in (w.prefill_tokens, w.tokens)}
+    calls = [(routing['prefill'][layer], routing['prefill_weights'][layer], layer) for layer in range(L)]
+    calls += [(routing['decode'][s, layer], routing['decode_weights'][s, layer], layer)
+              for s in range(w.steps) for layer in range(L)]
+    total_fetches = evictions = 0
+    for i, (sel_np, wts, layer) in enumerate(calls):
+        sel = torch.from_numpy(np.ascontiguousarray(sel_np))
+        before = planner.slots.copy()
+        out = rt.execute(layer, xs[sel.shape[0]], sel.to(device), wts.to(device), None)
+        hist.update(layer, frequency_rows(sel_np, E, 128))
+        fetches, _ = planner.plan(i, layer, sel_np, hist.scores(layer))
+        assert np.array_equal(rt.controller.slots[0], planner.slots), f'call {i} (layer {layer})'
+        assert np.array_equal(rt.controller.last, planner.last), f'call {i}'
+        assert np.array_equal(rt.controller.scores, planner.scores), f'call {i}'
+        total_fetches += len(fetches)
+        evictions += int(np.sum(before[fetches[:, 2]] >= 0)) if len(fetches) else 0
+        if i % 401 == 0 or i == len(calls) - 1:
+            torch.cuda.synchronize()
+            ref = moe_layer_ref(lambda e: pool[layer * E + e], xs[sel.shape[0]].cpu(), sel, wts, E,
+                                spec.hidden, spec.intermediate)
+            torch.testing.assert_close(out.cpu().float(), ref.float(), rtol=2e-2, atol=1e-2)
+    rt.h2d.synchronize()
+    assert rt.h2d.copies == total_fetches == int(rt.fetches_per_rank.sum())
+    decode_calls = w.steps * L
+    # the decode phase refetches experts evicted by the other layers (~70 per layer-step)
+    assert int(rt.decode_fetches_per_rank.sum()) > 30 * decode_calls
+    assert evictions > 0.9 * total_fetches - cap
+    rt.close()
