@@ -208,14 +208,18 @@ class SharedExpert:
 
 
 def history_update(selected, experts, window, layer, ring, counts, meta, scores, ids_out=None):
-    """Device GateHistory update of ``layer`` (ferry/metadata.py:15-38, frequency rows)."""
+    """Device GateHistory update of ``layer`` (ferry/metadata.py:15-38, frequency rows).
+
+    ``scores`` (fp32 [E]) and ``ids_out`` (uint8 [T*k]) are CUDA tensors or raw device
+    addresses (ints), e.g. of a mapped host buffer that the kernel writes directly."""
     T, k = selected.shape
+    sp = scores if isinstance(scores, int) else _dev(scores, 'scores', torch.float32)
+    ip = (ids_out if isinstance(ids_out, int) or ids_out is None
+          else _dev(ids_out, 'ids_out', torch.uint8))
     check(lib().ferry_history_update(
         _dev(selected, 'selected', torch.int64), T, k, experts, window, layer,
         _dev(ring, 'ring', torch.int32), _dev(counts, 'counts', torch.int32),
-        _dev(meta, 'meta', torch.int32), _dev(scores, 'scores', torch.float32),
-        _dev(ids_out, 'ids_out', torch.uint8) if ids_out is not None else None,
-        current_stream(selected.device)), 'history_update')
+        _dev(meta, 'meta', torch.int32), sp, ip, current_stream(selected.device)), 'history_update')
 
 
 # ------------------------------------------------------------------------------------------

@@ -14,31 +14,6 @@ import torch
 from ._lib import check, lib
 
 
-_hip = None
-
-
-def pinned_empty(shape, dtype=torch.bfloat16):
-    """Uninitialised pinned host tensor allocated with hipHostMalloc.
-
-    torch's pinned allocator rounds every request up to a power of two, so a 58 GB expert pool
-    would ask for 64 GB of page-locked memory; this allocates exactly the pool's bytes.  The
-    memory is freed with hipHostFree when the tensor is released."""
-    import weakref
-    global _hip
-    if _hip is None:
-        _hip = ctypes.CDLL('libamdhip64.so')
-        _hip.hipHostMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t, ctypes.c_uint]
-        _hip.hipHostFree.argtypes = [ctypes.c_void_p]
-    n = int(np.prod(shape)) * torch.empty((), dtype=dtype).element_size()
-    ptr = ctypes.c_void_p()
-    rc = _hip.hipHostMalloc(ctypes.byref(ptr), max(n, 1), 0)
-    if rc != 0:
-        raise RuntimeError(f'hipHostMalloc of {n} bytes failed (error {rc})')
-    buf = np.ctypeslib.as_array(ctypes.cast(ptr, ctypes.POINTER(ctypes.c_uint8)), shape=(max(n, 1),))
-    weakref.finalize(buf, _hip.hipHostFree, ptr.value)
-    return torch.from_numpy(buf)[:n].view(dtype).view(shape)
-
-
 def _i64(values):
     return np.ascontiguousarray(np.asarray(values, dtype=np.int64).reshape(-1))
 

@@ -2,10 +2,10 @@
 
 Per MoE layer call (world = 1):
   1. history: the device window counters of the layer are updated from ``selected``; the
-     expert IDs (uint8) and the layer's scores are copied to pinned host memory in one D2H
-     copy -- the host must know the misses to enqueue fetches;
-  2. the layout kernel is enqueued before the host waits for that copy, so it overlaps the
-     host planning;
+     same kernel writes the expert IDs (uint8) and the layer's scores straight into mapped
+     host memory -- the host must know the misses to enqueue fetches;
+  2. the layout kernel is enqueued before the host waits for those results, so it overlaps
+     the host planning;
   3. the C++ planner picks the misses (ascending expert) and their slots (routing-aware
      eviction, bit-exact with the reference) and the H2D engine enqueues their copies on its
      own stream;
@@ -21,6 +21,7 @@ import torch
 import torch.distributed as dist
 
 from . import expert_ops as ops
+from .hostmem import mapped_buffer
 from .metadata import DeviceGateHistory, GateHistory, RouteGather
 from .policy import Controller, layer_slots
 from .transport import Transport
@@ -54,8 +55,8 @@ class OffloadRuntime:
         self.controller = Controller(spec, capacities, policy, topology, balance_tol_bps, salt)
         self.gather = RouteGather(spec.topk, spec.experts, history_window, eviction_score)
         self.transport = Transport(self.ops, spec.topk, spec.experts)
-        self._stage_dev = None   # [scores fp32 E | IDs uint8 T*k]: one D2H copy per call
-        self._stage_host = None
+        self._stage_dev = None   # device staging (probability mode): [scores fp32 E | IDs uint8 T*k]
+        self._stage_host = None  # mapped host staging buffer of the same layout
         self._bufs = {}
         self.h2d = None
         self.reset()
@@ -81,6 +82,10 @@ class OffloadRuntime:
         self.serial_wait_ns = 0
         self.timings = []
         self.kernel_bytes = dict(up=0, down=0, flops=0, experts=0, launches=0)
+        # host time per phase of execute (ns, timing=True): the planning path between the
+        # wait for the routing IDs and the fetch enqueue is on the critical path of a step
+        self.host_ns = dict(enqueue_before_wait=0, wait_for_ids=0, plan=0, fetch_enqueue=0,
+                            enqueue_after_fetch=0)
 
     def _buffers(self, tokens):
         b = self._bufs.get(tokens)
@@ -93,9 +98,11 @@ class OffloadRuntime:
                      layout=None)
             self._bufs[tokens] = b
         n = 4 * self.spec.experts + tokens * self.spec.topk
-        if self._stage_dev is None or self._stage_dev.numel() < n:
+        if self._stage_host is None or self._stage_host.numel() < n:
+            # coherent mapped host memory: the history kernel writes the layer's scores and the
+            # uint8 IDs straight into it, so the host needs no separate D2H copy
+            self._stage_host, self._stage_ptr = mapped_buffer(max(n, 4096))
             self._stage_dev = torch.zeros(n, dtype=torch.uint8, device=self.device)
-            self._stage_host = torch.zeros(n, dtype=torch.uint8, pin_memory=True)
         return b
 
     # -- one layer call ------------------------------------------------------------------------
@@ -104,6 +111,7 @@ class OffloadRuntime:
         """One MoE layer call (runtime.py:64-89).  ``shared`` (an ``expert_ops.SharedExpert``,
         not a reference argument) adds an always-on expert's output to every token, as
         DeepSeek-V2's block does after the routed experts; it runs while the misses copy."""
+        t_enter = time.perf_counter_ns()
         spec = self.spec
         T, k = selected.shape
         E = spec.experts
@@ -114,17 +122,16 @@ class OffloadRuntime:
         selected = selected.contiguous()
         weights = weights.to(torch.bfloat16).contiguous()
 
-        # 1. history + D2H of the IDs (and scores)
+        # 1. history; the kernel writes scores and IDs into the mapped host staging buffer
         frequency = self.gather.score == 'frequency'
         nbytes = 4 * E + T * k
-        scores_dev = self._stage_dev[:4 * E].view(torch.float32)
-        ids_dev = self._stage_dev[4 * E:nbytes]
-        if frequency:
-            self.device_history.update(layer, selected, scores_dev, ids_dev)
-        else:
-            ids_dev.copy_(selected.reshape(-1).to(torch.uint8))
         stage_host = self._stage_host[:nbytes]
-        stage_host.copy_(self._stage_dev[:nbytes], non_blocking=True)
+        if frequency:
+            self.device_history.update(layer, selected, self._stage_ptr, self._stage_ptr + 4 * E)
+        else:
+            ids_dev = self._stage_dev[4 * E:nbytes]
+            ids_dev.copy_(selected.reshape(-1).to(torch.uint8))
+            stage_host.copy_(self._stage_dev[:nbytes], non_blocking=True)
         tail_host = None
         if not frequency:
             tail = min(T, self.window)
@@ -137,7 +144,9 @@ class OffloadRuntime:
         lay = buf['layout']
 
         # 3. plan + fetch
+        t_sync = time.perf_counter_ns()
         d2h.synchronize()
+        t_ready = time.perf_counter_ns()
         host = stage_host.numpy()
         ids = host[4 * E:].astype(np.int64).reshape(T, k)
         if frequency:
@@ -156,7 +165,9 @@ class OffloadRuntime:
             copy_stream = self.h2d.stream
             ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
             ev[0].record(copy_stream)
+        t_plan = time.perf_counter_ns()
         self.h2d.fetch(fetch_slots, fetches[:, 1])
+        t_fetch = time.perf_counter_ns()
         if timing:
             ev[1].record(copy_stream)
 
@@ -192,7 +203,15 @@ class OffloadRuntime:
         self.event += 1
 
         # 5. combine (+ the shared experts' output)
-        return self.transport.combine(hidden, buf['part'], dict(layout=lay), addend=shared_out)
+        out = self.transport.combine(hidden, buf['part'], dict(layout=lay), addend=shared_out)
+        if self.timing:
+            h = self.host_ns
+            h['enqueue_before_wait'] += t_sync - t_enter
+            h['wait_for_ids'] += t_ready - t_sync
+            h['plan'] += t_plan - t_ready
+            h['fetch_enqueue'] += t_fetch - t_plan
+            h['enqueue_after_fetch'] += time.perf_counter_ns() - t_fetch
+        return out
 
     def _shared_out(self, tokens):
         b = self._bufs[tokens]

@@ -113,7 +113,7 @@ def router_gates(spec, layers, seed, device='cuda', std=0.02):
 
 def make_pool(spec, layers, seed=0, device='cuda', chunk=32):
     """Pinned host pool [layers * E, 3 H I] bf16 of ~N(0, 0.02) rows (model.py:86-106 format)."""
-    from .h2d import pinned_empty
+    from .hostmem import pinned_empty
     n = layers * spec.experts
     pool = pinned_empty((n, spec.expert_elements), torch.bfloat16)
     for k0 in range(0, n, chunk):
