@@ -56,7 +56,7 @@ def parse():
     p.add_argument('--gpus', type=int, default=1)
     p.add_argument('--steps', type=int, default=300)
     p.add_argument('--warmup', type=int, default=30)
-    p.add_argument('--prefill-reps', type=int, default=20)
+    p.add_argument('--prefill-reps', type=int, default=10)
     p.add_argument('--no-prefill', action='store_true')
     p.add_argument('--no-cpu-baseline', action='store_true')
     p.add_argument('--cpu-seconds', type=float, default=15.0)
@@ -146,37 +146,48 @@ def run_decode(args, device):
     return res
 
 
-def run_prefill(args, device):
-    """One Qwen3-shaped prefill layer, 8192 tokens, all 128 experts resident in HBM."""
+def run_prefill(args, device, config=3):
+    """One prefill layer with every expert resident in HBM: the Qwen3-shaped 8192-token layer
+    (config 3 shape) or the DeepSeek-V2-Lite-shaped 65,536-token layer with its two shared
+    experts (config 4 shape)."""
     from ferry_amd import expert_ops as ops
     from ferry_amd import workloads
-    w = workloads.CONFIGS[3]
-    spec = replace(w.spec, moe_layers=(0,))
+    w = workloads.CONFIGS[config]
+    spec = replace(w.spec, moe_layers=w.spec.moe_layers[:1])
     E, k, H, I, T = spec.experts, spec.topk, spec.hidden, spec.intermediate, w.tokens
-    cache = workloads.expert_rows(range(E), spec.expert_elements, seed=0, device=device)
+    cache = workloads.expert_rows(range(E), spec.expert_elements, seed=w.seed, device=device)
     logits = workloads.RouterLogits(replace(w, layers=1), device).next(0, T)
     x = workloads.hidden_states(T, H, seed=w.seed + 7, device=device)
     act = torch.empty((T * k, I), dtype=torch.bfloat16, device=device)
     part = torch.empty((T * k, H), dtype=torch.bfloat16, device=device)
     slot_of = np.arange(E, dtype=np.int32)
-    stream = torch.cuda.current_stream()
+    Is = w.shared_intermediate
+    shared = None
+    if Is:
+        srow = workloads.shared_rows(1, H, Is, seed=w.seed, device=device)[0]
+        shared = ops.SharedExpert(srow, H, Is)
+        shared_out = torch.empty((T, H), dtype=torch.bfloat16, device=device)
 
     def layer():
-        wts, sel = ops.router_topk(logits, k)
+        wts, sel = ops.router_topk(logits, k, renorm=w.renorm, sorted=w.sorted)
         lay = ops.layout(sel, wts, E)
         ops.expert_ffn(cache, x, lay.w_sorted, lay.starts, lay.rows, lay.cols, np.arange(E), slot_of,
                        H, I, act, part, max_rows=T)
-        return ops.combine(part, T, k, H), sel
+        add = shared(x, out=shared_out) if shared is not None else None
+        return ops.combine(part, T, k, H, addend=add), sel
 
     _, sel = layer()
     torch.cuda.synchronize()
     counts = np.bincount(sel.cpu().numpy().reshape(-1), minlength=E)
-    ops.timing_enable(True)
     t0 = time.perf_counter()
     for _ in range(args.prefill_reps):
         layer()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
+    ops.timing_enable(True)
+    for _ in range(args.prefill_reps):
+        layer()
+    torch.cuda.synchronize()
     kern = {name: ops.timing_summary(name) for name in
             ('router_kernel', 'layout_count', 'layout_scan', 'layout_scatter', 'ffn_up_skinny',
              'ffn_tiled_up', 'ffn_down_skinny', 'ffn_tiled_down', 'combine_kernel')}
@@ -184,11 +195,13 @@ def run_prefill(args, device):
     per = lambda name: kern[name][1] / max(1, args.prefill_reps)  # noqa: E731
     up_ms = per('ffn_up_skinny') + per('ffn_tiled_up')
     down_ms = per('ffn_down_skinny') + per('ffn_tiled_down')
-    flops = 2 * 3 * H * I * int(counts.sum())
+    flops = 2 * 3 * H * I * int(counts.sum()) + (2 * 3 * H * Is * T if Is else 0)
     gemm_ms = up_ms + down_ms
-    return dict(workload='qwen3_30b_a3b_moe_prefill_t8192_layer_resident', tokens=T,
-                tokens_per_s=T / ((t1 - t0) / args.prefill_reps),
-                gemm_ms=gemm_ms, up_ms=up_ms, down_ms=down_ms,
+    name = ('qwen3_30b_a3b_moe_prefill_t8192_layer_resident' if config == 3 else
+            'deepseek_v2_lite_moe_prefill_t65536_layer_resident_shared2')
+    return dict(workload=name, tokens=T, tokens_per_s=T / ((t1 - t0) / args.prefill_reps),
+                layer_ms=(t1 - t0) / args.prefill_reps * 1e3,
+                gemm_ms=gemm_ms, up_ms=up_ms, down_ms=down_ms, gemm_tflop=flops / 1e12,
                 mfma_tflops=flops / (gemm_ms * 1e-3) / 1e12,
                 mfma_util=flops / (gemm_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
                 active_experts=int((counts > 0).sum()), max_rows=int(counts.max()),
@@ -358,7 +371,8 @@ def main():
                     hidden_cap=min(1.0, compute_ms / dec['fetch_ms']) if dec['fetch_ms'] else None),
     )
     if not args.no_prefill:
-        line['prefill'] = run_prefill(args, device)
+        line['prefill'] = run_prefill(args, device, 3)
+        line['prefill_deepseek'] = run_prefill(args, device, 4)
     if args.decode_loop:
         line['decode_loop'] = run_decode_loop(args, device)
     if not args.no_cpu_baseline:
