@@ -353,10 +353,9 @@ template <int OFF>
 __device__ __forceinline__ void ds_read16(bf16x8& v, uint32_t addr) {
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
 }
-__device__ __forceinline__ void lds_wait(bf16x8 (&a)[4], bf16x8 (&b)[4]) {
+__device__ __forceinline__ void lds_wait(bf16x8 (&a)[4], bf16x8 (&b)[2]) {
   asm volatile("s_waitcnt lgkmcnt(0)"
-               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]),
-                 "+v"(b[2]), "+v"(b[3])
+               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1])
                :
                : "memory");
 }
@@ -371,8 +370,15 @@ __device__ __forceinline__ void wg_barrier() {
 //         epilogue act[p, i0 + c] = bf16(silu(bf16(g)) * bf16(u)).
 // MODE 1: A = activation rows (K = I); B rows = Wd[h0 ..];
 //         epilogue out[row(p), h0 + c] = bf16(bf16(y) * w(p)).
+//
+// Eight wavefronts, two per SIMD: wavefront (wm, wn) = (w / 4, w % 4) computes rows
+// 128 wm .. +128 of the tile and a quarter of its columns (MODE 0: gate and up columns
+// 32 wn .. +32, MODE 1: columns 64 wn .. +64), 4 x 2 tiles of 32x32 (128 accumulators).
+// A wavefront that stalls -- issuing its direct loads while the address unit drains the
+// others', or waiting for LDS fragments -- leaves its SIMD to the other wavefront's MFMAs.
+constexpr int kTiledThreads = 512;
 template <int MODE>
-__global__ __launch_bounds__(256, 1) void ffn_tiled(FfnArgs a) {
+__global__ __launch_bounds__(kTiledThreads, 1) void ffn_tiled(FfnArgs a) {
   __shared__ TileTable tt;
   __shared__ __attribute__((aligned(1024))) bf16_t smem[kTileLds];
   __shared__ int64_t orow_s[BM];
@@ -381,8 +387,9 @@ __global__ __launch_bounds__(256, 1) void ffn_tiled(FfnArgs a) {
   const int64_t K = MODE == 0 ? a.H : a.I;
   const int ntn = MODE == 0 ? (int)(a.I / 128) : (int)(a.H / BN);
   const int total = tt.total * ntn;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 2, wn = wave & 3;
   const int KT = (int)(K / BK);
   const int l32 = lane & 31;
 
@@ -401,16 +408,16 @@ __global__ __launch_bounds__(256, 1) void ffn_tiled(FfnArgs a) {
     const int m0 = (mt_global - tt.cum[li]) * BM;
     const bf16_t* slot = a.cache + (int64_t)a.list.slot[li] * 3 * a.H * a.I;
 
-    // Direct loads: this wavefront moves tile rows 64*wave + 8*q + lane/8 (q < 8) of A and of
+    // Direct loads: this wavefront moves tile rows 32*wave + 8*q + lane/8 (q < 4) of A and of
     // B, lane slot lane % 8 holding chunk (lane % 8) ^ ((row >> 1) & 7).  Rows past the
     // expert's last row load a valid row instead: each output row depends only on its own A
     // row, and those rows are never stored.
     const int r8 = lane >> 3, slot8 = lane & 7;
-    uint32_t aoff[8];                    // element offsets of the A rows (+ chunk)
+    uint32_t aoff[4];                    // element offsets of the A rows (+ chunk)
     const bf16_t* abase = MODE == 0 ? a.x : a.act;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int row = 64 * wave + 8 * q + r8;
+    for (int q = 0; q < 4; ++q) {
+      const int row = 32 * wave + 8 * q + r8;
       const int chunk = slot8 ^ ((row >> 1) & 7);
       const int r = m0 + row;
       const bool ok = r < n;
@@ -421,16 +428,16 @@ __global__ __launch_bounds__(256, 1) void ffn_tiled(FfnArgs a) {
         aoff[q] = (uint32_t)((start + (ok ? r : 0)) * a.I + chunk * 8);
       }
     }
-    // B rows of this wavefront: 64*wave .. +64 (MODE 0: waves 0, 1 gate rows, 2, 3 up rows)
+    // B rows of this wavefront: 32*wave .. +32 (MODE 0: waves 0-3 gate rows, 4-7 up rows)
     const int64_t ldb = MODE == 0 ? a.H : a.I;
-    const int brow0 = 64 * wave;
+    const int brow0 = 32 * wave;
     const bf16_t* bbase =
         MODE == 0 ? slot + (brow0 < 128 ? (int64_t)(ntile * 128 + brow0) * a.H
                                         : a.H * a.I + (int64_t)(ntile * 128 + brow0 - 128) * a.H)
                   : slot + 2 * a.H * a.I + (int64_t)(ntile * BN + brow0) * a.I;
-    uint32_t boff[8];
+    uint32_t boff[4];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
+    for (int q = 0; q < 4; ++q) {
       const int row = brow0 + 8 * q + r8;
       boff[q] = (uint32_t)((8 * q + r8) * ldb + (slot8 ^ ((row >> 1) & 7)) * 8);
     }
@@ -438,17 +445,17 @@ __global__ __launch_bounds__(256, 1) void ffn_tiled(FfnArgs a) {
       bf16_t* st = smem + (kt % STAGES) * (kStageBytes / 2);
       const int k0 = kt * BK;
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        __builtin_amdgcn_global_load_lds(abase + aoff[q] + k0, st + (64 * wave + 8 * q) * (kRowBytes / 2),
+      for (int q = 0; q < 4; ++q) {
+        __builtin_amdgcn_global_load_lds(abase + aoff[q] + k0, st + (32 * wave + 8 * q) * (kRowBytes / 2),
                                          16, 0, 0);
         __builtin_amdgcn_global_load_lds(bbase + boff[q] + k0,
-                                         st + kOperandBytes / 2 + (64 * wave + 8 * q) * (kRowBytes / 2),
+                                         st + kOperandBytes / 2 + (32 * wave + 8 * q) * (kRowBytes / 2),
                                          16, 0, 0);
       }
     };
     if (MODE == 1) {
       // per-row output row and routing weight for the epilogue
-      for (int r = tid; r < BM; r += 256) {
+      for (int r = tid; r < BM; r += kTiledThreads) {
         const int rr = m0 + r;
         int64_t orow = 0;
         float wt = 0.f;
@@ -463,19 +470,19 @@ __global__ __launch_bounds__(256, 1) void ffn_tiled(FfnArgs a) {
       }
     }
 
-    floatx16 acc[4][4];
+    floatx16 acc[4][2];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
     // Fragment addresses.  Lane l reads row (first row of the fragment) + l % 32, chunk
     // 2*sub + l / 32, at byte row*128 + ((chunk ^ ((row >> 1) & 7)) << 4); fragment rows are
     // multiples of 32 apart, so the swizzle term only depends on the lane and the sub-step.
-    // A fragments i: rows wm*128 + 32 i.  B fragments j: MODE 0 gate rows wn*64 + 32 j (j < 2)
-    // and up rows 128 + wn*64 + 32 (j - 2); MODE 1 rows wn*128 + 32 j.
+    // A fragments i: rows wm*128 + 32 i.  B fragments j: MODE 0 gate rows 32 wn (j = 0) and
+    // up rows 128 + 32 wn (j = 1); MODE 1 rows 64 wn + 32 j.
     const uint32_t smem_base = lds_addr(smem);
     const int swz = (l32 >> 1) & 7, half = lane >> 5;
     uint32_t a_addr[4], b_addr[4];
@@ -483,40 +490,31 @@ __global__ __launch_bounds__(256, 1) void ffn_tiled(FfnArgs a) {
     for (int sub = 0; sub < 4; ++sub) {
       const uint32_t slotb = (uint32_t)((((2 * sub + half) ^ swz)) << 4);
       a_addr[sub] = smem_base + (uint32_t)((wm * 128 + l32) * kRowBytes) + slotb;
-      b_addr[sub] = smem_base + kOperandBytes + (uint32_t)(((MODE == 0 ? wn * 64 : wn * 128) + l32) * kRowBytes) + slotb;
+      b_addr[sub] = smem_base + kOperandBytes + (uint32_t)(((MODE == 0 ? wn * 32 : wn * 64) + l32) * kRowBytes) + slotb;
     }
-    auto rd = [&](int kt, int sub, bf16x8 (&fa)[4], bf16x8 (&fb)[4]) {
+    auto rd = [&](int kt, int sub, bf16x8 (&fa)[4], bf16x8 (&fb)[2]) {
       const uint32_t so = (uint32_t)((kt % STAGES) * kStageBytes);
       const uint32_t ab = a_addr[sub] + so, bb = b_addr[sub] + so;
       ds_read16<0 * 4096>(fa[0], ab);
       ds_read16<1 * 4096>(fa[1], ab);
       ds_read16<2 * 4096>(fa[2], ab);
       ds_read16<3 * 4096>(fa[3], ab);
-      if constexpr (MODE == 0) {
-        ds_read16<0>(fb[0], bb);
-        ds_read16<4096>(fb[1], bb);
-        ds_read16<16384>(fb[2], bb);
-        ds_read16<16384 + 4096>(fb[3], bb);
-      } else {
-        ds_read16<0 * 4096>(fb[0], bb);
-        ds_read16<1 * 4096>(fb[1], bb);
-        ds_read16<2 * 4096>(fb[2], bb);
-        ds_read16<3 * 4096>(fb[3], bb);
-      }
+      ds_read16<0>(fb[0], bb);
+      ds_read16<MODE == 0 ? 16384 : 4096>(fb[1], bb);
     };
-    auto mma = [&](const bf16x8 (&fa)[4], const bf16x8 (&fb)[4]) {
+    auto mma = [&](const bf16x8 (&fa)[4], const bf16x8 (&fb)[2]) {
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 2; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
     };
 
     // pipeline: stage kt+1 streams in while stage kt is multiplied; the fragments of the next
     // sub-step are read while the MFMAs of the current one run
-    bf16x8 f0a[4], f0b[4], f1a[4], f1b[4];
+    bf16x8 f0a[4], f0b[2], f1a[4], f1b[2];
     issue(0);
     wait_vmcnt0();
     wg_barrier();
@@ -555,33 +553,30 @@ __global__ __launch_bounds__(256, 1) void ffn_tiled(FfnArgs a) {
     constexpr int CPR = OC / 8;  // 16-byte chunks per row
     bf16_t* os = smem;
 #pragma unroll
-    for (int half = 0; half < HALVES; ++half) {
-      if (HALVES == 1 || wm == half) {
+    for (int hf = 0; hf < HALVES; ++hf) {
+      if (HALVES == 1 || wm == hf) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
             const int r = wm * 128 + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-            const int rs = r - half * HROWS;
+            const int rs = r - hf * HROWS;
             if (MODE == 0) {
-#pragma unroll
-              for (int jg = 0; jg < 2; ++jg) {
-                const float g = bf16r(acc[i][jg][v]), u = bf16r(acc[i][jg + 2][v]);
-                os[rs * OLD + wn * 64 + jg * 32 + l32] = f32_to_bf16(silu_mul(g, u));
-              }
+              const float g = bf16r(acc[i][0][v]), u = bf16r(acc[i][1][v]);
+              os[rs * OLD + wn * 32 + l32] = f32_to_bf16(silu_mul(g, u));
             } else {
               const float wt = wt_s[r];
 #pragma unroll
-              for (int j = 0; j < 4; ++j)
-                os[rs * OLD + wn * 128 + j * 32 + l32] = f32_to_bf16(bf16r(acc[i][j][v]) * wt);
+              for (int j = 0; j < 2; ++j)
+                os[rs * OLD + wn * 64 + j * 32 + l32] = f32_to_bf16(bf16r(acc[i][j][v]) * wt);
             }
           }
         }
       }
       __syncthreads();
-      for (int c = tid; c < HROWS * CPR; c += 256) {
+      for (int c = tid; c < HROWS * CPR; c += kTiledThreads) {
         const int rs = c / CPR, cc = (c % CPR) * 8;
-        const int r = rs + half * HROWS;
+        const int r = rs + hf * HROWS;
         if (m0 + r >= n) continue;
         const u32x4 v = *reinterpret_cast<const u32x4*>(&os[rs * OLD + cc]);
         if (MODE == 0) {
@@ -684,7 +679,7 @@ extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t h
       if (any_big) {
         const int64_t t1 = tile_bound * (inter / 128);
         launch("ffn_tiled_up", ffn_tiled<0>, dim3((unsigned)(t1 < grid_cap ? t1 : grid_cap)),
-                           dim3(256), 0, s, args);
+                           dim3(kTiledThreads), 0, s, args);
         FERRY_LAUNCHED("ffn_tiled<up>");
       }
     }
@@ -700,7 +695,7 @@ extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t h
       if (any_big) {
         const int64_t t2 = tile_bound * (hidden / BN);
         launch("ffn_tiled_down", ffn_tiled<1>, dim3((unsigned)(t2 < grid_cap ? t2 : grid_cap)),
-                           dim3(256), 0, s, args);
+                           dim3(kTiledThreads), 0, s, args);
         FERRY_LAUNCHED("ffn_tiled<down>");
       }
     }
