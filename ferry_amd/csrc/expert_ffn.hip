@@ -339,6 +339,26 @@ __device__ __forceinline__ int find_entry(const TileTable& tt, int m) {
   return lo;
 }
 
+// a wave-uniform pointer moved to scalar registers
+template <typename T>
+__device__ __forceinline__ const T* uniform_ptr(const T* p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const T*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+// 16-byte global->LDS direct load of each lane: global address sbase + voff (wave-uniform base
+// in scalar registers, 32-bit lane byte offset), LDS byte address lds + 16 * lane.  Issued as
+// inline asm so that the address keeps this form wherever the load is scheduled; the compiler
+// does not track these loads, their completion is awaited with wait_vmcnt0.
+__device__ __forceinline__ void dma16(const char* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "global_load_lds_dwordx4 %0, %1"
+      :
+      : "v"(voff), "s"(sbase), "s"(lds)
+      : "memory", "m0");
+}
 // wait until at most N of this wavefront's vector-memory operations are outstanding
 __device__ __forceinline__ void wait_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
@@ -413,45 +433,47 @@ __global__ __launch_bounds__(kTiledThreads, 1) void ffn_tiled(FfnArgs a) {
     // expert's last row load a valid row instead: each output row depends only on its own A
     // row, and those rows are never stored.
     const int r8 = lane >> 3, slot8 = lane & 7;
-    uint32_t aoff[4];                    // element offsets of the A rows (+ chunk)
-    const bf16_t* abase = MODE == 0 ? a.x : a.act;
+    // byte offsets of this lane's A rows (+ chunk) from abase: < 2^32 (host-checked sizes)
+    uint32_t aoff[4];
+    const char* abase = reinterpret_cast<const char*>(MODE == 0 ? a.x : a.act);
+    const uint32_t lda = (uint32_t)(MODE == 0 ? a.H : a.I);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int row = 32 * wave + 8 * q + r8;
       const int chunk = slot8 ^ ((row >> 1) & 7);
       const int r = m0 + row;
       const bool ok = r < n;
-      if (MODE == 0) {
-        const int64_t t = a.rows[start + (ok ? r : 0)];
-        aoff[q] = (uint32_t)(t * a.H + chunk * 8);
-      } else {
-        aoff[q] = (uint32_t)((start + (ok ? r : 0)) * a.I + chunk * 8);
-      }
+      const uint32_t t = MODE == 0 ? (uint32_t)a.rows[start + (ok ? r : 0)]
+                                   : (uint32_t)(start + (ok ? r : 0));
+      aoff[q] = (t * lda + (uint32_t)(chunk * 8)) * 2u;
     }
     // B rows of this wavefront: 32*wave .. +32 (MODE 0: waves 0-3 gate rows, 4-7 up rows)
     const int64_t ldb = MODE == 0 ? a.H : a.I;
     const int brow0 = 32 * wave;
-    const bf16_t* bbase =
+    const char* bbase = reinterpret_cast<const char*>(uniform_ptr(
         MODE == 0 ? slot + (brow0 < 128 ? (int64_t)(ntile * 128 + brow0) * a.H
                                         : a.H * a.I + (int64_t)(ntile * 128 + brow0 - 128) * a.H)
-                  : slot + 2 * a.H * a.I + (int64_t)(ntile * BN + brow0) * a.I;
+                  : slot + 2 * a.H * a.I + (int64_t)(ntile * BN + brow0) * a.I));
     uint32_t boff[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int row = brow0 + 8 * q + r8;
-      boff[q] = (uint32_t)((8 * q + r8) * ldb + (slot8 ^ ((row >> 1) & 7)) * 8);
+      boff[q] = (uint32_t)(((8 * q + r8) * ldb + (slot8 ^ ((row >> 1) & 7)) * 8) * 2);
     }
+    const uint32_t lds_smem = lds_addr(smem);
+    // direct load n (< 8) of stage kt: A rows 32 wave + 8n of this wavefront for n < 4, B rows
+    // 32 wave + 8 (n - 4) for n >= 4
+    auto dma = [&](int kt, int n) {
+      const uint32_t st = lds_smem + (uint32_t)((kt % STAGES) * kStageBytes + 32 * wave * kRowBytes);
+      const int q = n & 3;
+      if (n < 4)
+        dma16(abase + kt * BK * 2, aoff[q], st + (uint32_t)(8 * q * kRowBytes));
+      else
+        dma16(bbase + kt * BK * 2, boff[q], st + (uint32_t)(kOperandBytes + 8 * q * kRowBytes));
+    };
     auto issue = [&](int kt) {
-      bf16_t* st = smem + (kt % STAGES) * (kStageBytes / 2);
-      const int k0 = kt * BK;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        __builtin_amdgcn_global_load_lds(abase + aoff[q] + k0, st + (32 * wave + 8 * q) * (kRowBytes / 2),
-                                         16, 0, 0);
-        __builtin_amdgcn_global_load_lds(bbase + boff[q] + k0,
-                                         st + kOperandBytes / 2 + (32 * wave + 8 * q) * (kRowBytes / 2),
-                                         16, 0, 0);
-      }
+      for (int n = 0; n < 8; ++n) dma(kt, n);
     };
     if (MODE == 1) {
       // per-row output row and routing weight for the epilogue
@@ -535,7 +557,7 @@ __global__ __launch_bounds__(kTiledThreads, 1) void ffn_tiled(FfnArgs a) {
       if (more) {
         wait_vmcnt0();   // this wavefront's loads of stage kt+1 landed
         wg_barrier();    // ... everyone's; and stage kt is no longer read by anyone
-        if (kt + 2 < KT) issue(kt + 2);
+        if (kt + 2 < KT) issue(kt + 2);  // stage kt+2 into the buffer stage kt just freed
         rd(kt + 1, 0, f0a, f0b);
       }
       mma(f1a, f1b);
@@ -618,10 +640,10 @@ extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t h
                   "hidden must be a multiple of 256 when an expert has more than %d rows",
                   kSkinnyMax);
   FERRY_CHECK_ARG(rows_in * topk < (int64_t)1 << 31, "rows*topk must be < 2^31");
-  // the tiled kernels address A rows with 32-bit element offsets
-  FERRY_CHECK_ARG(rows_in * hidden < ((int64_t)1 << 32) &&
-                      rows_in * topk * inter < ((int64_t)1 << 32),
-                  "x / act must hold fewer than 2^32 elements");
+  // the tiled kernels address A rows with 32-bit byte offsets
+  FERRY_CHECK_ARG(rows_in * hidden < ((int64_t)1 << 31) &&
+                      rows_in * topk * inter < ((int64_t)1 << 31),
+                  "x / act must hold fewer than 2^31 elements");
   if (n_list == 0 || rows_in == 0) return 0;
   FERRY_CHECK_ARG(cache && x && w_sorted && starts && rows && cols && expert_list && slot_of &&
                       act && out,
