@@ -57,8 +57,10 @@ struct FfnArgs {
 
 
 __device__ __forceinline__ float silu_mul(float g, float u) {
-  // silu(g) * u in fp32 on the bf16-rounded GEMM outputs
-  return (g / (1.0f + expf(-g))) * u;
+  // silu(g) * u in fp32 on the bf16-rounded GEMM outputs: g * u / (1 + e^-g) with the
+  // hardware exp2 and reciprocal (relative error ~1e-6, far below the bf16 rounding that
+  // follows); a large negative g gives e^-g = inf and a zero result, the exact formula's limit
+  return g * u * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
 }
 
 __device__ __forceinline__ bf16x8 load8(const bf16_t* p) {
@@ -607,7 +609,10 @@ __global__ __launch_bounds__(kTiledThreads, 1) void ffn_tiled(FfnArgs a) {
           *reinterpret_cast<u32x4*>(&a.out[orow_s[r] * a.H + ntile * BN + cc]) = v;
         }
       }
-      __syncthreads();
+      // the staging reads are complete (their values are in the stores); the stores stay in
+      // flight across the barrier (__syncthreads would wait for them)
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      wg_barrier();
     }
   }
 }
