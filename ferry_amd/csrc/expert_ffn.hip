@@ -267,10 +267,9 @@ __global__ __launch_bounds__(256) void ffn_down_skinny(FfnArgs a) {
 // Tiled kernels
 // =============================================================================================
 
-// Output tile 256 x 256 per workgroup, four wavefronts of 128 x 128 (2 x 2), each a 4 x 4 grid
-// of 32x32 MFMA accumulators (256 fp32 per lane, in AGPRs).  Phase 1's 256 B rows are 128 gate
-// rows and the 128 up rows of the same intermediate columns, so every wavefront owns matching
-// gate/up accumulators and the SwiGLU runs in registers.
+// Output tile 256 x 256 per workgroup (the wavefront layout is described at ffn_tiled).
+// Phase 1's 256 B rows are 128 gate rows and the 128 up rows of the same intermediate columns,
+// so every wavefront owns matching gate/up accumulators and the SwiGLU runs in registers.
 //
 // Operand staging: global -> LDS direct loads (global_load_lds_dwordx4, no VGPR round trip).
 // A stage holds BK = 64 columns of K: 256 A rows and 256 B rows of 128 bytes.  One direct
@@ -352,7 +351,8 @@ __device__ __forceinline__ const T* uniform_ptr(const T* p) {
 // 16-byte global->LDS direct load of each lane: global address sbase + voff (wave-uniform base
 // in scalar registers, 32-bit lane byte offset), LDS byte address lds + 16 * lane.  Issued as
 // inline asm so that the address keeps this form wherever the load is scheduled; the compiler
-// does not track these loads, their completion is awaited with wait_vmcnt0.
+// does not track these loads, their completion is awaited with wait_vmcnt0.  The asm writes
+// m0 (the LDS base of the direct load); nothing else in these kernels uses m0.
 __device__ __forceinline__ void dma16(const char* sbase, uint32_t voff, uint32_t lds) {
   asm volatile(
       "s_mov_b32 m0, %2\n\t"
