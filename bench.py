@@ -7,15 +7,23 @@ router logits N(0, 1) + log Zipf(1.1) popularity (seed 1).  One step = one layer
 router kernel -> device history + D2H of the IDs -> host planner -> H2D fetch of the misses
 -> layout -> grouped SwiGLU (resident experts first) -> combine.
 
+The timed pass runs without instrumentation; a second pass over the same stream (from an empty
+cache again) collects per-launch kernel times, fetch events and host phase times.
+
 Also reported on the same line:
   * roofline: the decode expert FFN phase-1 kernel (ffn_up_skinny: gate/up projection +
     SwiGLU, 2/3 of the expert bytes), achieved GB/s on its algorithmic bytes vs 8 TB/s,
-    from HIP events around each launch on the compute stream;
+    from HIP events around each launch on the compute stream; traffic from the committed
+    FETCH_SIZE / WRITE_SIZE profile of that kernel;
   * prefill: the Qwen3-shaped 8192-token layer (experts resident), tokens/s and MFMA
     utilisation of the grouped GEMMs vs 2.5 PFLOP/s;
+  * prefill_deepseek: the DeepSeek-V2-Lite-shaped 65,536-token layer with its two shared
+    experts (experts resident), the same figures;
   * fetch: H2D GB/s of the expert copies and the fraction hidden behind compute;
   * cpu_baseline: the oracle's torch-CPU restatement of the reference op order on the host
     cores, on a bounded sample of the same decode stream.
+With --decode-loop: the 48-layer Qwen3 decode loop (1024-token prefill, then 64-token steps,
+pooled cache of 1,843 slots) as a decode_loop block.
 """
 import argparse
 import json
