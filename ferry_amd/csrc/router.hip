@@ -224,35 +224,43 @@ __device__ __forceinline__ void wave_sync_lds() {
 // value at uniform position p = 64 * slot + lane: read lane (p & 63) of each of the four
 // registers and select by slot (selecting between register values, not array elements, keeps
 // the arrays out of scratch memory)
-__device__ __forceinline__ uint32_t key_at(const uint32_t (&k)[4], int p) {
+template <int NS>
+__device__ __forceinline__ uint32_t key_at(const uint32_t (&k)[NS], int p) {
   const int l = p & 63, s = p >> 6;
-  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)k[0], l);
-  const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)k[1], l);
-  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)k[2], l);
-  const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)k[3], l);
-  return s == 0 ? r0 : s == 1 ? r1 : s == 2 ? r2 : r3;
+  uint32_t r = (uint32_t)__builtin_amdgcn_readlane((int)k[0], l);
+#pragma unroll
+  for (int q = 1; q < NS; ++q) {
+    const uint32_t rq = (uint32_t)__builtin_amdgcn_readlane((int)k[q], l);
+    r = s == q ? rq : r;
+  }
+  return r;
 }
-__device__ __forceinline__ int32_t idx_at(const int32_t (&ix)[4], int p) {
+template <int NS>
+__device__ __forceinline__ int32_t idx_at(const int32_t (&ix)[NS], int p) {
   const int l = p & 63, s = p >> 6;
-  const int32_t r0 = __builtin_amdgcn_readlane(ix[0], l);
-  const int32_t r1 = __builtin_amdgcn_readlane(ix[1], l);
-  const int32_t r2 = __builtin_amdgcn_readlane(ix[2], l);
-  const int32_t r3 = __builtin_amdgcn_readlane(ix[3], l);
-  return s == 0 ? r0 : s == 1 ? r1 : s == 2 ? r2 : r3;
+  int32_t r = __builtin_amdgcn_readlane(ix[0], l);
+#pragma unroll
+  for (int q = 1; q < NS; ++q) {
+    const int32_t rq = __builtin_amdgcn_readlane(ix[q], l);
+    r = s == q ? rq : r;
+  }
+  return r;
 }
-__device__ __forceinline__ void set_at(uint32_t (&k)[4], int32_t (&ix)[4], int p, uint32_t kv,
+template <int NS>
+__device__ __forceinline__ void set_at(uint32_t (&k)[NS], int32_t (&ix)[NS], int p, uint32_t kv,
                                        int32_t iv, int lane) {
   const bool mine = lane == (p & 63);
   const int s = p >> 6;
   // per-element selects (no indexed store, which would move the arrays to scratch)
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
+  for (int q = 0; q < NS; ++q) {
     const bool hit = mine && q == s;
     k[q] = hit ? kv : k[q];
     ix[q] = hit ? iv : ix[q];
   }
 }
-__device__ __forceinline__ void swap_at(uint32_t (&k)[4], int32_t (&ix)[4], int a, int b,
+template <int NS>
+__device__ __forceinline__ void swap_at(uint32_t (&k)[NS], int32_t (&ix)[NS], int a, int b,
                                         int lane) {
   const uint32_t ka = key_at(k, a), kb = key_at(k, b);
   const int32_t ia = idx_at(ix, a), ib = idx_at(ix, b);
@@ -261,7 +269,8 @@ __device__ __forceinline__ void swap_at(uint32_t (&k)[4], int32_t (&ix)[4], int 
 }
 
 // One std::__unguarded_partition_pivot step on [first, last); returns the cut.
-__device__ __forceinline__ int wave_partition_pivot(uint32_t (&k)[4], int32_t (&ix)[4], int first, int last,
+template <int NS>
+__device__ __forceinline__ int wave_partition_pivot(uint32_t (&k)[NS], int32_t (&ix)[NS], int first, int last,
                                     int lane, WaveScratch& ws) {
   const int mid = first + (last - first) / 2;
   {
@@ -278,10 +287,10 @@ __device__ __forceinline__ int wave_partition_pivot(uint32_t (&k)[4], int32_t (&
   }
   const uint32_t piv = key_at(k, first);
   // left stops: [first+1, last) with key <= pivot; right stops: [first, last) with key >= pivot
-  uint64_t bl[4], bg[4];
-  bool le[4], ge[4];
+  uint64_t bl[NS], bg[NS];
+  bool le[NS], ge[NS];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
+  for (int s = 0; s < NS; ++s) {
     const int pos = s * 64 + lane;
     le[s] = pos > first && pos < last && k[s] <= piv;
     ge[s] = pos >= first && pos < last && k[s] >= piv;
@@ -291,23 +300,23 @@ __device__ __forceinline__ int wave_partition_pivot(uint32_t (&k)[4], int32_t (&
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   const uint64_t gt_mask = (lane == 63) ? 0ull : (~0ull << (lane + 1));
   int nl = 0, ng = 0;
-  int rl[4], rg[4];
+  int rl[NS], rg[NS];
   int below_l = 0;
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
+  for (int s = 0; s < NS; ++s) {
     rl[s] = below_l + __popcll(bl[s] & lt_mask);
     below_l += __popcll(bl[s]);
   }
   nl = below_l;
   int above_g = 0;
 #pragma unroll
-  for (int s = 3; s >= 0; --s) {
+  for (int s = NS - 1; s >= 0; --s) {
     rg[s] = above_g + __popcll(bg[s] & gt_mask);
     above_g += __popcll(bg[s]);
   }
   ng = above_g;
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
+  for (int s = 0; s < NS; ++s) {
     const int pos = s * 64 + lane;
     if (le[s]) ws.lstop[rl[s]] = (int16_t)pos;
     if (ge[s]) ws.rstop[rg[s]] = (int16_t)pos;
@@ -318,7 +327,7 @@ __device__ __forceinline__ int wave_partition_pivot(uint32_t (&k)[4], int32_t (&
   const int mm = nl < ng ? nl : ng;
   int nswap = 0;
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
+  for (int s = 0; s < NS; ++s) {
     const int m = s * 64 + lane;
     const bool f = m < mm && ws.lstop[m] < ws.rstop[m];
     nswap += __popcll(__ballot(f));
@@ -335,7 +344,7 @@ __device__ __forceinline__ int wave_partition_pivot(uint32_t (&k)[4], int32_t (&
   // [first + 1, last - 1]; the clamp only keeps indices in range should that ever fail
   cut = cut < first + 1 ? first + 1 : (cut > last - 1 ? last - 1 : cut);
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
+  for (int s = 0; s < NS; ++s) {
     int src = -1;
     if (le[s] && rl[s] < nswap) src = ws.rstop[rl[s]];
     else if (ge[s] && rg[s] < nswap) src = ws.lstop[rg[s]];
@@ -351,19 +360,20 @@ __device__ __forceinline__ int wave_partition_pivot(uint32_t (&k)[4], int32_t (&
 
 // stable descending sort of the uniform positions [first, last) (last - first <= 16):
 // the result of std::__insertion_sort on that range
-__device__ __forceinline__ void wave_insertion_sort(uint32_t (&k)[4], int32_t (&ix)[4], int first, int last,
+template <int NS>
+__device__ __forceinline__ void wave_insertion_sort(uint32_t (&k)[NS], int32_t (&ix)[NS], int first, int last,
                                     int lane, WaveScratch& ws) {
   const int len = last - first;
   if (len <= 1) return;
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
+  for (int s = 0; s < NS; ++s) {
     const int pos = s * 64 + lane;
     if (pos >= first && pos < last) ws.stage[pos] = Pair{k[s], ix[s]};
   }
   wave_sync_lds();
-  int dest[4];
+  int dest[NS];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
+  for (int s = 0; s < NS; ++s) {
     const int pos = s * 64 + lane;
     dest[s] = -1;
     if (pos >= first && pos < last) {
@@ -377,11 +387,11 @@ __device__ __forceinline__ void wave_insertion_sort(uint32_t (&k)[4], int32_t (&
   }
   wave_sync_lds();
 #pragma unroll
-  for (int s = 0; s < 4; ++s)
+  for (int s = 0; s < NS; ++s)
     if (dest[s] >= 0) ws.stage[dest[s]] = Pair{k[s], ix[s]};
   wave_sync_lds();
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
+  for (int s = 0; s < NS; ++s) {
     const int pos = s * 64 + lane;
     if (pos >= first && pos < last) {
       k[s] = ws.stage[pos].v;
@@ -393,7 +403,8 @@ __device__ __forceinline__ void wave_insertion_sort(uint32_t (&k)[4], int32_t (&
 
 // Exact CPU top-k selection of the row (n keys, position p = 64*s + lane); the chosen indices
 // are written to ws.sel[0..k).
-__device__ __forceinline__ void exact_select(uint32_t (&k)[4], int32_t (&ix)[4], int n, int kk, bool sorted,
+template <int NS>
+__device__ __forceinline__ void exact_select(uint32_t (&k)[NS], int32_t (&ix)[NS], int n, int kk, bool sorted,
                              int lane, WaveScratch& ws) {
   bool serial = kk * 64 <= n || (sorted && kk - 1 > 16);
   if (!serial) {
@@ -418,7 +429,7 @@ __device__ __forceinline__ void exact_select(uint32_t (&k)[4], int32_t (&ix)[4],
     }
     if (serial) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
+      for (int s = 0; s < NS; ++s) {
         const int pos = s * 64 + lane;
         if (pos < n) ws.stage[pos] = Pair{k[s], ix[s]};
       }
@@ -434,7 +445,7 @@ __device__ __forceinline__ void exact_select(uint32_t (&k)[4], int32_t (&ix)[4],
     }
     if (sorted) wave_insertion_sort(k, ix, 0, kk - 1, lane, ws);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < NS; ++s) {
       const int pos = s * 64 + lane;
       if (pos < kk) ws.sel[pos] = ix[s];
     }
@@ -443,7 +454,7 @@ __device__ __forceinline__ void exact_select(uint32_t (&k)[4], int32_t (&ix)[4],
   }
   // partial_sort regime, or a final sort longer than 16: sequential on lane 0
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
+  for (int s = 0; s < NS; ++s) {
     const int pos = s * 64 + lane;
     if (pos < n) ws.stage[pos] = Pair{k[s], ix[s]};
   }
@@ -511,7 +522,7 @@ __device__ __forceinline__ float load_logit<bf16_t>(const bf16_t* p) {
   return bf16_to_f32(*p);
 }
 
-template <typename T>
+template <typename T, int NS>
 __global__ __launch_bounds__(64 * kWaves) void router_kernel(
     const T* __restrict__ logits, int64_t tokens, int n, int kk, int renorm, float scale,
     int sorted, int64_t* __restrict__ idx_out, bf16_t* __restrict__ w_out,
@@ -522,31 +533,33 @@ __global__ __launch_bounds__(64 * kWaves) void router_kernel(
   for (int64_t row = (int64_t)blockIdx.x * kWaves + wave; row < tokens;
        row += (int64_t)gridDim.x * kWaves) {
     const T* src = logits + row * n;
-    float x[4];
+    float x[NS];
     bool bad = false;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < NS; ++s) {
       const int e = s * 64 + lane;
       x[s] = e < n ? load_logit<T>(src + e) : -INFINITY;
       bad |= (e < n) && (x[s] != x[s] || x[s] == INFINITY);
     }
     const bool row_bad = __any(bad);  // softmax of this row is all NaN
     // softmax in fp32
-    float m = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-    m = wave_max(m);
-    float ex[4], part = 0.f;
+    float m = x[0];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 1; s < NS; ++s) m = fmaxf(m, x[s]);
+    m = wave_max(m);
+    float ex[NS], part = 0.f;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
       const int e = s * 64 + lane;
       ex[s] = e < n ? expf(x[s] - m) : 0.f;
       part += ex[s];
     }
     const float sum = wave_sum(part);
     const float inv = 1.0f / sum;
-    uint32_t key[4];
-    int32_t ix[4];
+    uint32_t key[NS];
+    int32_t ix[NS];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < NS; ++s) {
       const int e = s * 64 + lane;
       const float p = row_bad ? __builtin_nanf("") : ex[s] * inv;
       if (e < n) {
@@ -559,17 +572,17 @@ __global__ __launch_bounds__(64 * kWaves) void router_kernel(
     // fast path: kk arg-max rounds on distinct keys (nth_element regime, sorted output)
     bool exact = !sorted || row_bad || kk * 64 <= n;
     if (!exact) {
-      uint32_t cur[4];
+      uint32_t cur[NS];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) cur[s] = (s * 64 + lane < n) ? key[s] : 0u;
+      for (int s = 0; s < NS; ++s) cur[s] = (s * 64 + lane < n) ? key[s] : 0u;
       for (int r = 0; r < kk; ++r) {
         uint32_t lm = cur[0];
 #pragma unroll
-        for (int s = 1; s < 4; ++s) lm = cur[s] > lm ? cur[s] : lm;
+        for (int s = 1; s < NS; ++s) lm = cur[s] > lm ? cur[s] : lm;
         const uint32_t best = wave_max_u(lm);
         int eq = 0, where = 0;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
+        for (int s = 0; s < NS; ++s) {
           const bool hit = (s * 64 + lane < n) && cur[s] == best;
           eq += hit;
           if (hit) where = s * 64 + lane;
@@ -584,7 +597,7 @@ __global__ __launch_bounds__(64 * kWaves) void router_kernel(
         const int pos = __shfl(where, owner, 64);
         if (lane == 0) ws.sel[r] = pos;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) cur[s] = (lane == owner && s == (pos >> 6)) ? 0u : cur[s];
+        for (int s = 0; s < NS; ++s) cur[s] = (lane == owner && s == (pos >> 6)) ? 0u : cur[s];
       }
       wave_sync_lds();
     }
@@ -634,14 +647,21 @@ extern "C" int ferry_router_topk(const void* logits, int32_t logits_dtype, int64
   const int64_t want = ceil_div(tokens, kWaves);
   const int grid = (int)(want < 65535 ? want : 65535);
   hipStream_t s = (hipStream_t)stream;
+  // NS = 64-key slots per lane: the exact path's wave-parallel steps scale with it
+  auto go = [&](auto kernel, const auto* lg) {
+    launch("router_kernel", kernel, dim3(grid), dim3(64 * kWaves), 0, s, lg, tokens, (int)experts,
+           (int)topk, renorm, scale, sorted, idx_out, (bf16_t*)w_out_bf16, probs_out, tie_rows);
+  };
   if (logits_dtype == FERRY_BF16) {
-    launch("router_kernel", router_kernel<bf16_t>, dim3(grid), dim3(64 * kWaves), 0, s,
-                       (const bf16_t*)logits, tokens, (int)experts, (int)topk, renorm, scale,
-                       sorted, idx_out, (bf16_t*)w_out_bf16, probs_out, tie_rows);
+    const bf16_t* lg = (const bf16_t*)logits;
+    if (experts <= 64) go(router_kernel<bf16_t, 1>, lg);
+    else if (experts <= 128) go(router_kernel<bf16_t, 2>, lg);
+    else go(router_kernel<bf16_t, 4>, lg);
   } else {
-    launch("router_kernel", router_kernel<float>, dim3(grid), dim3(64 * kWaves), 0, s,
-                       (const float*)logits, tokens, (int)experts, (int)topk, renorm, scale,
-                       sorted, idx_out, (bf16_t*)w_out_bf16, probs_out, tie_rows);
+    const float* lg = (const float*)logits;
+    if (experts <= 64) go(router_kernel<float, 1>, lg);
+    else if (experts <= 128) go(router_kernel<float, 2>, lg);
+    else go(router_kernel<float, 4>, lg);
   }
   FERRY_LAUNCHED("router_kernel");
   return 0;
