@@ -71,14 +71,76 @@ __device__ __forceinline__ bf16x8 load8(const bf16_t* p) {
 // Skinny kernels
 // =============================================================================================
 
-// Phase 1, skinny: one workgroup = (expert, 16*NT intermediate columns), K split KS = 4/NT
-// ways over its wavefronts.  MT = number of 16-row M tiles (rows of the expert, <= 16*MT).
-// Each lane streams 16-byte weight fragments straight into MFMA B-operand registers; UNR
-// K steps of loads are issued before their MFMAs so ~UNR*32 bytes per lane are in flight.
-template <int NT, int MT>
+// Skinny kernels (experts with at most 64 rows: decode, and the small experts of a prefill).
+// They are bound by the weight bytes.  Each lane streams 16-byte weight fragments straight
+// into MFMA B-operand registers, the loads of UNR K steps issued before their MFMAs.  A
+// wavefront computes NC 16-column tiles from the same activation fragment, so per K step it
+// issues NC (phase 1: 2 NC) weight loads and MT activation loads: the activation rows are
+// L2 hits, and the fewer of them per weight byte, the closer the address units get to the
+// HBM rate.  The four wavefronts of a workgroup split K into contiguous ranges of 32-element
+// steps; their partial sums are added in LDS in a fixed order.
+
+template <int U, int MT, int NB>
+__device__ __forceinline__ void skinny_batch(const bf16_t* const (&pb)[NB], const bf16_t* const (&px)[MT],
+                                             const bool (&okx)[MT], int k0,
+                                             floatx4 (&acc)[MT][NB]) {
+  const bf16x8 zero8 = {};
+  bf16x8 b[NB][U], ax[MT][U];
+#pragma unroll
+  for (int s = 0; s < U; ++s)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) b[j][s] = load8(pb[j] + k0 + s * 32);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int s = 0; s < U; ++s) ax[mt][s] = okx[mt] ? load8(px[mt] + k0 + s * 32) : zero8;
+#pragma unroll
+  for (int s = 0; s < U; ++s)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+        acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax[mt][s], b[j][s], acc[mt][j], 0, 0, 0);
+}
+// K steps [k0, kend) (multiples of 32) in batches of U, then of 2 and 1 for the remainder
+template <int U, int MT, int NB>
+__device__ __forceinline__ void skinny_k_range(const bf16_t* const (&pb)[NB], const bf16_t* const (&px)[MT],
+                                               const bool (&okx)[MT], int k0, int kend,
+                                               floatx4 (&acc)[MT][NB]) {
+  for (; k0 + U * 32 <= kend; k0 += U * 32) skinny_batch<U>(pb, px, okx, k0, acc);
+  for (; k0 + 2 * 32 <= kend; k0 += 2 * 32) skinny_batch<2>(pb, px, okx, k0, acc);
+  if (k0 < kend) skinny_batch<1>(pb, px, okx, k0, acc);
+}
+// the fixed-order K reduction over the KS wavefronts of a column group nt; the wavefront with
+// ks = 0 returns true with the sums
+template <int KS, int NT, int MT, int NB>
+__device__ __forceinline__ bool skinny_reduce(floatx4 (&acc)[MT][NB], int ks, int nt, int lane) {
+  if constexpr (KS == 1) return true;
+  __shared__ floatx4 red[KS][NT][MT][NB][64];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) red[ks][nt][mt][j][lane] = acc[mt][j];
+  __syncthreads();
+  if (ks != 0) return false;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      acc[mt][j] = red[0][nt][mt][j][lane];
+#pragma unroll
+      for (int q = 1; q < KS; ++q) acc[mt][j] += red[q][nt][mt][j][lane];
+    }
+  return true;
+}
+
+// Phase 1, skinny: one workgroup = (expert, 16*NT*NC intermediate columns): NT column groups of
+// NC tiles, each group's K split over KS = 4/NT wavefronts.  MT = number of 16-row M tiles
+// (rows of the expert, <= 16*MT).  B operands j < NC: gate tiles, j >= NC: up tiles.
+template <int NT, int NC, int MT>
 __global__ __launch_bounds__(256) void ffn_up_skinny(FfnArgs a) {
   constexpr int KS = 4 / NT;
-  constexpr int UNR = 8;
+  constexpr int UNR = NC == 1 && MT == 1 ? 8 : 4;
   const int li = blockIdx.y;
   if (li >= a.list.n) return;
   const int e = a.list.expert[li];
@@ -88,12 +150,16 @@ __global__ __launch_bounds__(256) void ffn_up_skinny(FfnArgs a) {
   const int H = (int)a.H;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nt = wave % NT, ks = wave / NT;
-  const int i0 = blockIdx.x * 16 * NT + nt * 16;
+  const int i0 = (blockIdx.x * NT + nt) * 16 * NC;
   const bf16_t* wg = a.cache + (int64_t)a.list.slot[li] * 3 * a.H * a.I;
   const bf16_t* wu = wg + a.H * a.I;
   const int r16 = lane & 15, kg = (lane >> 4) * 8;
-  const bf16_t* pg = wg + (int64_t)(i0 + r16) * H + kg;
-  const bf16_t* pu = wu + (int64_t)(i0 + r16) * H + kg;
+  const bf16_t* pb[2 * NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    pb[c] = wg + (int64_t)(i0 + 16 * c + r16) * H + kg;
+    pb[NC + c] = wu + (int64_t)(i0 + 16 * c + r16) * H + kg;
+  }
   const bf16_t* px[MT];
   bool okx[MT];
 #pragma unroll
@@ -103,85 +169,37 @@ __global__ __launch_bounds__(256) void ffn_up_skinny(FfnArgs a) {
     const int64_t t = okx[mt] ? a.rows[start + r] : 0;
     px[mt] = a.x + t * a.H + kg;
   }
-  floatx4 accg[MT], accu[MT];
+  floatx4 acc[MT][2 * NC];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    accg[mt] = floatx4{0, 0, 0, 0};
-    accu[mt] = floatx4{0, 0, 0, 0};
-  }
-  const int kspan = H / KS;
-  const int kbeg = ks * kspan, kend = kbeg + kspan;
-  const bf16x8 zero8 = {};
-  int k0 = kbeg;
-  for (; k0 + UNR * 32 <= kend; k0 += UNR * 32) {
-    bf16x8 bg[UNR], bu[UNR], ax[MT][UNR];
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int s = 0; s < UNR; ++s) {
-      bg[s] = load8(pg + k0 + s * 32);
-      bu[s] = load8(pu + k0 + s * 32);
-    }
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int s = 0; s < UNR; ++s) ax[mt][s] = okx[mt] ? load8(px[mt] + k0 + s * 32) : zero8;
-#pragma unroll
-    for (int s = 0; s < UNR; ++s)
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        accg[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax[mt][s], bg[s], accg[mt], 0, 0, 0);
-        accu[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax[mt][s], bu[s], accu[mt], 0, 0, 0);
-      }
-  }
-  for (; k0 < kend; k0 += 32) {
-    const bf16x8 bg = load8(pg + k0), bu = load8(pu + k0);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const bf16x8 ax = okx[mt] ? load8(px[mt] + k0) : zero8;
-      accg[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, bg, accg[mt], 0, 0, 0);
-      accu[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, bu, accu[mt], 0, 0, 0);
-    }
-  }
-  // cross-wavefront K reduction, fixed order ks = 0..KS-1
-  if constexpr (KS > 1) {
-    __shared__ floatx4 red[KS][NT][MT][2][64];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      red[ks][nt][mt][0][lane] = accg[mt];
-      red[ks][nt][mt][1][lane] = accu[mt];
-    }
-    __syncthreads();
-    if (ks != 0) return;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      accg[mt] = red[0][nt][mt][0][lane];
-      accu[mt] = red[0][nt][mt][1][lane];
-#pragma unroll
-      for (int q = 1; q < KS; ++q) {
-        accg[mt] += red[q][nt][mt][0][lane];
-        accu[mt] += red[q][nt][mt][1][lane];
-      }
-    }
-  }
+    for (int j = 0; j < 2 * NC; ++j) acc[mt][j] = floatx4{0, 0, 0, 0};
+  const int steps = H / 32;
+  skinny_k_range<UNR>(pb, px, okx, ks * steps / KS * 32, (ks + 1) * steps / KS * 32, acc);
+  if (!skinny_reduce<KS, NT>(acc, ks, nt, lane)) return;
   // 16x16 accumulator layout: column = lane & 15, rows (lane >> 4) * 4 + [0, 4)
-  const int col = i0 + (lane & 15);
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
+  for (int c = 0; c < NC; ++c) {
+    const int col = i0 + 16 * c + (lane & 15);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int r = mt * 16 + (lane >> 4) * 4 + q;
-      if (r < n) {
-        const float g = bf16r(accg[mt][q]), u = bf16r(accu[mt][q]);
-        a.act[(start + r) * a.I + col] = f32_to_bf16(silu_mul(g, u));
+    for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = mt * 16 + (lane >> 4) * 4 + q;
+        if (r < n) {
+          const float g = bf16r(acc[mt][c][q]), u = bf16r(acc[mt][NC + c][q]);
+          a.act[(start + r) * a.I + col] = f32_to_bf16(silu_mul(g, u));
+        }
       }
     }
   }
 }
 
-// Phase 2, skinny: one workgroup = (expert, 16*NT hidden rows), K = I split KS = 4/NT ways.
-template <int NT, int MT>
+// Phase 2, skinny: one workgroup = (expert, 16*NT*NC hidden rows), laid out as phase 1.
+template <int NT, int NC, int MT>
 __global__ __launch_bounds__(256) void ffn_down_skinny(FfnArgs a) {
   constexpr int KS = 4 / NT;
-  constexpr int UNR = 8;
+  constexpr int UNR = NC == 1 ? 8 : 4;
   const int li = blockIdx.y;
   if (li >= a.list.n) return;
   const int e = a.list.expert[li];
@@ -191,10 +209,12 @@ __global__ __launch_bounds__(256) void ffn_down_skinny(FfnArgs a) {
   const int I = (int)a.I;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nt = wave % NT, ks = wave / NT;
-  const int h0 = blockIdx.x * 16 * NT + nt * 16;
+  const int h0 = (blockIdx.x * NT + nt) * 16 * NC;
   const bf16_t* wd = a.cache + (int64_t)a.list.slot[li] * 3 * a.H * a.I + 2 * a.H * a.I;
   const int r16 = lane & 15, kg = (lane >> 4) * 8;
-  const bf16_t* pd = wd + (int64_t)(h0 + r16) * I + kg;
+  const bf16_t* pb[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) pb[c] = wd + (int64_t)(h0 + 16 * c + r16) * I + kg;
   const bf16_t* pa[MT];
   bool oka[MT];
 #pragma unroll
@@ -203,49 +223,14 @@ __global__ __launch_bounds__(256) void ffn_down_skinny(FfnArgs a) {
     oka[mt] = r < n;
     pa[mt] = a.act + (start + (oka[mt] ? r : 0)) * a.I + kg;
   }
-  floatx4 acc[MT];
+  floatx4 acc[MT][NC];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) acc[mt] = floatx4{0, 0, 0, 0};
-  const int kspan = I / KS;
-  const int kbeg = ks * kspan, kend = kbeg + kspan;
-  const bf16x8 zero8 = {};
-  int k0 = kbeg;
-  for (; k0 + UNR * 32 <= kend; k0 += UNR * 32) {
-    bf16x8 b[UNR], ax[MT][UNR];
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int s = 0; s < UNR; ++s) b[s] = load8(pd + k0 + s * 32);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int s = 0; s < UNR; ++s) ax[mt][s] = oka[mt] ? load8(pa[mt] + k0 + s * 32) : zero8;
-#pragma unroll
-    for (int s = 0; s < UNR; ++s)
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax[mt][s], b[s], acc[mt], 0, 0, 0);
-  }
-  for (; k0 < kend; k0 += 32) {
-    const bf16x8 b = load8(pd + k0);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const bf16x8 ax = oka[mt] ? load8(pa[mt] + k0) : zero8;
-      acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax, b, acc[mt], 0, 0, 0);
-    }
-  }
-  if constexpr (KS > 1) {
-    __shared__ floatx4 red[KS][NT][MT][64];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) red[ks][nt][mt][lane] = acc[mt];
-    __syncthreads();
-    if (ks != 0) return;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      acc[mt] = red[0][nt][mt][lane];
-#pragma unroll
-      for (int q = 1; q < KS; ++q) acc[mt] += red[q][nt][mt][lane];
-    }
-  }
-  const int h = h0 + (lane & 15);
+    for (int c = 0; c < NC; ++c) acc[mt][c] = floatx4{0, 0, 0, 0};
+  const int steps = I / 32;
+  skinny_k_range<UNR>(pb, pa, oka, ks * steps / KS * 32, (ks + 1) * steps / KS * 32, acc);
+  if (!skinny_reduce<KS, NT>(acc, ks, nt, lane)) return;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
@@ -255,9 +240,10 @@ __global__ __launch_bounds__(256) void ffn_down_skinny(FfnArgs a) {
         const int64_t p = start + r;
         const int64_t t = a.rows[p], j = a.cols[p];
         const float wt = bf16_to_f32(a.w[t * a.k + j]);
-        const float y = bf16r(acc[mt][q]);
         const int64_t orow = a.out_mode == 0 ? t * a.k + j : p;
-        a.out[orow * a.H + h] = f32_to_bf16(y * wt);
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+          a.out[orow * a.H + h0 + 16 * c + (lane & 15)] = f32_to_bf16(bf16r(acc[mt][c][q]) * wt);
       }
     }
   }
@@ -695,13 +681,14 @@ extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t h
     const int64_t tile_bound = pairs / BM + pairs / (kSkinnyMax + 1) + 1;  // >= sum ceil(n/BM)
     const int64_t grid_cap = (int64_t)g_num_cus;  // one 256x256 workgroup per CU
     if (phases & 1) {
+      // 16 intermediate columns per workgroup, K split over the four wavefronts
       const dim3 g1((unsigned)(inter / 16), cnt);
       if (maxn <= 16)
-        launch("ffn_up_skinny", ffn_up_skinny<1, 1>, g1, dim3(256), 0, s, args);
+        launch("ffn_up_skinny", ffn_up_skinny<1, 1, 1>, g1, dim3(256), 0, s, args);
       else if (maxn <= 32)
-        launch("ffn_up_skinny", ffn_up_skinny<1, 2>, g1, dim3(256), 0, s, args);
+        launch("ffn_up_skinny", ffn_up_skinny<1, 1, 2>, g1, dim3(256), 0, s, args);
       else
-        launch("ffn_up_skinny", ffn_up_skinny<1, 4>, g1, dim3(256), 0, s, args);
+        launch("ffn_up_skinny", ffn_up_skinny<1, 1, 4>, g1, dim3(256), 0, s, args);
       FERRY_LAUNCHED("ffn_up_skinny");
       if (any_big) {
         const int64_t t1 = tile_bound * (inter / 128);
@@ -711,13 +698,15 @@ extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t h
       }
     }
     if (phases & 2) {
+      // 64 hidden rows per workgroup: one wavefront row group of four tiles with K split four
+      // ways for up to 16 rows (decode), four single-tile groups with the full K above
       const dim3 g2((unsigned)(hidden / 64), cnt);
       if (maxn <= 16)
-        launch("ffn_down_skinny", ffn_down_skinny<4, 1>, g2, dim3(256), 0, s, args);
+        launch("ffn_down_skinny", ffn_down_skinny<1, 4, 1>, g2, dim3(256), 0, s, args);
       else if (maxn <= 32)
-        launch("ffn_down_skinny", ffn_down_skinny<4, 2>, g2, dim3(256), 0, s, args);
+        launch("ffn_down_skinny", ffn_down_skinny<4, 1, 2>, g2, dim3(256), 0, s, args);
       else
-        launch("ffn_down_skinny", ffn_down_skinny<4, 4>, g2, dim3(256), 0, s, args);
+        launch("ffn_down_skinny", ffn_down_skinny<4, 1, 4>, g2, dim3(256), 0, s, args);
       FERRY_LAUNCHED("ffn_down_skinny");
       if (any_big) {
         const int64_t t2 = tile_bound * (hidden / BN);
