@@ -11,16 +11,16 @@
 // Two kernel families, selected per expert by its row count n_e:
 //  * skinny (n_e <= 64, decode): bandwidth-bound.  Weight fragments go straight from HBM
 //    into MFMA B-operand registers (16 B per lane, no LDS) and are reused across up to four
-//    16-row M tiles; x rows come from L2.  v_mfma_f32_16x16x32_bf16.  A workgroup owns 16*NT
-//    weight rows and splits K over 4/NT wavefronts; the partial sums meet in LDS.
+//    16-row M tiles; x rows come from L2.  v_mfma_f32_16x16x32_bf16.  A workgroup owns
+//    16*NT*NC weight rows (NT column groups of NC tiles) and splits K over 4/NT wavefronts;
+//    the partial sums meet in LDS.
 //  * tiled (n_e > 64, prefill): MFMA-bound.  Persistent workgroups walk a device-computed
-//    list of 128x128 output tiles; A (gathered x rows / activation rows) and B (weight rows)
-//    tiles of 64 along K are staged through padded, double-buffered LDS.
-//    v_mfma_f32_32x32x16_bf16, 2x2 wavefronts of 64x64.
+//    list of 256x256 output tiles; A (gathered x rows / activation rows) and B (weight rows)
+//    tiles of 64 along K are staged by direct global->LDS loads into a swizzled,
+//    double-buffered LDS layout.  v_mfma_f32_32x32x16_bf16, eight wavefronts of 128x64.
 // Phase 1 ("up") computes the gate and up projections together and applies silu(g)*u in the
 // epilogue; phase 2 ("down") applies the routing weight in the epilogue and writes the
 // per-(token, expert) row that the combine kernel sums.
-#include <type_traits>
 
 #include "common.h"
 
@@ -677,8 +677,8 @@ extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t h
       args.list.slot[i] = i < cnt ? slot_of[expert_list[off + i]] : 0;
     }
     const bool any_big = maxn > kSkinnyMax;
-    // M tiles over experts with > 64 rows: sum ceil(n/128) <= pairs/128 + pairs/65
-    const int64_t tile_bound = pairs / BM + pairs / (kSkinnyMax + 1) + 1;  // >= sum ceil(n/BM)
+    // M tiles over experts with > 64 rows: sum ceil(n/BM) <= pairs/BM + (experts with > 64 rows)
+    const int64_t tile_bound = pairs / BM + pairs / (kSkinnyMax + 1) + 1;  // and those are <= pairs/65
     const int64_t grid_cap = (int64_t)g_num_cus;  // one 256x256 workgroup per CU
     if (phases & 1) {
       // 16 intermediate columns per workgroup, K split over the four wavefronts
