@@ -15,7 +15,6 @@ pytestmark = pytest.mark.gpu
 def _run(device, spec, cap, calls, tokens_of, seed, zipf, overlap=True, check_every=1,
          gate_scale=8.0):
     from ferry_amd import workloads
-    from ferry_amd.model import qwen3_moe
     from ferry_amd.quota import Topology
     from ferry_amd.runtime import OffloadRuntime
     pool = workloads.make_pool(spec, spec.layers, seed=seed)
