@@ -86,4 +86,4 @@ extern "C" int ferry_timing_summary(const char* kernel, int64_t* launches, doubl
 
 extern "C" const char* ferry_last_error(void) { return ferry::g_last_error.c_str(); }
 
-extern "C" int32_t ferry_abi_version(void) { return 1; }
+extern "C" int32_t ferry_abi_version(void) { return 2; }

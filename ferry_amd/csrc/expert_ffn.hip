@@ -68,6 +68,59 @@ __device__ __forceinline__ bf16x8 load8(const bf16_t* p) {
 }
 
 // =============================================================================================
+// Memory helpers shared by the kernels below
+// =============================================================================================
+
+// a wave-uniform pointer moved to scalar registers
+template <typename T>
+__device__ __forceinline__ const T* uniform_ptr(const T* p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const T*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+// 16-byte global->LDS direct load of each lane: global address sbase + voff (wave-uniform base
+// in scalar registers, 32-bit lane byte offset), LDS byte address lds + 16 * lane.  Issued as
+// inline asm so that the address keeps this form wherever the load is scheduled; the compiler
+// does not track these loads, their completion is awaited with wait_vmcnt0.  The asm writes
+// m0 (the LDS base of the direct load); nothing else in these kernels uses m0.
+__device__ __forceinline__ void dma16(const char* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "global_load_lds_dwordx4 %0, %1"
+      :
+      : "v"(voff), "s"(sbase), "s"(lds)
+      : "memory", "m0");
+}
+// wait until at most N of this wavefront's vector-memory operations are outstanding
+__device__ __forceinline__ void wait_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+typedef __attribute__((address_space(3))) char lds_char;
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(lds_char*)p;
+}
+// LDS fragment read issued as inline asm: the compiler cannot see that it reads memory that
+// the in-flight direct loads write, so it does not insert a vmcnt(0) drain in front of it.
+// Completion is awaited explicitly with lds_wait, which also ties the fragment registers.
+template <int OFF>
+__device__ __forceinline__ void ds_read16(bf16x8& v, uint32_t addr) {
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
+}
+__device__ __forceinline__ void lds_wait(bf16x8 (&a)[4], bf16x8 (&b)[2]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1])
+               :
+               : "memory");
+}
+// workgroup barrier without the release/acquire fence of __syncthreads (which would drain
+// the direct loads of the later stages); LDS visibility is established by the explicit waits
+__device__ __forceinline__ void wg_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// =============================================================================================
 // Skinny kernels
 // =============================================================================================
 
@@ -111,25 +164,28 @@ __device__ __forceinline__ void skinny_k_range(const bf16_t* const (&pb)[NB], co
   for (; k0 + 2 * 32 <= kend; k0 += 2 * 32) skinny_batch<2>(pb, px, okx, k0, acc);
   if (k0 < kend) skinny_batch<1>(pb, px, okx, k0, acc);
 }
-// the fixed-order K reduction over the KS wavefronts of a column group nt; the wavefront with
-// ks = 0 returns true with the sums
+// the fixed-order K reduction over the KS wavefronts of a column group nt, through the LDS
+// buffer red (KS*NT*MT*NB*64 entries); the wavefront with ks = 0 returns true with the sums
 template <int KS, int NT, int MT, int NB>
-__device__ __forceinline__ bool skinny_reduce(floatx4 (&acc)[MT][NB], int ks, int nt, int lane) {
+__device__ __forceinline__ bool skinny_reduce(floatx4 (&acc)[MT][NB], int ks, int nt, int lane,
+                                              floatx4* red) {
   if constexpr (KS == 1) return true;
-  __shared__ floatx4 red[KS][NT][MT][NB][64];
+  auto at = [&](int q, int mt, int j) -> floatx4& {
+    return red[(((q * NT + nt) * MT + mt) * NB + j) * 64 + lane];
+  };
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int j = 0; j < NB; ++j) red[ks][nt][mt][j][lane] = acc[mt][j];
+    for (int j = 0; j < NB; ++j) at(ks, mt, j) = acc[mt][j];
   __syncthreads();
   if (ks != 0) return false;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
-      acc[mt][j] = red[0][nt][mt][j][lane];
+      acc[mt][j] = at(0, mt, j);
 #pragma unroll
-      for (int q = 1; q < KS; ++q) acc[mt][j] += red[q][nt][mt][j][lane];
+      for (int q = 1; q < KS; ++q) acc[mt][j] += at(q, mt, j);
     }
   return true;
 }
@@ -138,19 +194,14 @@ __device__ __forceinline__ bool skinny_reduce(floatx4 (&acc)[MT][NB], int ks, in
 // NC tiles, each group's K split over KS = 4/NT wavefronts.  MT = number of 16-row M tiles
 // (rows of the expert, <= 16*MT).  B operands j < NC: gate tiles, j >= NC: up tiles.
 template <int NT, int NC, int MT>
-__global__ __launch_bounds__(256) void ffn_up_skinny(FfnArgs a) {
+__device__ __forceinline__ void up_skinny(const FfnArgs& a, int li, int64_t start, int n, int bx,
+                                          floatx4* red) {
   constexpr int KS = 4 / NT;
   constexpr int UNR = NC == 1 && MT == 1 ? 8 : 4;
-  const int li = blockIdx.y;
-  if (li >= a.list.n) return;
-  const int e = a.list.expert[li];
-  const int64_t start = a.starts[e];
-  const int n = (int)(a.starts[e + 1] - start);
-  if (n == 0 || n > 16 * MT) return;
   const int H = (int)a.H;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nt = wave % NT, ks = wave / NT;
-  const int i0 = (blockIdx.x * NT + nt) * 16 * NC;
+  const int i0 = (bx * NT + nt) * 16 * NC;
   const bf16_t* wg = a.cache + (int64_t)a.list.slot[li] * 3 * a.H * a.I;
   const bf16_t* wu = wg + a.H * a.I;
   const int r16 = lane & 15, kg = (lane >> 4) * 8;
@@ -176,7 +227,7 @@ __global__ __launch_bounds__(256) void ffn_up_skinny(FfnArgs a) {
     for (int j = 0; j < 2 * NC; ++j) acc[mt][j] = floatx4{0, 0, 0, 0};
   const int steps = H / 32;
   skinny_k_range<UNR>(pb, px, okx, ks * steps / KS * 32, (ks + 1) * steps / KS * 32, acc);
-  if (!skinny_reduce<KS, NT>(acc, ks, nt, lane)) return;
+  if (!skinny_reduce<KS, NT>(acc, ks, nt, lane, red)) return;
   // 16x16 accumulator layout: column = lane & 15, rows (lane >> 4) * 4 + [0, 4)
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
@@ -194,22 +245,35 @@ __global__ __launch_bounds__(256) void ffn_up_skinny(FfnArgs a) {
     }
   }
 }
-
-// Phase 2, skinny: one workgroup = (expert, 16*NT*NC hidden rows), laid out as phase 1.
-template <int NT, int NC, int MT>
-__global__ __launch_bounds__(256) void ffn_down_skinny(FfnArgs a) {
-  constexpr int KS = 4 / NT;
-  constexpr int UNR = NC == 1 ? 8 : 4;
+// Experts with up to 16*MTMAX rows; each workgroup takes the smallest M-tile count that holds
+// its expert, so experts of all sizes share one launch.  16 intermediate columns per workgroup.
+template <int MTMAX>
+__global__ __launch_bounds__(256) void ffn_up_skinny(FfnArgs a) {
+  __shared__ floatx4 red[4 * MTMAX * 2 * 64];
   const int li = blockIdx.y;
   if (li >= a.list.n) return;
   const int e = a.list.expert[li];
   const int64_t start = a.starts[e];
   const int n = (int)(a.starts[e + 1] - start);
-  if (n == 0 || n > 16 * MT) return;
+  if (n == 0 || n > 16 * MTMAX) return;
+  if (MTMAX >= 4 && n > 32)
+    up_skinny<1, 1, 4>(a, li, start, n, blockIdx.x, red);
+  else if (MTMAX >= 2 && n > 16)
+    up_skinny<1, 1, 2>(a, li, start, n, blockIdx.x, red);
+  else
+    up_skinny<1, 1, 1>(a, li, start, n, blockIdx.x, red);
+}
+
+// Phase 2, skinny: one workgroup = (expert, 16*NT*NC hidden rows), laid out as phase 1.
+template <int NT, int NC, int MT>
+__device__ __forceinline__ void down_skinny(const FfnArgs& a, int li, int64_t start, int n, int bx,
+                                            floatx4* red) {
+  constexpr int KS = 4 / NT;
+  constexpr int UNR = NC == 1 ? 8 : 4;
   const int I = (int)a.I;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nt = wave % NT, ks = wave / NT;
-  const int h0 = (blockIdx.x * NT + nt) * 16 * NC;
+  const int h0 = (bx * NT + nt) * 16 * NC;
   const bf16_t* wd = a.cache + (int64_t)a.list.slot[li] * 3 * a.H * a.I + 2 * a.H * a.I;
   const int r16 = lane & 15, kg = (lane >> 4) * 8;
   const bf16_t* pb[NC];
@@ -230,7 +294,7 @@ __global__ __launch_bounds__(256) void ffn_down_skinny(FfnArgs a) {
     for (int c = 0; c < NC; ++c) acc[mt][c] = floatx4{0, 0, 0, 0};
   const int steps = I / 32;
   skinny_k_range<UNR>(pb, pa, oka, ks * steps / KS * 32, (ks + 1) * steps / KS * 32, acc);
-  if (!skinny_reduce<KS, NT>(acc, ks, nt, lane)) return;
+  if (!skinny_reduce<KS, NT>(acc, ks, nt, lane, red)) return;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
@@ -247,6 +311,25 @@ __global__ __launch_bounds__(256) void ffn_down_skinny(FfnArgs a) {
       }
     }
   }
+}
+// Experts with up to 16*MTMAX rows, 64 hidden rows per workgroup: one wavefront row group of
+// four tiles with K split four ways for up to 16 rows, four single-tile groups with the full K
+// above (the activation fragments of 2 or 4 M tiles then serve one weight fragment each).
+template <int MTMAX>
+__global__ __launch_bounds__(256) void ffn_down_skinny(FfnArgs a) {
+  __shared__ floatx4 red[4 * 4 * 64];
+  const int li = blockIdx.y;
+  if (li >= a.list.n) return;
+  const int e = a.list.expert[li];
+  const int64_t start = a.starts[e];
+  const int n = (int)(a.starts[e + 1] - start);
+  if (n == 0 || n > 16 * MTMAX) return;
+  if (MTMAX >= 4 && n > 32)
+    down_skinny<4, 1, 4>(a, li, start, n, blockIdx.x, red);
+  else if (MTMAX >= 2 && n > 16)
+    down_skinny<4, 1, 2>(a, li, start, n, blockIdx.x, red);
+  else
+    down_skinny<1, 4, 1>(a, li, start, n, blockIdx.x, red);
 }
 
 // =============================================================================================
@@ -326,54 +409,6 @@ __device__ __forceinline__ int find_entry(const TileTable& tt, int m) {
   return lo;
 }
 
-// a wave-uniform pointer moved to scalar registers
-template <typename T>
-__device__ __forceinline__ const T* uniform_ptr(const T* p) {
-  const uint64_t v = (uint64_t)(uintptr_t)p;
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-  return (const T*)(uintptr_t)(((uint64_t)hi << 32) | lo);
-}
-// 16-byte global->LDS direct load of each lane: global address sbase + voff (wave-uniform base
-// in scalar registers, 32-bit lane byte offset), LDS byte address lds + 16 * lane.  Issued as
-// inline asm so that the address keeps this form wherever the load is scheduled; the compiler
-// does not track these loads, their completion is awaited with wait_vmcnt0.  The asm writes
-// m0 (the LDS base of the direct load); nothing else in these kernels uses m0.
-__device__ __forceinline__ void dma16(const char* sbase, uint32_t voff, uint32_t lds) {
-  asm volatile(
-      "s_mov_b32 m0, %2\n\t"
-      "global_load_lds_dwordx4 %0, %1"
-      :
-      : "v"(voff), "s"(sbase), "s"(lds)
-      : "memory", "m0");
-}
-// wait until at most N of this wavefront's vector-memory operations are outstanding
-__device__ __forceinline__ void wait_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
-typedef __attribute__((address_space(3))) char lds_char;
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(lds_char*)p;
-}
-// LDS fragment read issued as inline asm: the compiler cannot see that it reads memory that
-// the in-flight direct loads write, so it does not insert a vmcnt(0) drain in front of it.
-// Completion is awaited explicitly with lds_wait, which also ties the fragment registers.
-template <int OFF>
-__device__ __forceinline__ void ds_read16(bf16x8& v, uint32_t addr) {
-  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF) : "memory");
-}
-__device__ __forceinline__ void lds_wait(bf16x8 (&a)[4], bf16x8 (&b)[2]) {
-  asm volatile("s_waitcnt lgkmcnt(0)"
-               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1])
-               :
-               : "memory");
-}
-// workgroup barrier without the release/acquire fence of __syncthreads (which would drain
-// the direct loads of the later stages); LDS visibility is established by the explicit waits
-__device__ __forceinline__ void wg_barrier() {
-  __builtin_amdgcn_sched_barrier(0);
-  asm volatile("s_barrier" ::: "memory");
-  __builtin_amdgcn_sched_barrier(0);
-}
 // MODE 0: A = gathered x rows (K = H); B rows 0..127 = Wg[i0 ..], 128..255 = Wu[i0 ..];
 //         epilogue act[p, i0 + c] = bf16(silu(bf16(g)) * bf16(u)).
 // MODE 1: A = activation rows (K = I); B rows = Wd[h0 ..];
@@ -615,7 +650,8 @@ extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t h
                                 const void* w_sorted, const int64_t* starts, const int64_t* rows,
                                 const int64_t* cols, const int32_t* expert_list, int32_t n_list,
                                 const int32_t* slot_of, int64_t experts,
-                                int64_t max_rows_per_expert, void* act, void* out,
+                                int64_t max_rows_per_expert, int64_t min_rows_per_expert,
+                                void* act, void* out,
                                 int32_t out_mode, int32_t phases, void* stream) {
   clear_error();
   FERRY_CHECK_ARG(phases >= 1 && phases <= 3, "phases must be 1 (up), 2 (down) or 3 (both)");
@@ -623,6 +659,8 @@ extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t h
   FERRY_CHECK_ARG(inter > 0 && inter % 128 == 0, "intermediate must be a positive multiple of 128");
   FERRY_CHECK_ARG(topk >= 1 && rows_in >= 0 && n_list >= 0 && max_rows_per_expert >= 0,
                   "bad sizes");
+  FERRY_CHECK_ARG(min_rows_per_expert >= 0 && min_rows_per_expert <= max_rows_per_expert,
+                  "min_rows_per_expert must be in [0, max_rows_per_expert]");
   FERRY_CHECK_ARG(experts >= 1 && experts <= FERRY_MAX_EXPERTS, "experts must be in [1, %d]",
                   FERRY_MAX_EXPERTS);
   FERRY_CHECK_ARG(out_mode == 0 || out_mode == 1, "out_mode must be 0 or 1");
@@ -665,9 +703,11 @@ extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t h
   args.I = inter;
   args.k = topk;
   args.out_mode = out_mode;
-  // max_rows_per_expert must bound every n_e (rows_in does for a layout from ferry_layout);
-  // the tiled kernels size their work from the device starts, the bound only gates the launch
+  // max_rows_per_expert must bound every n_e from above (rows_in does for a layout from
+  // ferry_layout) and min_rows_per_expert from below (0 when unknown); the kernels size their
+  // work from the device starts, the bounds only select and gate the launches
   const int64_t maxn = max_rows_per_expert;
+  const bool any_small = min_rows_per_expert <= kSkinnyMax;
   const int64_t pairs = rows_in * topk;
   for (int32_t off = 0; off < n_list; off += kListMax) {
     const int32_t cnt = (n_list - off) < kListMax ? (n_list - off) : kListMax;
@@ -682,14 +722,16 @@ extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t h
     const int64_t grid_cap = (int64_t)g_num_cus;  // one 256x256 workgroup per CU
     if (phases & 1) {
       // 16 intermediate columns per workgroup, K split over the four wavefronts
-      const dim3 g1((unsigned)(inter / 16), cnt);
-      if (maxn <= 16)
-        launch("ffn_up_skinny", ffn_up_skinny<1, 1, 1>, g1, dim3(256), 0, s, args);
-      else if (maxn <= 32)
-        launch("ffn_up_skinny", ffn_up_skinny<1, 1, 2>, g1, dim3(256), 0, s, args);
-      else
-        launch("ffn_up_skinny", ffn_up_skinny<1, 1, 4>, g1, dim3(256), 0, s, args);
-      FERRY_LAUNCHED("ffn_up_skinny");
+      if (any_small) {
+        const dim3 g1((unsigned)(inter / 16), cnt);
+        if (maxn <= 16)
+          launch("ffn_up_skinny", ffn_up_skinny<1>, g1, dim3(256), 0, s, args);
+        else if (maxn <= 32)
+          launch("ffn_up_skinny", ffn_up_skinny<2>, g1, dim3(256), 0, s, args);
+        else
+          launch("ffn_up_skinny", ffn_up_skinny<4>, g1, dim3(256), 0, s, args);
+        FERRY_LAUNCHED("ffn_up_skinny");
+      }
       if (any_big) {
         const int64_t t1 = tile_bound * (inter / 128);
         launch("ffn_tiled_up", ffn_tiled<0>, dim3((unsigned)(t1 < grid_cap ? t1 : grid_cap)),
@@ -698,16 +740,17 @@ extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t h
       }
     }
     if (phases & 2) {
-      // 64 hidden rows per workgroup: one wavefront row group of four tiles with K split four
-      // ways for up to 16 rows (decode), four single-tile groups with the full K above
-      const dim3 g2((unsigned)(hidden / 64), cnt);
-      if (maxn <= 16)
-        launch("ffn_down_skinny", ffn_down_skinny<1, 4, 1>, g2, dim3(256), 0, s, args);
-      else if (maxn <= 32)
-        launch("ffn_down_skinny", ffn_down_skinny<4, 1, 2>, g2, dim3(256), 0, s, args);
-      else
-        launch("ffn_down_skinny", ffn_down_skinny<4, 1, 4>, g2, dim3(256), 0, s, args);
-      FERRY_LAUNCHED("ffn_down_skinny");
+      // 64 hidden rows per workgroup
+      if (any_small) {
+        const dim3 g2((unsigned)(hidden / 64), cnt);
+        if (maxn <= 16)
+          launch("ffn_down_skinny", ffn_down_skinny<1>, g2, dim3(256), 0, s, args);
+        else if (maxn <= 32)
+          launch("ffn_down_skinny", ffn_down_skinny<2>, g2, dim3(256), 0, s, args);
+        else
+          launch("ffn_down_skinny", ffn_down_skinny<4>, g2, dim3(256), 0, s, args);
+        FERRY_LAUNCHED("ffn_down_skinny");
+      }
       if (any_big) {
         const int64_t t2 = tile_bound * (hidden / BN);
         launch("ffn_tiled_down", ffn_tiled<1>, dim3((unsigned)(t2 < grid_cap ? t2 : grid_cap)),

@@ -118,27 +118,42 @@ def layout(selected, weights, experts, out=None):
 
 
 PHASE_UP, PHASE_DOWN, PHASE_BOTH = 1, 2, 3
+SKINNY_MAX_ROWS = 64   # experts with at most this many rows run the skinny kernels
 
 
 def expert_ffn(cache, x, w_sorted, starts, rows, cols, expert_list, slot_of, hidden,
-               intermediate, act, out, out_mode=0, max_rows=None, experts=None, phases=PHASE_BOTH):
+               intermediate, act, out, out_mode=0, max_rows=None, experts=None, phases=PHASE_BOTH,
+               counts=None):
     """Grouped SwiGLU over cache slots for the experts in ``expert_list`` (host ints).
 
     phases: PHASE_UP (gate/up + SwiGLU into ``act``), PHASE_DOWN (down + routing weight from
-    ``act`` into ``out``) or PHASE_BOTH.
+    ``act`` into ``out``) or PHASE_BOTH.  ``counts`` (optional, host, indexed by expert) holds
+    the row count of every expert, ``starts[e+1] - starts[e]``: the experts are then issued in
+    two calls, those with at most 64 rows (skinny kernels) and the larger ones (tiled kernels),
+    each with exact row bounds, and experts without rows are skipped.
     """
     R, k = w_sorted.shape
     el = np.ascontiguousarray(expert_list, dtype=np.int32)
     so = np.ascontiguousarray(slot_of, dtype=np.int32)
     E = int(experts if experts is not None else len(so))
-    check(lib().ferry_expert_ffn(
-        _dev(cache, 'cache', torch.bfloat16), cache.shape[0], hidden, intermediate,
-        _dev(x, 'x', torch.bfloat16), R, k, _dev(w_sorted, 'w_sorted', torch.bfloat16),
-        _dev(starts, 'starts', torch.int64), _dev(rows, 'rows', torch.int64),
-        _dev(cols, 'cols', torch.int64), el.ctypes.data, len(el), so.ctypes.data, E,
-        int(max_rows if max_rows is not None else R), _dev(act, 'act', torch.bfloat16),
-        _dev(out, 'out', torch.bfloat16), int(out_mode), int(phases), current_stream(x.device)),
-        'expert_ffn')
+    args = (_dev(cache, 'cache', torch.bfloat16), cache.shape[0], hidden, intermediate,
+            _dev(x, 'x', torch.bfloat16), R, k, _dev(w_sorted, 'w_sorted', torch.bfloat16),
+            _dev(starts, 'starts', torch.int64), _dev(rows, 'rows', torch.int64),
+            _dev(cols, 'cols', torch.int64))
+    tail = (_dev(act, 'act', torch.bfloat16), _dev(out, 'out', torch.bfloat16), int(out_mode),
+            int(phases), current_stream(x.device))
+
+    def call(sub, hi, lo):
+        check(lib().ferry_expert_ffn(*args, sub.ctypes.data, len(sub), so.ctypes.data, E, hi, lo,
+                                     *tail), 'expert_ffn')
+
+    if counts is None:
+        call(el, int(max_rows if max_rows is not None else R), 0)
+        return out
+    c = np.asarray(counts, dtype=np.int64)[el]
+    for part in ((c > 0) & (c <= SKINNY_MAX_ROWS), c > SKINNY_MAX_ROWS):
+        if part.any():
+            call(np.ascontiguousarray(el[part]), int(c[part].max()), int(c[part].min()))
     return out
 
 
@@ -204,7 +219,7 @@ class SharedExpert:
         b = self._buffers(T, x.device)
         return expert_ffn(self.row, x.contiguous(), b['w'], b['starts'], b['rows'], b['cols'], [0],
                           np.zeros(1, np.int32), self.hidden, self.intermediate, b['act'], out,
-                          out_mode=1, max_rows=T, experts=1)
+                          out_mode=1, experts=1, counts=[T])
 
 
 def history_update(selected, experts, window, layer, ring, counts, meta, scores, ids_out=None):
@@ -259,7 +274,7 @@ def execute_experts(cache, input, routing_weights, slots, rows, cols, hidden, in
     out = torch.empty((max(P, 1), hidden), dtype=torch.bfloat16, device=dev)
     expert_ffn(cache, input.contiguous(), routing_weights.contiguous(), starts, rows_cat, cols_cat,
                np.arange(G), np.asarray(slots, np.int32), hidden, intermediate, act, out,
-               out_mode=1, max_rows=max(sizes) if sizes else 0, experts=G)
+               out_mode=1, experts=G, counts=sizes)
     return list(out[:P].split(sizes))
 
 

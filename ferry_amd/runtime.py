@@ -180,7 +180,7 @@ class OffloadRuntime:
         resident_list = np.flatnonzero(active & ~missing)
         missing_list = np.flatnonzero(missing)
         slot32 = slot_of.astype(np.int32)
-        counts_e = np.bincount(ids.reshape(-1), minlength=E) if self.timing else None
+        counts_e = np.bincount(ids.reshape(-1), minlength=E)
         common = (self.cache, hidden.contiguous(), lay.w_sorted, lay.starts, lay.rows, lay.cols)
         if not self.overlap and len(fetch_slots):
             started = time.perf_counter_ns()
@@ -188,7 +188,7 @@ class OffloadRuntime:
             self.serial_wait_ns += time.perf_counter_ns() - started
         if len(resident_list):
             self.h2d.wait_stream(slot_of[resident_list], stream)
-            self._ffn(common, resident_list, slot32, buf, T, stream, counts_e)
+            self._ffn(common, resident_list, slot32, buf, stream, counts_e)
         shared_out = shared(common[1], out=self._shared_out(T)) if shared is not None else None
         if len(missing_list):
             if timing:
@@ -196,7 +196,7 @@ class OffloadRuntime:
             self.h2d.wait_stream(fetch_slots, stream)
             if timing:
                 ev[3].record(stream)
-            self._ffn(common, missing_list, slot32, buf, T, stream, counts_e)
+            self._ffn(common, missing_list, slot32, buf, stream, counts_e)
         self.h2d.mark_used(slot_of[np.flatnonzero(active)], stream)
         if timing:
             self.timings.append(ev)
@@ -220,11 +220,12 @@ class OffloadRuntime:
                                       device=self.device)
         return b['shared']
 
-    def _ffn(self, common, expert_list, slot32, buf, T, stream, counts_e):
+    def _ffn(self, common, expert_list, slot32, buf, stream, counts_e):
         """Phase 1 (gate/up + SwiGLU) and phase 2 (down + weight) for ``expert_list``."""
         spec = self.spec
         self.ops.expert_ffn(*common, expert_list, slot32, spec.hidden, spec.intermediate,
-                            buf['act'], buf['part'], out_mode=0, max_rows=T, experts=spec.experts)
+                            buf['act'], buf['part'], out_mode=0, experts=spec.experts,
+                            counts=counts_e)
         if self.timing:
             H, I = spec.hidden, spec.intermediate
             rows = int(counts_e[expert_list].sum())

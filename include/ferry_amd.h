@@ -70,7 +70,10 @@ int ferry_layout(const int64_t* selected, const void* weights_bf16, int64_t toke
  * w_sorted bf16 [R, k]; starts/rows/cols come from ferry_layout.  act is bf16 scratch of
  * [R*k, I] elements.  out_mode 0 writes bf16 rows out[rows[p]*k + cols[p]] (token-major,
  * the combine input); out_mode 1 writes row p of out (grouped order).
- * max_rows_per_expert must bound every n_e (R does for a layout from ferry_layout).
+ * max_rows_per_expert must bound every n_e from above (R does for a layout from ferry_layout),
+ * min_rows_per_expert from below (0 when unknown).  Experts with at most 64 rows run the
+ * bandwidth-bound skinny kernels, larger ones the tiled MFMA kernels; a launch is skipped when
+ * the bounds show that no listed expert needs it (e.g. min_rows_per_expert > 64).
  * phases: 1 = gate/up projection + SwiGLU (writes act), 2 = down projection + routing weight
  * (reads act, writes out), 3 = both.
  */
@@ -79,8 +82,9 @@ int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t hidden, int6
                      const void* x, int64_t rows_in, int64_t topk, const void* w_sorted,
                      const int64_t* starts, const int64_t* rows, const int64_t* cols,
                      const int32_t* expert_list, int32_t n_list, const int32_t* slot_of,
-                     int64_t experts, int64_t max_rows_per_expert, void* act, void* out,
-                     int32_t out_mode, int32_t phases, void* stream);
+                     int64_t experts, int64_t max_rows_per_expert,
+                     int64_t min_rows_per_expert, void* act, void* out, int32_t out_mode,
+                     int32_t phases, void* stream);
 
 /*
  * Combine: out[t, :] = bf16( sum_{j<k} fp32(part[src(t, j), :]) ), j ascending (= ascending
