@@ -83,10 +83,13 @@ __device__ __forceinline__ const T* uniform_ptr(const T* p) {
 // in scalar registers, 32-bit lane byte offset), LDS byte address lds + 16 * lane.  Issued as
 // inline asm so that the address keeps this form wherever the load is scheduled; the compiler
 // does not track these loads, their completion is awaited with wait_vmcnt0.  The asm writes
-// m0 (the LDS base of the direct load); nothing else in these kernels uses m0.
+// m0 (the LDS base of the direct load); nothing else in these kernels uses m0.  An LDS direct
+// load needs one wait state between the SALU write of m0 and its issue (the s_nop), which the
+// compiler's hazard pass would add for its own instructions but cannot see inside the asm.
 __device__ __forceinline__ void dma16(const char* sbase, uint32_t voff, uint32_t lds) {
   asm volatile(
       "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
       "global_load_lds_dwordx4 %0, %1"
       :
       : "v"(voff), "s"(sbase), "s"(lds)
