@@ -1,18 +1,21 @@
 // H2D expert fetch engine: pinned host pool rows -> device cache slots on a dedicated stream.
 //
-// Reference: ferry/csrc/expert_ops.cpp:94-142 (H2DEngine).  A copy into a slot first waits
-// (on the copy stream, GPU-side) for the last compute that read the slot (the "used" event of
-// mark_used), then records the slot's copy-done event.  Besides the reference's host wait
-// (wait_host), wait_stream makes a compute stream wait for the copies on the GPU, so that
-// experts that are already resident can run while missing ones are still in flight.
+// Reference: ferry/csrc/expert_ops.cpp:94-142 (H2DEngine).  The copies of a fetch call wait (on
+// the copy streams, GPU-side) for the last compute that read any of the call's slots (the
+// "used" events of mark_used); events that have already fired when the call is made add no
+// wait.  After the call's copies every lane records one event, which becomes the copy-done
+// event of each slot of the call.  Besides the reference's host wait (wait_host), wait_stream
+// makes a compute stream wait for the copies on the GPU, so that experts that are already
+// resident can run while missing ones are still in flight.
 //
 // Each row is copied as kLanes equal parts on kLanes streams: one DMA stream does not fill the
 // host link (measured on MI355X: ~47 GB/s with one stream, ~56.5 GB/s with two), and splitting
 // every row keeps the lanes balanced whatever the number of misses.  A slot is ready when the
-// copy-done events of all its parts have fired.  A fetch call forks the lanes from the first
+// copy-done events of all its lanes have fired.  A fetch call forks the lanes from the first
 // stream and joins them back into it, so that the first stream (ferry_h2d_stream) brackets
-// every copy of the call.  The engine owns its streams (default priority) and events;
-// it allocates no memory.
+// every copy of the call.  Per copy only the hipMemcpyAsync itself is queued: a stream wait or
+// an event between two copies on a DMA stream costs tens of microseconds of idle link.  The
+// engine owns its streams (default priority) and events; it allocates no device memory.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -47,7 +50,7 @@ struct ferry_h2d {
   int32_t device = 0;
   hipStream_t stream[kLanes] = {};
   hipEvent_t join = nullptr;          // fork / join of the lanes around a fetch call
-  std::vector<hipEvent_t> copy_done[kLanes];  // per lane, per slot
+  std::vector<std::shared_ptr<Event>> copy_done[kLanes];  // per lane, per slot
   std::vector<int64_t> copy_seq;      // per slot: sequence number of its last copy, -1 if none
   std::vector<std::shared_ptr<Event>> used;  // per slot: last compute that read it
   int64_t seq = 0;
@@ -90,7 +93,6 @@ extern "C" int ferry_h2d_create(void* cache, int64_t cache_rows, const void* poo
   for (int l = 0; l < kLanes; ++l) {
     H2D_HIP(hipStreamCreateWithFlags(&h->stream[l], hipStreamNonBlocking));
     h->copy_done[l].assign((size_t)cache_rows, nullptr);
-    for (auto& e : h->copy_done[l]) H2D_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
   }
   H2D_HIP(hipEventCreateWithFlags(&h->join, hipEventDisableTiming));
   h->copy_seq.assign((size_t)cache_rows, -1);
@@ -104,9 +106,7 @@ extern "C" int ferry_h2d_destroy(ferry_h2d* h) {
   if (!h) return 0;
   for (int l = 0; l < kLanes; ++l)
     if (h->stream[l]) (void)hipStreamSynchronize(h->stream[l]);
-  for (int l = 0; l < kLanes; ++l)
-    for (auto e : h->copy_done[l])
-      if (e) (void)hipEventDestroy(e);
+  for (int l = 0; l < kLanes; ++l) h->copy_done[l].clear();
   if (h->join) (void)hipEventDestroy(h->join);
   h->used.clear();
   for (int l = 0; l < kLanes; ++l)
@@ -118,14 +118,9 @@ extern "C" int ferry_h2d_destroy(ferry_h2d* h) {
 extern "C" int ferry_h2d_fetch(ferry_h2d* h, const int64_t* slots, const int64_t* keys,
                                int64_t n) {
   ferry::clear_error();
-  if (n > 0) {
-    // fork: the other lanes start after what is already queued on lane 0, so that events the
-    // caller records on lane 0 around the call bracket every copy of it
-    for (int l = 1; l < kLanes; ++l) {
-      H2D_HIP(hipEventRecord(h->join, h->stream[0]));
-      H2D_HIP(hipStreamWaitEvent(h->stream[l], h->join, 0));
-    }
-  }
+  if (n <= 0) return 0;
+  // the reads of the slots about to be overwritten that may still be running
+  std::vector<hipEvent_t> pending;
   for (int64_t i = 0; i < n; ++i) {
     const int64_t slot = slots[i], key = keys[i];
     if (slot < 0 || slot >= h->cache_rows || key < 0 || key >= h->pool_rows) {
@@ -133,24 +128,49 @@ extern "C" int ferry_h2d_fetch(ferry_h2d* h, const int64_t* slots, const int64_t
                        (long long)key);
       return 2;
     }
+    const auto& u = h->used[(size_t)slot];
+    if (!u) continue;
+    bool seen = false;
+    for (hipEvent_t e : pending) seen = seen || e == u->e;
+    if (seen) continue;
+    const hipError_t q = hipEventQuery(u->e);
+    if (q == hipErrorNotReady) {
+      (void)hipGetLastError();  // a pending event is not an error
+      pending.push_back(u->e);
+    } else if (q != hipSuccess) {
+      ferry::set_error("hipEventQuery failed: %s", hipGetErrorString(q));
+      return 3;
+    }
+  }
+  // fork: the other lanes start after what is already queued on lane 0, so that events the
+  // caller records on lane 0 around the call bracket every copy of it
+  for (int l = 1; l < kLanes; ++l) {
+    H2D_HIP(hipEventRecord(h->join, h->stream[0]));
+    H2D_HIP(hipStreamWaitEvent(h->stream[l], h->join, 0));
+  }
+  for (int l = 0; l < kLanes; ++l)
+    for (hipEvent_t e : pending) H2D_HIP(hipStreamWaitEvent(h->stream[l], e, 0));
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t slot = slots[i], key = keys[i];
     for (int l = 0; l < kLanes; ++l) {
       const int64_t b0 = h->part[l], nb = h->part[l + 1] - b0;
-      if (h->used[(size_t)slot])
-        H2D_HIP(hipStreamWaitEvent(h->stream[l], h->used[(size_t)slot]->e, 0));
       if (nb > 0)
         H2D_HIP(hipMemcpyAsync(h->cache + slot * h->row_bytes + b0,
                                h->pool + key * h->row_bytes + b0, (size_t)nb,
                                hipMemcpyHostToDevice, h->stream[l]));
-      H2D_HIP(hipEventRecord(h->copy_done[l][(size_t)slot], h->stream[l]));
     }
-    h->copy_seq[(size_t)slot] = h->seq++;
-    ++h->copies;
   }
-  if (n > 0) {
-    for (int l = 1; l < kLanes; ++l) {
-      H2D_HIP(hipEventRecord(h->join, h->stream[l]));
-      H2D_HIP(hipStreamWaitEvent(h->stream[0], h->join, 0));
-    }
+  for (int l = 0; l < kLanes; ++l) {
+    auto ev = std::make_shared<Event>();
+    H2D_HIP(hipEventCreateWithFlags(&ev->e, hipEventDisableTiming));
+    H2D_HIP(hipEventRecord(ev->e, h->stream[l]));
+    for (int64_t i = 0; i < n; ++i) h->copy_done[l][(size_t)slots[i]] = ev;
+  }
+  for (int64_t i = 0; i < n; ++i) h->copy_seq[(size_t)slots[i]] = h->seq++;
+  h->copies += n;
+  for (int l = 1; l < kLanes; ++l) {
+    H2D_HIP(hipEventRecord(h->join, h->stream[l]));
+    H2D_HIP(hipStreamWaitEvent(h->stream[0], h->join, 0));
   }
   return 0;
 }
@@ -164,7 +184,8 @@ extern "C" int ferry_h2d_wait_host(ferry_h2d* h, const int64_t* slots, int64_t n
       return 2;
     }
     if (h->copy_seq[(size_t)slot] >= 0)
-      for (int l = 0; l < kLanes; ++l) H2D_HIP(hipEventSynchronize(h->copy_done[l][(size_t)slot]));
+      for (int l = 0; l < kLanes; ++l)
+        H2D_HIP(hipEventSynchronize(h->copy_done[l][(size_t)slot]->e));
   }
   return 0;
 }
@@ -188,7 +209,7 @@ extern "C" int ferry_h2d_wait_stream(ferry_h2d* h, const int64_t* slots, int64_t
   }
   if (best >= 0)
     for (int l = 0; l < kLanes; ++l)
-      H2D_HIP(hipStreamWaitEvent((hipStream_t)stream, h->copy_done[l][(size_t)best], 0));
+      H2D_HIP(hipStreamWaitEvent((hipStream_t)stream, h->copy_done[l][(size_t)best]->e, 0));
   return 0;
 }
 
