@@ -492,23 +492,48 @@ __device__ __forceinline__ void exact_select(uint32_t (&k)[NS], int32_t (&ix)[NS
   wave_sync_lds();
 }
 
+// Wavefront reductions through DPP lane moves (a few cycles each, against an LDS round trip
+// per step for __shfl_xor): quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror and row_mirror
+// combine each row of 16 lanes in every lane; row_bcast:15 and row_bcast:31 then carry rows 0-2
+// into the last row, and lane 63 holds the result, which readlane makes wave-uniform.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t old, uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROW_MASK, 0xf, false);
+}
+__device__ __forceinline__ float dpp_asf(uint32_t v) { return __uint_as_float(v); }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
+  uint32_t u = __float_as_uint(v);
+  v = fmaxf(v, dpp_asf(dpp_u<0xB1>(u, u)));
+  u = __float_as_uint(v);
+  v = fmaxf(v, dpp_asf(dpp_u<0x4E>(u, u)));
+  u = __float_as_uint(v);
+  v = fmaxf(v, dpp_asf(dpp_u<0x141>(u, u)));
+  u = __float_as_uint(v);
+  v = fmaxf(v, dpp_asf(dpp_u<0x140>(u, u)));
+  u = __float_as_uint(v);
+  v = fmaxf(v, dpp_asf(dpp_u<0x142, 0xa>(u, u)));
+  u = __float_as_uint(v);
+  v = fmaxf(v, dpp_asf(dpp_u<0x143, 0xc>(u, u)));
+  return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(v), 63));
 }
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  v += dpp_asf(dpp_u<0xB1>(0u, __float_as_uint(v)));
+  v += dpp_asf(dpp_u<0x4E>(0u, __float_as_uint(v)));
+  v += dpp_asf(dpp_u<0x141>(0u, __float_as_uint(v)));
+  v += dpp_asf(dpp_u<0x140>(0u, __float_as_uint(v)));
+  v += dpp_asf(dpp_u<0x142, 0xa>(0u, __float_as_uint(v)));
+  v += dpp_asf(dpp_u<0x143, 0xc>(0u, __float_as_uint(v)));
+  return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(v), 63));
 }
+__device__ __forceinline__ uint32_t umax_(uint32_t a, uint32_t b) { return a > b ? a : b; }
 __device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const uint32_t o = (uint32_t)__shfl_xor((int)v, off, 64);
-    v = o > v ? o : v;
-  }
-  return v;
+  v = umax_(v, dpp_u<0xB1>(v, v));
+  v = umax_(v, dpp_u<0x4E>(v, v));
+  v = umax_(v, dpp_u<0x141>(v, v));
+  v = umax_(v, dpp_u<0x140>(v, v));
+  v = umax_(v, dpp_u<0x142, 0xa>(v, v));
+  v = umax_(v, dpp_u<0x143, 0xc>(v, v));
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
 template <typename T>
@@ -588,13 +613,13 @@ __global__ __launch_bounds__(64 * kWaves) void router_kernel(
           if (hit) where = s * 64 + lane;
         }
         const uint64_t hits = __ballot(eq > 0);
-        const int total = __popcll(hits) == 1 ? __shfl(eq, __ffsll((long long)hits) - 1, 64) : 2;
+        const int total = __popcll(hits) == 1 ? __builtin_amdgcn_readlane(eq, __ffsll((long long)hits) - 1) : 2;
         if (total != 1 || best == 0u) {
           exact = true;  // a tie decides membership or order
           break;
         }
         const int owner = __ffsll((long long)hits) - 1;
-        const int pos = __shfl(where, owner, 64);
+        const int pos = __builtin_amdgcn_readlane(where, owner);
         if (lane == 0) ws.sel[r] = pos;
 #pragma unroll
         for (int s = 0; s < NS; ++s) cur[s] = (lane == owner && s == (pos >> 6)) ? 0u : cur[s];
@@ -614,7 +639,7 @@ __global__ __launch_bounds__(64 * kWaves) void router_kernel(
       wv = ws.prob[e];
     }
     float tot = 0.f;
-    for (int j = 0; j < kk; ++j) tot += __shfl(wv, j, 64);  // j-ascending like the reference sum
+    for (int j = 0; j < kk; ++j) tot += __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(wv), j));  // j-ascending like the reference sum
     if (lane < kk) {
       float w = renorm ? wv / tot : wv;
       w = w * scale;
