@@ -109,3 +109,27 @@ extern "C" void ferry_layer_slots(const int64_t* slots, int64_t cap, int64_t lay
     if (key >= 0 && key / experts == layer) lookup[key % experts] = i;
   }
 }
+
+extern "C" int64_t ferry_plan_fetch(int64_t event, int64_t layer, const uint8_t* ids,
+                                    int64_t tokens, int64_t topk, const float* gate_scores,
+                                    int64_t* slots, int64_t cap, int64_t* owner, int64_t* last,
+                                    float* scores, int64_t experts, int64_t* fetches_out,
+                                    int64_t* destinations_out, ferry_h2d* h2d) {
+  if (tokens < 0 || topk <= 0) {
+    ferry::clear_error();
+    ferry::set_error("plan_fetch: bad sizes");
+    return -1;
+  }
+  std::vector<int64_t> sel((size_t)(tokens * topk));
+  for (size_t i = 0; i < sel.size(); ++i) sel[i] = ids[i];
+  const int64_t m = ferry_plan_layer(event, layer, sel.data(), tokens, topk, gate_scores, slots,
+                                     cap, owner, last, scores, experts, fetches_out,
+                                     destinations_out);
+  if (m <= 0 || !h2d) return m;
+  std::vector<int64_t> fs((size_t)m), fk((size_t)m);
+  for (int64_t j = 0; j < m; ++j) {
+    fk[(size_t)j] = fetches_out[3 * j + 1];
+    fs[(size_t)j] = fetches_out[3 * j + 2];
+  }
+  return ferry_h2d_fetch(h2d, fs.data(), fk.data(), m) == 0 ? m : -2;
+}

@@ -33,6 +33,11 @@ class H2DEngine:
                                      ctypes.byref(handle)), 'H2DEngine')
         self._h = handle.value
 
+    @property
+    def handle(self):
+        """The native engine (ferry_h2d*), for ferry_plan_fetch."""
+        return self._h
+
     def fetch(self, slots, keys):
         s, k = _i64(slots), _i64(keys)
         if len(s) != len(k):

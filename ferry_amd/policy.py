@@ -84,8 +84,29 @@ class Controller:
         self.owner = np.full(layers * experts, -1, np.int64)
         self.last = np.zeros(layers * experts, np.int64)
         self.scores = np.zeros((layers, experts), np.float32)
+        self._slots_ptr, self._owner_ptr = self.slots.ctypes.data, self.owner.ctypes.data
+        self._last_ptr, self._scores_ptr = self.last.ctypes.data, self.scores.ctypes.data
+        self._fetch_buf = None
 
     def plan(self, event, layer, selected, origins, gate_scores):
         return plan_layer(event, layer, selected, origins, gate_scores, self.policy, self.slots,
                           self.capacities, self.owner, self.last, self.scores, self.lut,
                           self.masks, self.seconds, self.balance_tol_bps, self.salt)
+
+    def plan_fetch(self, event, layer, ids_ptr, tokens, topk, scores_ptr, h2d_handle):
+        """plan() from raw host pointers (uint8 routing IDs [tokens*topk], float32 scores [E],
+        e.g. the mapped staging buffer) with the misses' copies queued on the fetch engine in
+        the same native call.  Returns fetches[m, 3] (a view of a buffer reused by the next
+        call) and the per-rank fetch counts."""
+        experts = self.spec.experts
+        if self._fetch_buf is None:
+            self._fetch_buf = np.empty((experts, 3), np.int64)
+        m = lib().ferry_plan_fetch(event, layer, ids_ptr, tokens, topk, scores_ptr,
+                                   self._slots_ptr, int(self.capacities[0]), self._owner_ptr,
+                                   self._last_ptr, self._scores_ptr, experts,
+                                   self._fetch_buf.ctypes.data, None, h2d_handle)
+        if m == -1:
+            raise AssertionError(last_error())
+        if m < 0:
+            raise RuntimeError(f'plan_fetch: {last_error()}')
+        return self._fetch_buf[:m], np.array([m], np.int64)

@@ -147,36 +147,48 @@ class OffloadRuntime:
         t_sync = time.perf_counter_ns()
         d2h.synchronize()
         t_ready = time.perf_counter_ns()
-        host = stage_host.numpy()
-        ids = host[4 * E:].astype(np.int64).reshape(T, k)
         if frequency:
-            scores = host[:4 * E].view(np.float32).copy()
+            # the planner reads the IDs and scores where the history kernel wrote them and
+            # queues the misses' copies in the same native call (with timing on, the copies
+            # are queued separately, after an event that marks their start on the copy stream)
+            fetches, counts = self.controller.plan_fetch(
+                self.event, layer, self._stage_ptr + 4 * E, T, k, self._stage_ptr,
+                None if self.timing else self.h2d.handle)
+            t_plan = time.perf_counter_ns()
+            if self.timing and len(fetches):
+                copy_stream = self.h2d.stream
+                ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+                ev[0].record(copy_stream)
+                self.h2d.fetch(fetches[:, 2], fetches[:, 1])
         else:
             self.history.update(layer, tail_host.numpy())
             scores = self.history.scores(layer)
-        origins = np.zeros(T, np.int64)
-        fetches, destinations, counts = self.controller.plan(self.event, layer, ids, origins, scores)
+            ids = stage_host.numpy()[4 * E:].astype(np.int64).reshape(T, k)
+            fetches, _, counts = self.controller.plan(self.event, layer, ids, np.zeros(T, np.int64),
+                                                      scores)
+            t_plan = time.perf_counter_ns()
+            if self.timing and len(fetches):
+                copy_stream = self.h2d.stream
+                ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+                ev[0].record(copy_stream)
+            self.h2d.fetch(fetches[:, 2], fetches[:, 1])
+        t_fetch = time.perf_counter_ns()
         self.fetches_per_rank += counts
         if self.event >= spec.layers:
             self.decode_fetches_per_rank += counts
-        fetch_slots = fetches[:, 2]
+        fetch_slots = fetches[:, 2].copy()
+        missing_keys = fetches[:, 1] - layer * E
         timing = self.timing and len(fetch_slots) > 0
         if timing:
-            copy_stream = self.h2d.stream
-            ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
-            ev[0].record(copy_stream)
-        t_plan = time.perf_counter_ns()
-        self.h2d.fetch(fetch_slots, fetches[:, 1])
-        t_fetch = time.perf_counter_ns()
-        if timing:
             ev[1].record(copy_stream)
+        ids = stage_host.numpy()[4 * E:].astype(np.int64).reshape(T, k)
 
         # 4. experts: resident first, then the fetched ones
         slot_of = layer_slots(self.controller.slots[0], self.cap, layer, E)
         active = np.zeros(E, bool)
         active[ids.reshape(-1)] = True
         missing = np.zeros(E, bool)
-        missing[fetches[:, 1] - layer * E] = True
+        missing[missing_keys] = True
         resident_list = np.flatnonzero(active & ~missing)
         missing_list = np.flatnonzero(missing)
         slot32 = slot_of.astype(np.int32)
@@ -208,7 +220,7 @@ class OffloadRuntime:
             h = self.host_ns
             h['enqueue_before_wait'] += t_sync - t_enter
             h['wait_for_ids'] += t_ready - t_sync
-            h['plan'] += t_plan - t_ready
+            h['plan'] += t_plan - t_ready       # with frequency scores: plan + fetch enqueue
             h['fetch_enqueue'] += t_fetch - t_plan
             h['enqueue_after_fetch'] += time.perf_counter_ns() - t_fetch
         return out

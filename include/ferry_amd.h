@@ -160,6 +160,22 @@ int64_t ferry_h2d_copies(const ferry_h2d* h);
 /* the engine's copy stream (for event timing by the caller) */
 void* ferry_h2d_stream(ferry_h2d* h);
 
+/*
+ * Plan one layer call and enqueue its fetch in one host call: the steps of ferry/runtime.py:64-89
+ * between the routing read-back and the expert computation (policy.plan_layer of
+ * ferry/policy.py:130-194, then H2DEngine.fetch of ferry/h2d.py / expert_ops.cpp:94-142).
+ * ids are the routing IDs as uint8 [tokens*topk] and gate_scores the layer's float32 scores,
+ * e.g. straight from the mapped staging buffer that ferry_history_update writes; the other
+ * arguments are those of ferry_plan_layer, plus the fetch engine (nullable: plan only).
+ * Returns the number of misses m (fetches_out rows as in ferry_plan_layer, their copies queued),
+ * -1 when the misses exceed the admission capacity, -2 when the fetch fails; errors set
+ * ferry_last_error().
+ */
+int64_t ferry_plan_fetch(int64_t event, int64_t layer, const uint8_t* ids, int64_t tokens,
+                         int64_t topk, const float* gate_scores, int64_t* slots, int64_t cap,
+                         int64_t* owner, int64_t* last, float* scores, int64_t experts,
+                         int64_t* fetches_out, int64_t* destinations_out, ferry_h2d* h2d);
+
 #ifdef __cplusplus
 }
 #endif

@@ -118,6 +118,40 @@ def test_product_planner_golden_trace():
     assert np.array_equal(ctl.slots[0], d['final_slots'])
 
 
+def test_fused_plan_fetch_matches_oracle_traces():
+    """ferry_plan_fetch (uint8 IDs and float32 scores from raw host pointers, plan only when no
+    fetch engine is given) makes the oracle's decisions and state updates."""
+    from ferry_amd.policy import Controller
+    from ferry_amd.quota import Topology
+    rng = np.random.default_rng(7)
+    for trial in range(8):
+        L, E = int(rng.integers(1, 4)), int(rng.integers(2, 200))
+        cap = int(rng.integers(1, 2 * E))
+        ctl = Controller(_Spec(L, E), [cap], 'ferry', Topology.uniform(1, E))
+        ref = PlannerRef(L, E, cap)
+        for ev in range(60):
+            layer = int(rng.integers(0, L))
+            k = int(rng.integers(1, min(E, 8) + 1))
+            T = int(rng.integers(1, 6))
+            sel = np.stack([rng.choice(E, k, replace=False) for _ in range(T)])
+            gs = (rng.integers(0, 5, E) / 4).astype(np.float32)
+            try:
+                f_ref, _ = ref.plan(ev, layer, sel, gs)
+            except AssertionError:
+                f_ref = None
+            ids = np.ascontiguousarray(sel.reshape(-1).astype(np.uint8))
+            try:
+                f, counts = ctl.plan_fetch(ev, layer, ids.ctypes.data, T, k, gs.ctypes.data, None)
+            except AssertionError:
+                f = None
+            assert (f is None) == (f_ref is None)
+            if f is None:
+                break
+            assert np.array_equal(f, f_ref) and counts.tolist() == [len(f)]
+            assert np.array_equal(ctl.slots[0], ref.slots)
+            assert np.array_equal(ctl.owner, ref.owner) and np.array_equal(ctl.last, ref.last)
+
+
 def test_product_planner_overflow_raises_assertion():
     from ferry_amd.policy import Controller
     from ferry_amd.quota import Topology
