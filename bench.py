@@ -141,12 +141,13 @@ def run_decode(args, device):
     ks['kernels'] = {name: ops.timing_summary(name) for name in
                      ('router_kernel', 'history_kernel', 'layout_single', 'ffn_up_skinny',
                       'ffn_down_skinny', 'combine_kernel')}
+    fetch_ms, exposed_ms, overlap_ms = rt.fetch_timing()   # reads the launch log: before disabling
     ops.timing_enable(False)
-    fetch_ms, exposed_ms = rt.fetch_timing()
     elapsed = t1 - t0
     tokens = w.tokens * args.steps
     res = dict(workload=w, elapsed=elapsed, instrumented_elapsed=t3 - t2, tokens=tokens,
                copies=copies, kernels=ks, fetch_ms=fetch_ms, exposed_ms=exposed_ms,
+               overlap_ms=overlap_ms,
                expert_bytes=spec.expert_bytes, samples=stream[args.warmup:],
                host_ns=dict(rt.host_ns))
     rt.close()
@@ -260,8 +261,8 @@ def run_decode_loop(args, device):
     up = ops_timing.timing_summary('ffn_up_skinny')[1] + ops_timing.timing_summary('ffn_tiled_up')[1]
     down = (ops_timing.timing_summary('ffn_down_skinny')[1]
             + ops_timing.timing_summary('ffn_tiled_down')[1])
+    fetch_ms, exposed_ms, overlap_ms = rt.fetch_timing()   # reads the launch log: before disabling
     ops_timing.timing_enable(False)
-    fetch_ms, exposed_ms = rt.fetch_timing()
     copies = rt.h2d.copies - prefill_copies
     calls = args.loop_steps * L
     res = dict(
@@ -273,7 +274,8 @@ def run_decode_loop(args, device):
         misses_per_layer_step=copies / calls,
         h2d_gbs=copies * spec.expert_bytes / (fetch_ms * 1e-3) / 1e9 if fetch_ms else None,
         fetch_ms_per_layer_step=fetch_ms / calls,
-        fetch_hidden_frac=1.0 - exposed_ms / fetch_ms if fetch_ms else None,
+        fetch_hidden_frac=overlap_ms / fetch_ms if fetch_ms else None,
+        fetch_exposed_frac=exposed_ms / fetch_ms if fetch_ms else None,
         ffn_ms_per_layer_step=(up + down) / calls,
         hidden_cap=min(1.0, (up + down) / fetch_ms) if fetch_ms else None,
         eviction_state_sha1=digest.hexdigest())
@@ -345,7 +347,9 @@ def main():
     value = dec['tokens'] / dec['elapsed']
     fetch_bytes = dec['copies'] * dec['expert_bytes']
     h2d_gbs = fetch_bytes / (dec['fetch_ms'] * 1e-3) / 1e9 if dec['fetch_ms'] else None
-    hidden = 1.0 - dec['exposed_ms'] / dec['fetch_ms'] if dec['fetch_ms'] else None
+    # fraction of the fetch time covered by compute kernels queued while the misses copy
+    hidden = dec['overlap_ms'] / dec['fetch_ms'] if dec['fetch_ms'] else None
+    exposed = dec['exposed_ms'] / dec['fetch_ms'] if dec['fetch_ms'] else None
     compute_ms = ks['up_ms'] + ks['down_ms']
     ratio = traffic_ratio()
     bytes_per_launch = ks['up'] / max(1, ks['up_launches'])
@@ -373,6 +377,7 @@ def main():
                     h2d_gbs=h2d_gbs, h2d_frac=(h2d_gbs / PCIE_PEAK_GBS) if h2d_gbs else None,
                     fetch_ms_per_step=dec['fetch_ms'] / args.steps,
                     fetch_hidden_frac=hidden,
+                    fetch_exposed_frac=exposed,
                     kernel_us_per_step={n: v[1] / args.steps * 1e3 for n, v in ks['kernels'].items()},
                     host_us_per_step={n: v / args.steps / 1e3 for n, v in dec['host_ns'].items()},
                     instrumented_ms_per_step=dec['instrumented_elapsed'] / args.steps * 1e3,

@@ -47,6 +47,8 @@ SIGNATURES = [
     ('ferry_h2d_copies', _i64, [_c_p]),
     ('ferry_h2d_stream', _c_p, [_c_p]),
     ('ferry_timing_enable', ctypes.c_int, [_i32]),
+    ('ferry_timing_mark', _i64, []),
+    ('ferry_timing_range', ctypes.c_int, [_i64, _i64, _c_p]),
     ('ferry_timing_summary', ctypes.c_int,
      [ctypes.c_char_p, ctypes.POINTER(_i64), ctypes.POINTER(ctypes.c_double)]),
 ]

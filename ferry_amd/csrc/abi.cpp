@@ -84,6 +84,28 @@ extern "C" int ferry_timing_summary(const char* kernel, int64_t* launches, doubl
   return 0;
 }
 
+// Number of launches recorded so far: a position in the timing log.
+extern "C" int64_t ferry_timing_mark(void) {
+  std::lock_guard<std::mutex> lock(ferry::g_timing_mu);
+  return (int64_t)ferry::g_launches.size();
+}
+
+// Summed duration in ms of the timed launches at log positions [begin, end) (waits for them).
+extern "C" int ferry_timing_range(int64_t begin, int64_t end, double* total_ms) {
+  std::lock_guard<std::mutex> lock(ferry::g_timing_mu);
+  const int64_t n = (int64_t)ferry::g_launches.size();
+  double ms = 0.0;
+  for (int64_t i = begin < 0 ? 0 : begin; i < end && i < n; ++i) {
+    const auto& l = ferry::g_launches[(size_t)i];
+    if (hipEventSynchronize(l.stop) != hipSuccess) return 3;
+    float t = 0.f;
+    if (hipEventElapsedTime(&t, l.start, l.stop) != hipSuccess) return 3;
+    ms += t;
+  }
+  *total_ms = ms;
+  return 0;
+}
+
 extern "C" const char* ferry_last_error(void) { return ferry::g_last_error.c_str(); }
 
 extern "C" int32_t ferry_abi_version(void) { return 2; }

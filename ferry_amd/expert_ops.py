@@ -37,6 +37,19 @@ def timing_summary(kernel):
     return int(n.value), float(ms.value)
 
 
+def timing_mark():
+    """Position in the per-launch timing log (the number of launches recorded so far)."""
+    return int(lib().ferry_timing_mark())
+
+
+def timing_range(begin, end):
+    """Summed ms of the timed launches at log positions [begin, end)."""
+    import ctypes
+    ms = ctypes.c_double()
+    check(lib().ferry_timing_range(int(begin), int(end), ctypes.byref(ms)), 'timing_range')
+    return float(ms.value)
+
+
 def current_stream(device=None):
     return torch.cuda.current_stream(device).cuda_stream
 

@@ -198,10 +198,13 @@ class OffloadRuntime:
             started = time.perf_counter_ns()
             self.h2d.wait_host(fetch_slots)
             self.serial_wait_ns += time.perf_counter_ns() - started
+        mark = self.ops.timing_mark() if timing else 0
         if len(resident_list):
             self.h2d.wait_stream(slot_of[resident_list], stream)
             self._ffn(common, resident_list, slot32, buf, stream, counts_e)
         shared_out = shared(common[1], out=self._shared_out(T)) if shared is not None else None
+        # the launches between the two marks are the compute queued while the misses copy
+        overlap_marks = (mark, self.ops.timing_mark() if timing else 0)
         if len(missing_list):
             if timing:
                 ev[2].record(stream)
@@ -211,7 +214,7 @@ class OffloadRuntime:
             self._ffn(common, missing_list, slot32, buf, stream, counts_e)
         self.h2d.mark_used(slot_of[np.flatnonzero(active)], stream)
         if timing:
-            self.timings.append(ev)
+            self.timings.append((ev, overlap_marks))
         self.event += 1
 
         # 5. combine (+ the shared experts' output)
@@ -250,11 +253,19 @@ class OffloadRuntime:
             self.kernel_bytes['launches'] += 1
 
     def fetch_timing(self):
-        """(total fetch ms, exposed wait ms) over the layer calls recorded with timing=True."""
+        """(total fetch ms, exposed wait ms, overlapped compute ms) over the layer calls recorded
+        with timing=True.  fetch: first copy start to last copy end on the copy stream.  exposed:
+        how long the compute stream waited for the copies.  overlapped: per call, the kernel time
+        of the resident experts (and shared experts) queued while the misses copy, at most that
+        call's fetch time; it needs the library's per-launch timing (expert_ops.timing_enable)."""
         torch.cuda.synchronize(self.device)
-        fetch = sum(e[0].elapsed_time(e[1]) for e in self.timings)
-        exposed = sum(max(0.0, e[2].elapsed_time(e[3])) for e in self.timings)
-        return fetch, exposed
+        fetch = exposed = overlapped = 0.0
+        for ev, (m0, m1) in self.timings:
+            f = ev[0].elapsed_time(ev[1])
+            fetch += f
+            exposed += max(0.0, ev[2].elapsed_time(ev[3]))
+            overlapped += min(f, self.ops.timing_range(m0, m1))
+        return fetch, exposed, overlapped
 
     def close(self):
         if self.h2d is not None:

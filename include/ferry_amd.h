@@ -24,6 +24,18 @@ const char* ferry_last_error(void);
 /* ABI version of this library (bumped on any signature change). */
 int32_t ferry_abi_version(void);
 
+/*
+ * Per-launch kernel timing (a measurement aid with no reference counterpart): when enabled,
+ * every kernel launch of the library is bracketed by its own start/stop HIP events.
+ * ferry_timing_enable clears the log; ferry_timing_summary sums the launches of one kernel;
+ * ferry_timing_mark returns the current log position and ferry_timing_range sums the launches
+ * between two positions.  The sums wait for the launches they cover.
+ */
+int ferry_timing_enable(int32_t enable);
+int ferry_timing_summary(const char* kernel, int64_t* launches, double* total_ms);
+int64_t ferry_timing_mark(void);
+int ferry_timing_range(int64_t begin, int64_t end, double* total_ms);
+
 enum { FERRY_BF16 = 0, FERRY_F32 = 1 };
 
 /*
