@@ -583,11 +583,17 @@ __global__ __launch_bounds__(kTiledThreads, 1) void ffn_tiled(FfnArgs a) {
       if (more) {
         wait_vmcnt0();   // this wavefront's loads of stage kt+1 landed
         wg_barrier();    // ... everyone's; and stage kt is no longer read by anyone
-        if (kt + 2 < KT) issue(kt + 2);  // stage kt+2 into the buffer stage kt just freed
+        // stage kt+2 into the buffer stage kt just freed.  The two wavefronts of a SIMD (wm 0
+        // and 1) issue their direct loads one MFMA group apart, so that one runs its MFMAs
+        // while the other waits for the address unit to take its loads.
+        if (kt + 2 < KT && wm == 0) issue(kt + 2);
         rd(kt + 1, 0, f0a, f0b);
       }
       mma(f1a, f1b);
-      if (more) lds_wait(f0a, f0b);
+      if (more) {
+        if (kt + 2 < KT && wm == 1) issue(kt + 2);
+        lds_wait(f0a, f0b);
+      }
     }
     __syncthreads();  // all fragment reads done before the staging area is reused
 
