@@ -315,12 +315,12 @@ __device__ __forceinline__ void down_skinny(const FfnArgs& a, int li, int64_t st
     }
   }
 }
-// Experts with up to 16*MTMAX rows, 64 hidden rows per workgroup: one wavefront row group of
-// four tiles with K split four ways for up to 16 rows, four single-tile groups with the full K
-// above (the activation fragments of 2 or 4 M tiles then serve one weight fragment each).
+// Experts with up to 16*MTMAX rows, 64 hidden rows per workgroup: up to 16 rows, one wavefront
+// row group of four tiles with K split four ways; above, two row groups of two tiles with K
+// split two ways, so that each activation fragment serves two weight fragments.
 template <int MTMAX>
 __global__ __launch_bounds__(256) void ffn_down_skinny(FfnArgs a) {
-  __shared__ floatx4 red[4 * 4 * 64];
+  __shared__ floatx4 red[(MTMAX >= 4 ? 2 : 1) * 1024];
   const int li = blockIdx.y;
   if (li >= a.list.n) return;
   const int e = a.list.expert[li];
@@ -328,9 +328,9 @@ __global__ __launch_bounds__(256) void ffn_down_skinny(FfnArgs a) {
   const int n = (int)(a.starts[e + 1] - start);
   if (n == 0 || n > 16 * MTMAX) return;
   if (MTMAX >= 4 && n > 32)
-    down_skinny<4, 1, 4>(a, li, start, n, blockIdx.x, red);
+    down_skinny<2, 2, 4>(a, li, start, n, blockIdx.x, red);
   else if (MTMAX >= 2 && n > 16)
-    down_skinny<4, 1, 2>(a, li, start, n, blockIdx.x, red);
+    down_skinny<2, 2, 2>(a, li, start, n, blockIdx.x, red);
   else
     down_skinny<1, 4, 1>(a, li, start, n, blockIdx.x, red);
 }
