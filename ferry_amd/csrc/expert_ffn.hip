@@ -8,12 +8,15 @@
 // are "NT" (both operands contiguous along K), which is the native operand order of the
 // CDNA4 MFMA instructions used here.  The bf16 rounding points of the reference are kept.
 //
-// Two kernel families, selected per expert by its row count n_e:
-//  * skinny (n_e <= 64, decode): bandwidth-bound.  Weight fragments go straight from HBM
-//    into MFMA B-operand registers (16 B per lane, no LDS) and are reused across up to four
-//    16-row M tiles; x rows come from L2.  v_mfma_f32_16x16x32_bf16.  A workgroup owns
-//    16*NT*NC weight rows (NT column groups of NC tiles) and splits K over 4/NT wavefronts;
-//    the partial sums meet in LDS.
+// Three kernel schemes, selected per expert by its row count n_e:
+//  * skinny (n_e <= 16, decode): bandwidth-bound.  A workgroup owns 16 (phase 1) or 64
+//    (phase 2) weight rows and splits K over its four wavefronts; the partial sums meet in
+//    LDS.  The weights are loaded 8 rows x 128 B per instruction and turned into MFMA B
+//    fragments through a small per-wavefront LDS tile; x rows come from L2.
+//    v_mfma_f32_16x16x32_bf16.
+//  * mid (16 < n_e <= 64, prefill): bandwidth-bound.  A workgroup owns 64 output columns over
+//    the full K; the expert's token rows are staged once per workgroup in LDS, the weights
+//    stream into MFMA B registers.  Launched together with the skinny experts of a list.
 //  * tiled (n_e > 64, prefill): MFMA-bound.  Persistent workgroups walk a device-computed
 //    list of 256x256 output tiles; A (gathered x rows / activation rows) and B (weight rows)
 //    tiles of 64 along K are staged by direct global->LDS loads into a swizzled,
@@ -24,6 +27,8 @@
 
 #include "common.h"
 
+#include <type_traits>
+
 namespace ferry {
 namespace {
 
@@ -33,7 +38,7 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kListMax = 256;   // experts per launch (longer lists are split by the host)
-constexpr int kSkinnyMax = 64;  // rows handled by the skinny kernels (4 tiles of 16)
+constexpr int kSkinnyMax = 64;  // rows handled by the skinny and mid kernels (4 tiles of 16)
 
 struct ExpertList {
   int32_t n;
@@ -127,14 +132,15 @@ __device__ __forceinline__ void wg_barrier() {
 // Skinny kernels
 // =============================================================================================
 
-// Skinny kernels (experts with at most 64 rows: decode, and the small experts of a prefill).
-// They are bound by the weight bytes.  Each lane streams 16-byte weight fragments straight
-// into MFMA B-operand registers, the loads of UNR K steps issued before their MFMAs.  A
-// wavefront computes NC 16-column tiles from the same activation fragment, so per K step it
-// issues NC (phase 1: 2 NC) weight loads and MT activation loads: the activation rows are
-// L2 hits, and the fewer of them per weight byte, the closer the address units get to the
-// HBM rate.  The four wavefronts of a workgroup split K into contiguous ranges of 32-element
-// steps; their partial sums are added in LDS in a fixed order.
+// Skinny kernels (experts with at most 16 rows: decode, and the smallest experts of a prefill).
+// They are bound by the weight bytes.  The four wavefronts of a workgroup split K into
+// contiguous ranges of 32-element steps; their partial sums are added in LDS in a fixed order.
+// up_skinny / down_skinny below load the weights in MFMA fragment order (each lane 16 bytes
+// straight into B-operand registers, the loads of UNR K steps issued before their MFMAs); they
+// serve shapes whose per-wavefront K range is not a multiple of 64.  up_skinny_t /
+// down_skinny_t load 128 bytes of a row per 8 lanes instead, which the memory system serves
+// at a higher rate (every 128-byte line fetched by one instruction, not two), and reorder the
+// data into fragments through LDS.
 
 template <int U, int MT, int NB>
 __device__ __forceinline__ void skinny_batch(const bf16_t* const (&pb)[NB], const bf16_t* const (&px)[MT],
@@ -248,23 +254,82 @@ __device__ __forceinline__ void up_skinny(const FfnArgs& a, int li, int64_t star
     }
   }
 }
-// Experts with up to 16*MTMAX rows; each workgroup takes the smallest M-tile count that holds
-// its expert, so experts of all sizes share one launch.  16 intermediate columns per workgroup.
-template <int MTMAX>
-__global__ __launch_bounds__(256) void ffn_up_skinny(FfnArgs a) {
-  __shared__ floatx4 red[4 * MTMAX * 2 * 64];
-  const int li = blockIdx.y;
-  if (li >= a.list.n) return;
-  const int e = a.list.expert[li];
-  const int64_t start = a.starts[e];
-  const int n = (int)(a.starts[e + 1] - start);
-  if (n == 0 || n > 16 * MTMAX) return;
-  if (MTMAX >= 4 && n > 32)
-    up_skinny<1, 1, 4>(a, li, start, n, blockIdx.x, red);
-  else if (MTMAX >= 2 && n > 16)
-    up_skinny<1, 1, 2>(a, li, start, n, blockIdx.x, red);
-  else
-    up_skinny<1, 1, 1>(a, li, start, n, blockIdx.x, red);
+// Phase 1, skinny, at most 16 rows (decode): one workgroup = (expert, 16 intermediate columns),
+// K split over the four wavefronts as above, but the weights are loaded 128 bytes of a row per
+// lane group (8 rows x 128 B per instruction, every 128-byte line fetched by one instruction)
+// rather than in the MFMA fragment order (16 rows x 64 B, each line fetched by two).  Each
+// wavefront turns them into B fragments through its own 4 KiB LDS tile, one K chunk of 64 at a
+// time: 32 rows (gate 0-15, up 16-31) x 128 B, chunk c of row r at slot c ^ ((r >> 1) & 7), which
+// keeps the fragment reads free of bank conflicts.  NCH chunks of loads are in flight.
+template <int NCH>
+__device__ __forceinline__ void up_skinny_t(const FfnArgs& a, int li, int64_t start, int n, int bx,
+                                            floatx4* red, char* tile) {
+  const int H = (int)a.H;
+  const int lane = threadIdx.x & 63, ks = threadIdx.x >> 6;
+  const int i0 = bx * 16;
+  const bf16_t* wg = a.cache + (int64_t)a.list.slot[li] * 3 * a.H * a.I;
+  const bf16_t* wu = wg + a.H * a.I;
+  const int lr = lane >> 3, lc = lane & 7, r16 = lane & 15, kg = (lane >> 4) * 8;
+  // row group g: rows 8g + lr of the tile (g = 0, 1 gate, 2, 3 up)
+  const bf16_t* prow[4];
+  uint32_t woff[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    prow[g] = (g < 2 ? wg : wu) + (int64_t)(i0 + 8 * (g & 1) + lr) * H + lc * 8;
+    const int row = 8 * g + lr;
+    woff[g] = (uint32_t)(row * 128 + ((lc ^ ((row >> 1) & 7)) << 4));
+  }
+  // fragment reads, K step s of a chunk: row r16 (gate) or 16 + r16 (up), chunk 4s + lane/16
+  uint32_t roff[2][2];
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int row = 16 * j + r16;
+      roff[st][j] = (uint32_t)(row * 128 + (((4 * st + (lane >> 4)) ^ ((row >> 1) & 7)) << 4));
+    }
+  const bool okx = r16 < n;
+  const bf16_t* px = a.x + (okx ? a.rows[start + r16] : 0) * a.H + kg;
+  floatx4 acc[2] = {floatx4{0, 0, 0, 0}, floatx4{0, 0, 0, 0}};
+  const bf16x8 zero8 = {};
+  auto batch = [&](int k0, auto nch) {
+    constexpr int N = decltype(nch)::value;
+    u32x4 w[N][4];
+#pragma unroll
+    for (int ch = 0; ch < N; ++ch)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) w[ch][g] = *reinterpret_cast<const u32x4*>(prow[g] + k0 + 64 * ch);
+    bf16x8 xa[2 * N];
+#pragma unroll
+    for (int st = 0; st < 2 * N; ++st) xa[st] = okx ? load8(px + k0 + 32 * st) : zero8;
+#pragma unroll
+    for (int ch = 0; ch < N; ++ch) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) *reinterpret_cast<u32x4*>(tile + woff[g]) = w[ch][g];
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const bf16x8 bg = *reinterpret_cast<const bf16x8*>(tile + roff[st][0]);
+        const bf16x8 bu = *reinterpret_cast<const bf16x8*>(tile + roff[st][1]);
+        acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[2 * ch + st], bg, acc[0], 0, 0, 0);
+        acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[2 * ch + st], bu, acc[1], 0, 0, 0);
+      }
+    }
+  };
+  const int kb = ks * (H / 4), ke = kb + H / 4;   // H / 4 is a multiple of 64
+  int k0 = kb;
+  for (; k0 + 64 * NCH <= ke; k0 += 64 * NCH) batch(k0, std::integral_constant<int, NCH>{});
+  for (; k0 < ke; k0 += 64) batch(k0, std::integral_constant<int, 1>{});
+  floatx4 accm[1][2] = {{acc[0], acc[1]}};
+  if (!skinny_reduce<4, 1>(accm, ks, 0, lane, red)) return;
+  const int col = i0 + (lane & 15);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = (lane >> 4) * 4 + q;
+    if (r < n) {
+      const float g = bf16r(accm[0][0][q]), u = bf16r(accm[0][1][q]);
+      a.act[(start + r) * a.I + col] = f32_to_bf16(silu_mul(g, u));
+    }
+  }
 }
 
 // Phase 2, skinny: one workgroup = (expert, 16*NT*NC hidden rows), laid out as phase 1.
@@ -315,24 +380,314 @@ __device__ __forceinline__ void down_skinny(const FfnArgs& a, int li, int64_t st
     }
   }
 }
-// Experts with up to 16*MTMAX rows, 64 hidden rows per workgroup: up to 16 rows, one wavefront
-// row group of four tiles with K split four ways; above, two row groups of two tiles with K
-// split two ways, so that each activation fragment serves two weight fragments.
+// 16-byte global load into registers (saddr + 32-bit lane byte offset) as inline asm: the
+// compiler does not track it, so the registers are read only after vmcnt_tie names them.
+__device__ __forceinline__ void gload16(bf16x8& v, const void* sbase, uint32_t voff) {
+  asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(v) : "v"(voff), "s"(sbase) : "memory");
+}
+// wait until at most N vector loads are outstanding; the registers named are those loads'
+// destinations, tied so that no use of them is scheduled before the wait
+template <int N>
+__device__ __forceinline__ void vmcnt_tie(bf16x8 (&r)[8]) {
+  asm volatile("s_waitcnt vmcnt(%8)"
+               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]),
+                 "+v"(r[6]), "+v"(r[7])
+               : "n"(N)
+               : "memory");
+}
+template <int N>
+__device__ __forceinline__ void vmcnt_tie(bf16x8 (&r)[4]) {
+  asm volatile("s_waitcnt vmcnt(%4)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]) : "n"(N) : "memory");
+}
+
+// =============================================================================================
+// Mid kernels
+// =============================================================================================
+
+// Experts with 17-64 rows (prefill).  The skinny kernels read an expert's token rows once per
+// 16 output columns, which at 64 rows is twice the weight bytes; here a workgroup covers 64
+// columns and reads them once.  One workgroup = (expert, 64 output columns), four wavefronts,
+// each a 16-column group over the full K (phase 1: its 16 gate and 16 up columns).  The token
+// rows are staged into LDS in K chunks of 128 elements by direct loads (two buffers, every
+// wavefront moving a quarter of each chunk); the weights, read exactly once, stream straight
+// into MFMA B registers one chunk ahead.  Rows are held in 16-row M tiles (MT of them).
+//
+// LDS row layout: a chunk row is 256 B = 16 chunks of 8 elements; chunk j of row r sits at
+// slot j ^ (r & 15), so the A-fragment read (16 rows x one chunk per 16 lanes) touches every
+// bank once.
+constexpr int kMidKC = 128;                   // K elements per staged chunk
+constexpr int kMidRowBytes = kMidKC * 2;      // 256
+constexpr int kMidBuf = 64 * kMidRowBytes;    // 16 KiB per buffer (64 rows)
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory"); }
+
+// MODE 0: x rows, gate/up weights, SwiGLU into act.  MODE 1: act rows, down weights, routing
+// weight, into out.
+template <int MODE, int MT>
+__device__ __forceinline__ void ffn_mid_body(const FfnArgs& a, int li, int64_t start, int n,
+                                             int bx, char* xs) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int K = (int)(MODE == 0 ? a.H : a.I);
+  const int C = K / kMidKC;
+  const uint32_t lds0 = lds_addr(xs);
+  // token-row staging: direct load q (< 4 MT) moves rows 4q .. 4q+3 of a chunk (16 lanes per
+  // row); this wavefront issues q = MT wave .. MT wave + MT - 1
+  const char* xbase = reinterpret_cast<const char*>(MODE == 0 ? a.x : a.act);
+  uint32_t xoff[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+    const int r = 4 * (MT * wave + i) + (lane >> 4);
+    const int rr = r < n ? r : 0;   // rows past the expert's last load a valid row
+    const uint32_t t = MODE == 0 ? (uint32_t)a.rows[start + rr] : (uint32_t)(start + rr);
+    xoff[i] = t * (uint32_t)(K * 2) + (uint32_t)(((lane & 15) ^ (r & 15)) * 16);
+  }
+  // chunks past the last one restage the last chunk into the buffer nobody reads any more
+  auto stage = [&](int c) {
+    const int cc = c < C ? c : C - 1;
+    const uint32_t dst = lds0 + (uint32_t)((c & 1) * kMidBuf + MT * wave * 1024);
+#pragma unroll
+    for (int i = 0; i < MT; ++i) dma16(xbase + cc * kMidRowBytes, xoff[i], dst + (uint32_t)(i * 1024));
+  };
+  // this wavefront's columns col0 .. col0+16
+  const int col0 = bx * 64 + wave * 16;
+  const int r16 = lane & 15, kg = (lane >> 4) * 8;
+  const bf16_t* slot = a.cache + (int64_t)a.list.slot[li] * 3 * a.H * a.I;
+  constexpr int NB = MODE == 0 ? 2 : 1;
+  // weight rows of this lane (wave-uniform base + 32-bit lane offset): gate then up, or down
+  const bf16_t* wbase = uniform_ptr(slot + (MODE == 0 ? (int64_t)col0 * a.H
+                                                      : 2 * a.H * a.I + (int64_t)col0 * a.I));
+  uint32_t woff[NB];
+  woff[0] = (uint32_t)((r16 * K + kg) * 2);
+  if (MODE == 0) woff[NB - 1] = (uint32_t)((a.H * a.I + (int64_t)r16 * K + kg) * 2);
+  floatx4 acc[MT][NB];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[mt][j] = floatx4{0, 0, 0, 0};
+  // A fragment of M tile mt, step s: row mt*16 + r16, chunk 4s + lane/16 at slot chunk ^ r16
+  uint32_t aoff[4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st)
+    aoff[st] = (uint32_t)(r16 * kMidRowBytes + (((4 * st + (lane >> 4)) ^ r16) * 16));
+  // weights of chunk c: w[st * NB + j] = 16 bytes of row j, K step st (chunks past the last
+  // reload the last one)
+  constexpr int NW = 4 * NB;
+  bf16x8 wb[2][NW];
+  auto wload = [&](int c, bf16x8 (&w)[NW]) {
+    const int cc = c < C ? c : C - 1;
+    const char* b = reinterpret_cast<const char*>(wbase) + cc * kMidRowBytes;
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+      for (int j = 0; j < NB; ++j) gload16(w[st * NB + j], b + st * 64, woff[j]);
+  };
+  // Every chunk issues, in this order, the direct loads of the next chunk's token rows and the
+  // next chunk's weight loads, so the counts behind each wait are fixed: the weights of chunk c
+  // are older than MT + 4 NB loads, the token rows of chunk c+1 older than 4 NB.
+  auto chunk = [&](int c, auto par) {
+    constexpr int P = decltype(par)::value;   // c % 2
+    wg_barrier();   // chunk c staged by every wavefront; chunk c-1's buffer no longer read
+    stage(c + 1);
+    wload(c + 1, wb[1 - P]);
+    vmcnt_tie<MT + NW>(wb[P]);
+    const char* xb = xs + P * kMidBuf;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      bf16x8 xa[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        xa[mt] = *reinterpret_cast<const bf16x8*>(xb + mt * 16 * kMidRowBytes + aoff[st]);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+          acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[mt], wb[P][st * NB + j], acc[mt][j], 0, 0, 0);
+    }
+    wait_vmcnt<NW>();   // this wavefront's share of chunk c+1 landed
+  };
+  stage(0);
+  wload(0, wb[0]);
+  wait_vmcnt<NW>();
+  for (int c = 0; c < C; c += 2) {
+    chunk(c, std::integral_constant<int, 0>{});
+    if (c + 1 < C) chunk(c + 1, std::integral_constant<int, 1>{});
+  }
+  // the loads past the last chunk are never used: hold their registers (and the LDS) until
+  // they landed
+  vmcnt_tie<0>(wb[0]);
+  vmcnt_tie<0>(wb[1]);
+  // 16x16 accumulator layout: column = lane & 15, rows (lane >> 4) * 4 + [0, 4)
+  const int col = col0 + (lane & 15);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int r = mt * 16 + (lane >> 4) * 4 + q;
+      if (r < n) {
+        if (MODE == 0) {
+          const float g = bf16r(acc[mt][0][q]), u = bf16r(acc[mt][NB - 1][q]);
+          a.act[(start + r) * a.I + col] = f32_to_bf16(silu_mul(g, u));
+        } else {
+          const int64_t p = start + r;
+          const int64_t t = a.rows[p], j = a.cols[p];
+          const float wt = bf16_to_f32(a.w[t * a.k + j]);
+          const int64_t orow = a.out_mode == 0 ? t * a.k + j : p;
+          a.out[orow * a.H + col] = f32_to_bf16(bf16r(acc[mt][0][q]) * wt);
+        }
+      }
+    }
+  }
+}
+// Phase 2, skinny, at most 16 rows (decode): one workgroup = (expert, 64 hidden rows), K split
+// over the four wavefronts; the weights go through the wavefront's LDS tile as in up_skinny_t,
+// 32 rows (two 16-row column tiles) at a time.
+template <int NCH>
+__device__ __forceinline__ void down_skinny_t(const FfnArgs& a, int li, int64_t start, int n, int bx,
+                                              floatx4* red, char* tile) {
+  const int I = (int)a.I;
+  const int lane = threadIdx.x & 63, ks = threadIdx.x >> 6;
+  const int h0 = bx * 64;
+  const bf16_t* wd = a.cache + (int64_t)a.list.slot[li] * 3 * a.H * a.I + 2 * a.H * a.I;
+  const int lr = lane >> 3, lc = lane & 7, r16 = lane & 15, kg = (lane >> 4) * 8;
+  // row group g (< 8): rows h0 + 8g + lr, at p0 + g * gstride; tile row (8g + lr) % 32
+  const bf16_t* p0 = wd + (int64_t)(h0 + lr) * I + lc * 8;
+  const int64_t gstride = (int64_t)8 * I;
+  uint32_t woff[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int row = 8 * g + lr;
+    woff[g] = (uint32_t)(row * 128 + ((lc ^ ((row >> 1) & 7)) << 4));
+  }
+  uint32_t roff[2][2];
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int row = 16 * j + r16;
+      roff[st][j] = (uint32_t)(row * 128 + (((4 * st + (lane >> 4)) ^ ((row >> 1) & 7)) << 4));
+    }
+  const bool oka = r16 < n;
+  const bf16_t* pa = a.act + (start + (oka ? r16 : 0)) * a.I + kg;
+  floatx4 acc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) acc[c] = floatx4{0, 0, 0, 0};
+  const bf16x8 zero8 = {};
+  auto batch = [&](int k0, auto nch) {
+    constexpr int N = decltype(nch)::value;
+    u32x4 w[N][8];
+#pragma unroll
+    for (int ch = 0; ch < N; ++ch)
+#pragma unroll
+      for (int g = 0; g < 8; ++g) w[ch][g] = *reinterpret_cast<const u32x4*>(p0 + g * gstride + k0 + 64 * ch);
+    bf16x8 xa[2 * N];
+#pragma unroll
+    for (int st = 0; st < 2 * N; ++st) xa[st] = oka ? load8(pa + k0 + 32 * st) : zero8;
+#pragma unroll
+    for (int ch = 0; ch < N; ++ch) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) *reinterpret_cast<u32x4*>(tile + woff[g]) = w[ch][4 * h + g];
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+          const bf16x8 b0 = *reinterpret_cast<const bf16x8*>(tile + roff[st][0]);
+          const bf16x8 b1 = *reinterpret_cast<const bf16x8*>(tile + roff[st][1]);
+          acc[2 * h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[2 * ch + st], b0, acc[2 * h], 0, 0, 0);
+          acc[2 * h + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[2 * ch + st], b1, acc[2 * h + 1], 0, 0, 0);
+        }
+      }
+    }
+  };
+  const int kb = ks * (I / 4), ke = kb + I / 4;   // I / 4 is a multiple of 64
+  int k0 = kb;
+  for (; k0 + 64 * NCH <= ke; k0 += 64 * NCH) batch(k0, std::integral_constant<int, NCH>{});
+  for (; k0 < ke; k0 += 64) batch(k0, std::integral_constant<int, 1>{});
+  floatx4 accm[1][4] = {{acc[0], acc[1], acc[2], acc[3]}};
+  if (!skinny_reduce<4, 1>(accm, ks, 0, lane, red)) return;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = (lane >> 4) * 4 + q;
+    if (r < n) {
+      const int64_t p = start + r;
+      const int64_t t = a.rows[p], j = a.cols[p];
+      const float wt = bf16_to_f32(a.w[t * a.k + j]);
+      const int64_t orow = a.out_mode == 0 ? t * a.k + j : p;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        a.out[orow * a.H + h0 + 16 * c + (lane & 15)] = f32_to_bf16(bf16r(accm[0][c][q]) * wt);
+    }
+  }
+}
+
+// Small experts (at most 64 rows), one launch for a list of mixed sizes so that together they
+// fill the GPU: up to 16 rows the skinny scheme, 17-64 rows the mid scheme.  MTMAX = 1 when no
+// expert of the list has more than 16 rows: then only the skinny scheme is compiled in and a
+// phase-1 workgroup covers 16 intermediate columns (grid (I / 16, list)).  Otherwise every
+// workgroup covers 64 columns, which the skinny experts' workgroups do as four 16-column passes
+// (as a one-tile mid workgroup when H is not a multiple of 256), so that all workgroups stream
+// the same weight bytes (grid (I / 64, list)).  Phase 2: 64 hidden rows per workgroup in both
+// schemes (grid (H / 64, list)).
 template <int MTMAX>
-__global__ __launch_bounds__(256) void ffn_down_skinny(FfnArgs a) {
-  __shared__ floatx4 red[(MTMAX >= 4 ? 2 : 1) * 1024];
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void ffn_up_skinny(FfnArgs a) {
+  // MTMAX = 1: the K-reduction buffer (8 KiB) and four 4 KiB weight tiles
+  __shared__ __attribute__((aligned(1024))) char sm[MTMAX > 1 ? 2 * kMidBuf : 8192 + 4 * 4096];
   const int li = blockIdx.y;
   if (li >= a.list.n) return;
   const int e = a.list.expert[li];
   const int64_t start = a.starts[e];
   const int n = (int)(a.starts[e + 1] - start);
   if (n == 0 || n > 16 * MTMAX) return;
-  if (MTMAX >= 4 && n > 32)
-    down_skinny<2, 2, 4>(a, li, start, n, blockIdx.x, red);
-  else if (MTMAX >= 2 && n > 16)
-    down_skinny<2, 2, 2>(a, li, start, n, blockIdx.x, red);
-  else
-    down_skinny<1, 4, 1>(a, li, start, n, blockIdx.x, red);
+  if (MTMAX == 1) {
+    if (a.H % 256 == 0)
+      up_skinny_t<4>(a, li, start, n, blockIdx.x, reinterpret_cast<floatx4*>(sm),
+                     sm + 8192 + (threadIdx.x >> 6) * 4096);
+    else
+      up_skinny<1, 1, 1>(a, li, start, n, blockIdx.x, reinterpret_cast<floatx4*>(sm));
+    return;
+  }
+  if constexpr (MTMAX > 1) {
+    if (n > 32) {
+      ffn_mid_body<0, 4>(a, li, start, n, blockIdx.x, sm);
+    } else if (n > 16) {
+      ffn_mid_body<0, 2>(a, li, start, n, blockIdx.x, sm);
+    } else if (a.H % 256 == 0) {
+#pragma unroll 1
+      for (int j = 0; j < 4; ++j) {
+        up_skinny_t<2>(a, li, start, n, blockIdx.x * 4 + j, reinterpret_cast<floatx4*>(sm),
+                       sm + 8192 + (threadIdx.x >> 6) * 4096);
+        __syncthreads();   // the K-reduction buffer is free again
+      }
+    } else {
+      ffn_mid_body<0, 1>(a, li, start, n, blockIdx.x, sm);
+    }
+  }
+}
+template <int MTMAX>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void ffn_down_skinny(FfnArgs a) {
+  // the K-reduction buffer (16 KiB) and four 4 KiB weight tiles
+  __shared__ __attribute__((aligned(1024))) char sm[MTMAX > 1 ? 2 * kMidBuf : 16384 + 4 * 4096];
+  const int li = blockIdx.y;
+  if (li >= a.list.n) return;
+  const int e = a.list.expert[li];
+  const int64_t start = a.starts[e];
+  const int n = (int)(a.starts[e + 1] - start);
+  if (n == 0 || n > 16 * MTMAX) return;
+  if (MTMAX == 1 || n <= 16) {
+    if (a.I % 256 == 0)
+      down_skinny_t<2>(a, li, start, n, blockIdx.x, reinterpret_cast<floatx4*>(sm),
+                       sm + 16384 + (threadIdx.x >> 6) * 4096);
+    else
+      down_skinny<1, 4, 1>(a, li, start, n, blockIdx.x, reinterpret_cast<floatx4*>(sm));
+    return;
+  }
+  if constexpr (MTMAX > 1) {
+    if (n > 32)
+      ffn_mid_body<1, 4>(a, li, start, n, blockIdx.x, sm);
+    else
+      ffn_mid_body<1, 2>(a, li, start, n, blockIdx.x, sm);
+  }
 }
 
 // =============================================================================================
@@ -735,10 +1090,9 @@ extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t h
         const dim3 g1((unsigned)(inter / 16), cnt);
         if (maxn <= 16)
           launch("ffn_up_skinny", ffn_up_skinny<1>, g1, dim3(256), 0, s, args);
-        else if (maxn <= 32)
-          launch("ffn_up_skinny", ffn_up_skinny<2>, g1, dim3(256), 0, s, args);
         else
-          launch("ffn_up_skinny", ffn_up_skinny<4>, g1, dim3(256), 0, s, args);
+          launch("ffn_up_skinny", ffn_up_skinny<4>, dim3((unsigned)(inter / 64), cnt), dim3(256), 0,
+                 s, args);
         FERRY_LAUNCHED("ffn_up_skinny");
       }
       if (any_big) {
@@ -754,8 +1108,6 @@ extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t h
         const dim3 g2((unsigned)(hidden / 64), cnt);
         if (maxn <= 16)
           launch("ffn_down_skinny", ffn_down_skinny<1>, g2, dim3(256), 0, s, args);
-        else if (maxn <= 32)
-          launch("ffn_down_skinny", ffn_down_skinny<2>, g2, dim3(256), 0, s, args);
         else
           launch("ffn_down_skinny", ffn_down_skinny<4>, g2, dim3(256), 0, s, args);
         FERRY_LAUNCHED("ffn_down_skinny");

@@ -131,7 +131,7 @@ def layout(selected, weights, experts, out=None):
 
 
 PHASE_UP, PHASE_DOWN, PHASE_BOTH = 1, 2, 3
-SKINNY_MAX_ROWS = 64   # experts with at most this many rows run the skinny kernels
+SKINNY_MAX_ROWS = 64   # experts with at most this many rows run the small-expert kernels
 
 
 def expert_ffn(cache, x, w_sorted, starts, rows, cols, expert_list, slot_of, hidden,
@@ -142,7 +142,7 @@ def expert_ffn(cache, x, w_sorted, starts, rows, cols, expert_list, slot_of, hid
     phases: PHASE_UP (gate/up + SwiGLU into ``act``), PHASE_DOWN (down + routing weight from
     ``act`` into ``out``) or PHASE_BOTH.  ``counts`` (optional, host, indexed by expert) holds
     the row count of every expert, ``starts[e+1] - starts[e]``: the experts are then issued in
-    two calls, those with at most 64 rows (skinny kernels) and the larger ones (tiled kernels),
+    two calls, those with at most 64 rows (small-expert kernels) and the larger ones (tiled kernels),
     each with exact row bounds, and experts without rows are skipped.
     """
     R, k = w_sorted.shape

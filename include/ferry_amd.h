@@ -84,8 +84,9 @@ int ferry_layout(const int64_t* selected, const void* weights_bf16, int64_t toke
  * the combine input); out_mode 1 writes row p of out (grouped order).
  * max_rows_per_expert must bound every n_e from above (R does for a layout from ferry_layout),
  * min_rows_per_expert from below (0 when unknown).  Experts with at most 64 rows run the
- * bandwidth-bound skinny kernels, larger ones the tiled MFMA kernels; a launch is skipped when
- * the bounds show that no listed expert needs it (e.g. min_rows_per_expert > 64).
+ * bandwidth-bound small-expert kernels (one launch per phase; their workgroups cover 64 columns
+ * when max_rows_per_expert > 16, 16 otherwise), larger ones the tiled MFMA kernels; a launch is
+ * skipped when the bounds show that no listed expert needs it (e.g. min_rows_per_expert > 64).
  * phases: 1 = gate/up projection + SwiGLU (writes act), 2 = down projection + routing weight
  * (reads act, writes out), 3 = both.
  */

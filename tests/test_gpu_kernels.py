@@ -225,6 +225,46 @@ def test_expert_ffn_and_combine_vs_oracle(device, T, E, k, H, I, zipf):
     assert torch.equal(out.cpu(), mine)
 
 
+@pytest.mark.parametrize('H,I,counts,split', [
+    # Qwen3 expert shape: the 8-row x 128-byte weight loads of the skinny kernels (H, I multiples
+    # of 256) and the mid kernel (17-64 rows), in one mixed launch and split by size
+    (2048, 768, [1, 5, 16, 17, 31, 32, 33, 47, 64, 3, 0, 64], False),
+    (2048, 768, [1, 5, 16, 17, 31, 32, 33, 47, 64, 3, 0, 64], True),
+    (2048, 768, [1, 2, 3, 4, 8, 12, 16, 16], True),          # decode: skinny kernels only
+    # H, I not multiples of 256: the skinny kernels' fragment-order loads
+    (384, 128, [1, 9, 16, 20, 40, 64, 2], False),
+    (384, 128, [1, 9, 16, 7], True),
+])
+def test_small_expert_kernels_vs_oracle(device, H, I, counts, split):
+    """Experts of at most 64 rows: every row count class of the skinny and mid kernels, each
+    expert's rows against the reference op order."""
+    ops = _ops()
+    E = len(counts)
+    rows_w = _pool(E, H, I, seed=H + len(counts))
+    g = torch.Generator().manual_seed(E)
+    ids = np.concatenate([np.full(c, e, np.int64) for e, c in enumerate(counts)])
+    ids = ids[np.random.default_rng(E).permutation(len(ids))]
+    T = len(ids)
+    sel = torch.from_numpy(ids).view(T, 1)
+    w = (torch.rand((T, 1), generator=g) + 0.5).to(torch.bfloat16)
+    x = torch.randn((T, H), generator=g).to(torch.bfloat16)
+    lay = ops.layout(sel.to(device), w.to(device), E)
+    act = torch.empty((T, I), dtype=torch.bfloat16, device=device)
+    part = torch.empty((T, H), dtype=torch.bfloat16, device=device)
+    ops.expert_ffn(rows_w.to(device), x.to(device), lay.w_sorted, lay.starts, lay.rows, lay.cols,
+                   np.arange(E), np.arange(E, dtype=np.int32), H, I, act, part, out_mode=0,
+                   max_rows=max(counts), counts=counts if split else None)
+    torch.cuda.synchronize()
+    got = part.cpu().float()
+    for e, c in enumerate(counts):
+        if c == 0:
+            continue
+        r = torch.from_numpy(np.nonzero(ids == e)[0])
+        ref = execute_experts_ref([rows_w[e]], x, w, [r], [torch.zeros(c, dtype=torch.long)], H, I)[0]
+        torch.testing.assert_close(got[r], ref.float(), rtol=2e-2, atol=1e-2,
+                                   msg=lambda m: f'expert {e} ({c} rows): {m}')
+
+
 def test_execute_experts_api(device):
     """The reference's execute_experts signature (expert_ops.cpp:16-45) on groups of any size."""
     ops = _ops()
