@@ -842,20 +842,14 @@ __global__ __launch_bounds__(kTiledThreads, 1) void ffn_tiled(FfnArgs a) {
       boff[q] = (uint32_t)(((8 * q + r8) * ldb + (slot8 ^ ((row >> 1) & 7)) * 8) * 2);
     }
     const uint32_t lds_smem = lds_addr(smem);
-    // direct load n (< 8) of stage kt: A rows 32 wave + 8n of this wavefront for n < 4, B rows
-    // 32 wave + 8 (n - 4) for n >= 4
-    auto dma = [&](int kt, int n) {
-      const uint32_t st = lds_smem + (uint32_t)((kt % STAGES) * kStageBytes + 32 * wave * kRowBytes);
-      const int q = n & 3;
-      if (n < 4)
-        dma16(abase + kt * BK * 2, aoff[q], st + (uint32_t)(8 * q * kRowBytes));
-      else
-        dma16(bbase + kt * BK * 2, boff[q], st + (uint32_t)(kOperandBytes + 8 * q * kRowBytes));
-    };
-    auto issue = [&](int kt) {
-#pragma unroll
-      for (int n = 0; n < 8; ++n) dma(kt, n);
-    };
+    // Rows past the expert's last one (the partial last M tile of an expert) are not computed:
+    // in such a tile the A direct loads of 8-row groups that lie wholly past it are skipped,
+    // and so are the MFMAs of 32-row blocks that do.  Their LDS rows then hold stale data, which
+    // only reaches output rows that are never stored.  Full tiles run a copy of the loop
+    // without these tests.
+    const int vrows = n - m0;                                          // > 0
+    const int nfa = __builtin_amdgcn_readfirstlane(
+        vrows >= wm * 128 + 128 ? 4 : (vrows > wm * 128 ? (vrows - wm * 128 + 31) / 32 : 0));
     if (MODE == 1) {
       // per-row output row and routing weight for the epilogue
       for (int r = tid; r < BM; r += kTiledThreads) {
@@ -905,16 +899,35 @@ __global__ __launch_bounds__(kTiledThreads, 1) void ffn_tiled(FfnArgs a) {
       ds_read16<0>(fb[0], bb);
       ds_read16<MODE == 0 ? 16384 : 4096>(fb[1], bb);
     };
+    auto pipeline = [&](auto part) {
+    constexpr bool PARTIAL = decltype(part)::value;
+    // direct load n (< 8) of stage kt: A rows 32 wave + 8n of this wavefront for n < 4, B rows
+    // 32 wave + 8 (n - 4) for n >= 4
+    auto dma = [&](int kt, int n) {
+      const uint32_t st = lds_smem + (uint32_t)((kt % STAGES) * kStageBytes + 32 * wave * kRowBytes);
+      const int q = n & 3;
+      if (n < 4) {
+        if (!PARTIAL || 32 * wave + 8 * q < vrows)
+          dma16(abase + kt * BK * 2, aoff[q], st + (uint32_t)(8 * q * kRowBytes));
+      } else {
+        dma16(bbase + kt * BK * 2, boff[q], st + (uint32_t)(kOperandBytes + 8 * q * kRowBytes));
+      }
+    };
+    auto issue = [&](int kt) {
+#pragma unroll
+      for (int n = 0; n < 8; ++n) dma(kt, n);
+    };
     auto mma = [&](const bf16x8 (&fa)[4], const bf16x8 (&fb)[2]) {
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
+        if (!PARTIAL || i < nfa) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        }
       __builtin_amdgcn_sched_barrier(0);
     };
-
     // pipeline: stage kt+1 streams in while stage kt is multiplied; the fragments of the next
     // sub-step are read while the MFMAs of the current one run
     bf16x8 f0a[4], f0b[2], f1a[4], f1b[2];
@@ -950,6 +963,11 @@ __global__ __launch_bounds__(kTiledThreads, 1) void ffn_tiled(FfnArgs a) {
         lds_wait(f0a, f0b);
       }
     }
+    };
+    if (vrows >= BM)
+      pipeline(std::false_type{});
+    else
+      pipeline(std::true_type{});
     __syncthreads();  // all fragment reads done before the staging area is reused
 
     // epilogue: bf16 tile staged in LDS (in two halves of 128 rows for phase 2), then
