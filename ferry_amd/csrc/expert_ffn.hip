@@ -380,166 +380,6 @@ __device__ __forceinline__ void down_skinny(const FfnArgs& a, int li, int64_t st
     }
   }
 }
-// 16-byte global load into registers (saddr + 32-bit lane byte offset) as inline asm: the
-// compiler does not track it, so the registers are read only after vmcnt_tie names them.
-__device__ __forceinline__ void gload16(bf16x8& v, const void* sbase, uint32_t voff) {
-  asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(v) : "v"(voff), "s"(sbase) : "memory");
-}
-// wait until at most N vector loads are outstanding; the registers named are those loads'
-// destinations, tied so that no use of them is scheduled before the wait
-template <int N>
-__device__ __forceinline__ void vmcnt_tie(bf16x8 (&r)[8]) {
-  asm volatile("s_waitcnt vmcnt(%8)"
-               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]),
-                 "+v"(r[6]), "+v"(r[7])
-               : "n"(N)
-               : "memory");
-}
-template <int N>
-__device__ __forceinline__ void vmcnt_tie(bf16x8 (&r)[4]) {
-  asm volatile("s_waitcnt vmcnt(%4)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]) : "n"(N) : "memory");
-}
-
-// =============================================================================================
-// Mid kernels
-// =============================================================================================
-
-// Experts with 17-64 rows (prefill).  The skinny kernels read an expert's token rows once per
-// 16 output columns, which at 64 rows is twice the weight bytes; here a workgroup covers 64
-// columns and reads them once.  One workgroup = (expert, 64 output columns), four wavefronts,
-// each a 16-column group over the full K (phase 1: its 16 gate and 16 up columns).  The token
-// rows are staged into LDS in K chunks of 128 elements by direct loads (two buffers, every
-// wavefront moving a quarter of each chunk); the weights, read exactly once, stream straight
-// into MFMA B registers one chunk ahead.  Rows are held in 16-row M tiles (MT of them).
-//
-// LDS row layout: a chunk row is 256 B = 16 chunks of 8 elements; chunk j of row r sits at
-// slot j ^ (r & 15), so the A-fragment read (16 rows x one chunk per 16 lanes) touches every
-// bank once.
-constexpr int kMidKC = 128;                   // K elements per staged chunk
-constexpr int kMidRowBytes = kMidKC * 2;      // 256
-constexpr int kMidBuf = 64 * kMidRowBytes;    // 16 KiB per buffer (64 rows)
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory"); }
-
-// MODE 0: x rows, gate/up weights, SwiGLU into act.  MODE 1: act rows, down weights, routing
-// weight, into out.
-template <int MODE, int MT>
-__device__ __forceinline__ void ffn_mid_body(const FfnArgs& a, int li, int64_t start, int n,
-                                             int bx, char* xs) {
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int K = (int)(MODE == 0 ? a.H : a.I);
-  const int C = K / kMidKC;
-  const uint32_t lds0 = lds_addr(xs);
-  // token-row staging: direct load q (< 4 MT) moves rows 4q .. 4q+3 of a chunk (16 lanes per
-  // row); this wavefront issues q = MT wave .. MT wave + MT - 1
-  const char* xbase = reinterpret_cast<const char*>(MODE == 0 ? a.x : a.act);
-  uint32_t xoff[MT];
-#pragma unroll
-  for (int i = 0; i < MT; ++i) {
-    const int r = 4 * (MT * wave + i) + (lane >> 4);
-    const int rr = r < n ? r : 0;   // rows past the expert's last load a valid row
-    const uint32_t t = MODE == 0 ? (uint32_t)a.rows[start + rr] : (uint32_t)(start + rr);
-    xoff[i] = t * (uint32_t)(K * 2) + (uint32_t)(((lane & 15) ^ (r & 15)) * 16);
-  }
-  // chunks past the last one restage the last chunk into the buffer nobody reads any more
-  auto stage = [&](int c) {
-    const int cc = c < C ? c : C - 1;
-    const uint32_t dst = lds0 + (uint32_t)((c & 1) * kMidBuf + MT * wave * 1024);
-#pragma unroll
-    for (int i = 0; i < MT; ++i) dma16(xbase + cc * kMidRowBytes, xoff[i], dst + (uint32_t)(i * 1024));
-  };
-  // this wavefront's columns col0 .. col0+16
-  const int col0 = bx * 64 + wave * 16;
-  const int r16 = lane & 15, kg = (lane >> 4) * 8;
-  const bf16_t* slot = a.cache + (int64_t)a.list.slot[li] * 3 * a.H * a.I;
-  constexpr int NB = MODE == 0 ? 2 : 1;
-  // weight rows of this lane (wave-uniform base + 32-bit lane offset): gate then up, or down
-  const bf16_t* wbase = uniform_ptr(slot + (MODE == 0 ? (int64_t)col0 * a.H
-                                                      : 2 * a.H * a.I + (int64_t)col0 * a.I));
-  uint32_t woff[NB];
-  woff[0] = (uint32_t)((r16 * K + kg) * 2);
-  if (MODE == 0) woff[NB - 1] = (uint32_t)((a.H * a.I + (int64_t)r16 * K + kg) * 2);
-  floatx4 acc[MT][NB];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int j = 0; j < NB; ++j) acc[mt][j] = floatx4{0, 0, 0, 0};
-  // A fragment of M tile mt, step s: row mt*16 + r16, chunk 4s + lane/16 at slot chunk ^ r16
-  uint32_t aoff[4];
-#pragma unroll
-  for (int st = 0; st < 4; ++st)
-    aoff[st] = (uint32_t)(r16 * kMidRowBytes + (((4 * st + (lane >> 4)) ^ r16) * 16));
-  // weights of chunk c: w[st * NB + j] = 16 bytes of row j, K step st (chunks past the last
-  // reload the last one)
-  constexpr int NW = 4 * NB;
-  bf16x8 wb[2][NW];
-  auto wload = [&](int c, bf16x8 (&w)[NW]) {
-    const int cc = c < C ? c : C - 1;
-    const char* b = reinterpret_cast<const char*>(wbase) + cc * kMidRowBytes;
-#pragma unroll
-    for (int st = 0; st < 4; ++st)
-#pragma unroll
-      for (int j = 0; j < NB; ++j) gload16(w[st * NB + j], b + st * 64, woff[j]);
-  };
-  // Every chunk issues, in this order, the direct loads of the next chunk's token rows and the
-  // next chunk's weight loads, so the counts behind each wait are fixed: the weights of chunk c
-  // are older than MT + 4 NB loads, the token rows of chunk c+1 older than 4 NB.
-  auto chunk = [&](int c, auto par) {
-    constexpr int P = decltype(par)::value;   // c % 2
-    wg_barrier();   // chunk c staged by every wavefront; chunk c-1's buffer no longer read
-    stage(c + 1);
-    wload(c + 1, wb[1 - P]);
-    vmcnt_tie<MT + NW>(wb[P]);
-    const char* xb = xs + P * kMidBuf;
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      bf16x8 xa[MT];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-        xa[mt] = *reinterpret_cast<const bf16x8*>(xb + mt * 16 * kMidRowBytes + aoff[st]);
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int j = 0; j < NB; ++j)
-          acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[mt], wb[P][st * NB + j], acc[mt][j], 0, 0, 0);
-    }
-    wait_vmcnt<NW>();   // this wavefront's share of chunk c+1 landed
-  };
-  stage(0);
-  wload(0, wb[0]);
-  wait_vmcnt<NW>();
-  for (int c = 0; c < C; c += 2) {
-    chunk(c, std::integral_constant<int, 0>{});
-    if (c + 1 < C) chunk(c + 1, std::integral_constant<int, 1>{});
-  }
-  // the loads past the last chunk are never used: hold their registers (and the LDS) until
-  // they landed
-  vmcnt_tie<0>(wb[0]);
-  vmcnt_tie<0>(wb[1]);
-  // 16x16 accumulator layout: column = lane & 15, rows (lane >> 4) * 4 + [0, 4)
-  const int col = col0 + (lane & 15);
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int r = mt * 16 + (lane >> 4) * 4 + q;
-      if (r < n) {
-        if (MODE == 0) {
-          const float g = bf16r(acc[mt][0][q]), u = bf16r(acc[mt][NB - 1][q]);
-          a.act[(start + r) * a.I + col] = f32_to_bf16(silu_mul(g, u));
-        } else {
-          const int64_t p = start + r;
-          const int64_t t = a.rows[p], j = a.cols[p];
-          const float wt = bf16_to_f32(a.w[t * a.k + j]);
-          const int64_t orow = a.out_mode == 0 ? t * a.k + j : p;
-          a.out[orow * a.H + col] = f32_to_bf16(bf16r(acc[mt][0][q]) * wt);
-        }
-      }
-    }
-  }
-}
 // Phase 2, skinny, at most 16 rows (decode): one workgroup = (expert, 64 hidden rows), K split
 // over the four wavefronts; the weights go through the wavefront's LDS tile as in up_skinny_t,
 // 32 rows (two 16-row column tiles) at a time.
@@ -621,6 +461,192 @@ __device__ __forceinline__ void down_skinny_t(const FfnArgs& a, int li, int64_t 
   }
 }
 
+// 16-byte global load into registers (saddr + 32-bit lane byte offset) as inline asm: the
+// compiler does not track it, so the registers are read only after vmcnt_tie names them.
+__device__ __forceinline__ void gload16(bf16x8& v, const void* sbase, uint32_t voff) {
+  asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(v) : "v"(voff), "s"(sbase) : "memory");
+}
+// wait until at most N vector loads are outstanding; the registers named are those loads'
+// destinations, tied so that no use of them is scheduled before the wait
+template <int N>
+__device__ __forceinline__ void vmcnt_tie(bf16x8 (&r)[8]) {
+  asm volatile("s_waitcnt vmcnt(%8)"
+               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]),
+                 "+v"(r[6]), "+v"(r[7])
+               : "n"(N)
+               : "memory");
+}
+template <int N>
+__device__ __forceinline__ void vmcnt_tie(bf16x8 (&r)[2]) {
+  asm volatile("s_waitcnt vmcnt(%2)" : "+v"(r[0]), "+v"(r[1]) : "n"(N) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void vmcnt_tie(bf16x8 (&r)[4]) {
+  asm volatile("s_waitcnt vmcnt(%4)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]) : "n"(N) : "memory");
+}
+
+// =============================================================================================
+// Mid kernels
+// =============================================================================================
+
+// Mid scheme (experts with 17-64 rows, prefill).  The skinny kernels read an expert's token rows
+// once per 16 output columns, which at 64 rows is twice the weight bytes; here a workgroup covers
+// 64 columns and reads them once.  One workgroup = (expert, 64 output columns), four wavefronts,
+// each a 16-column group over the full K (phase 1: its 16 gate and 16 up columns).  Rows are held
+// in 16-row M tiles (MT of them).  K is walked in chunks of 64:
+//  * the token rows go through a ring of three 8 KiB LDS buffers, staged by direct loads (8 rows
+//    x 128 B each, XD per wavefront) two chunks ahead; 128-byte rows, chunk j of row r at slot
+//    j ^ ((r >> 1) & 7), so that the A-fragment reads are free of bank conflicts;
+//  * the weights, read exactly once, are loaded 8 rows x 128 B per instruction (every 128-byte
+//    line fetched by one instruction) into a ring of three register sets three chunks ahead, and
+//    each chunk goes through the wavefront's 2 KiB LDS tile (16 rows x 128 B) into B fragments.
+// Per wavefront and chunk the loads are issued in a fixed order -- XD token-row loads at the top
+// of the chunk, NW weight loads after the tile writes -- so every wait has a fixed count of
+// younger loads.
+constexpr int kMidXBuf = 64 * 128;                    // token-row ring buffer (64 rows x 128 B)
+constexpr int kMidLds = 3 * kMidXBuf + 4 * 2048;      // ring + four wavefront tiles: 32 KiB
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory"); }
+
+template <int MODE, int MT>
+__device__ __forceinline__ void ffn_mid_body_t(const FfnArgs& a, int li, int64_t start, int n,
+                                               int bx, char* sm) {
+  static_assert(MT == 1 || MT == 2 || MT == 4, "MT 16-row tiles");
+  // token-row direct loads per wavefront and chunk (MT = 1 stages 32 rows, of which 16 are used)
+  constexpr int XD = MT >= 2 ? MT / 2 : 1;
+  constexpr int NB = MODE == 0 ? 2 : 1;
+  constexpr int NW = 2 * NB;                 // weight loads per wavefront and chunk
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int K = (int)(MODE == 0 ? a.H : a.I);
+  const int C = K / 64;
+  const int lr = lane >> 3, lc = lane & 7, r16 = lane & 15;
+  const uint32_t lds0 = lds_addr(sm);
+  char* tile = sm + 3 * kMidXBuf + wave * 2048;
+  // token rows: direct load i of this wavefront moves rows 8 (XD wave + i) + lr
+  const char* xbase = reinterpret_cast<const char*>(MODE == 0 ? a.x : a.act);
+  uint32_t xoff[XD];
+#pragma unroll
+  for (int i = 0; i < XD; ++i) {
+    const int r = 8 * (XD * wave + i) + lr;
+    const int rr = r < n ? r : 0;   // rows past the expert's last load a valid row
+    const uint32_t t = MODE == 0 ? (uint32_t)a.rows[start + rr] : (uint32_t)(start + rr);
+    xoff[i] = t * (uint32_t)(K * 2) + (uint32_t)((lc ^ ((r >> 1) & 7)) << 4);
+  }
+  auto stage = [&](int c) {   // chunks past the last restage it into a buffer nobody reads
+    const int cc = c < C ? c : C - 1;
+    const uint32_t dst = lds0 + (uint32_t)((c % 3) * kMidXBuf + XD * wave * 1024);
+#pragma unroll
+    for (int i = 0; i < XD; ++i) dma16(xbase + cc * 128, xoff[i], dst + (uint32_t)(i * 1024));
+  };
+  // weights: row group g (< NW) = rows 8 (g & 1) + lr of gate (g < 2) or up / down, 128 B of
+  // the chunk per lane group
+  const int col0 = bx * 64 + wave * 16;
+  const bf16_t* slot = a.cache + (int64_t)a.list.slot[li] * 3 * a.H * a.I;
+  const bf16_t* wbase = uniform_ptr(slot + (MODE == 0 ? (int64_t)col0 * a.H
+                                                      : 2 * a.H * a.I + (int64_t)col0 * a.I));
+  uint32_t woff[NW];
+#pragma unroll
+  for (int g = 0; g < NW; ++g)
+    woff[g] = (uint32_t)(((g >= 2 ? a.H * a.I : 0) + (int64_t)(8 * (g & 1) + lr) * K + lc * 8) * 2);
+  bf16x8 wb[3][NW];
+  auto wload = [&](int c, bf16x8 (&w)[NW]) {   // chunks past the last reload it
+    const int cc = c < C ? c : C - 1;
+    const char* b = reinterpret_cast<const char*>(wbase) + cc * 128;
+#pragma unroll
+    for (int g = 0; g < NW; ++g) gload16(w[g], b, woff[g]);
+  };
+  // tile rows: write row group g2 (< 2) at rows 8 g2 + lr; fragment read of K step st: row r16,
+  // chunk 4 st + lane / 16
+  uint32_t twoff[2], troff[2], aoff[2];
+#pragma unroll
+  for (int g2 = 0; g2 < 2; ++g2) {
+    const int row = 8 * g2 + lr;
+    twoff[g2] = (uint32_t)(row * 128 + ((lc ^ ((row >> 1) & 7)) << 4));
+  }
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    troff[st] = (uint32_t)(r16 * 128 + (((4 * st + (lane >> 4)) ^ ((r16 >> 1) & 7)) << 4));
+    aoff[st] = troff[st];   // token-row fragments: the same layout, rows mt*16 + r16
+  }
+  floatx4 acc[MT][NB];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[mt][j] = floatx4{0, 0, 0, 0};
+  auto chunk = [&](int c, auto par) {
+    constexpr int P = decltype(par)::value;   // c % 3
+    wg_barrier();             // chunk c staged by every wavefront; chunk c-1's buffer free
+    stage(c + 2);
+    // this chunk's weights: older than x(c), w(c+1), x(c+1), w(c+2), x(c+2)
+    vmcnt_tie<3 * XD + 2 * NW>(wb[P]);
+    bf16x8 bfr[NB][2];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+#pragma unroll
+      for (int g2 = 0; g2 < 2; ++g2) *reinterpret_cast<bf16x8*>(tile + twoff[g2]) = wb[P][2 * j + g2];
+#pragma unroll
+      for (int st = 0; st < 2; ++st) bfr[j][st] = *reinterpret_cast<const bf16x8*>(tile + troff[st]);
+    }
+    wload(c + 3, wb[P]);
+    const char* xb = sm + P * kMidXBuf;
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      bf16x8 xa[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        xa[mt] = *reinterpret_cast<const bf16x8*>(xb + mt * 16 * 128 + aoff[st]);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+          acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[mt], bfr[j][st], acc[mt][j], 0, 0, 0);
+    }
+    // token rows of chunk c+1 landed: older than w(c+2), x(c+2), w(c+3)
+    wait_vmcnt<2 * NW + XD>();
+  };
+  // prologue in the steady-state order: w(0), x(0), w(1), x(1), w(2)
+  wload(0, wb[0]);
+  stage(0);
+  wload(1, wb[1]);
+  stage(1);
+  wload(2, wb[2]);
+  wait_vmcnt<2 * NW + XD>();   // x(0) landed
+  for (int c = 0; c < C; c += 3) {
+    chunk(c, std::integral_constant<int, 0>{});
+    if (c + 1 < C) chunk(c + 1, std::integral_constant<int, 1>{});
+    if (c + 2 < C) chunk(c + 2, std::integral_constant<int, 2>{});
+  }
+  // the loads past the last chunk are never used: hold their registers (and the LDS) until
+  // they landed
+  wait_vmcnt<0>();
+  vmcnt_tie<0>(wb[0]);
+  vmcnt_tie<0>(wb[1]);
+  vmcnt_tie<0>(wb[2]);
+  // 16x16 accumulator layout: column = lane & 15, rows (lane >> 4) * 4 + [0, 4)
+  const int col = col0 + (lane & 15);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int r = mt * 16 + (lane >> 4) * 4 + q;
+      if (r < n) {
+        if (MODE == 0) {
+          const float g = bf16r(acc[mt][0][q]), u = bf16r(acc[mt][NB - 1][q]);
+          a.act[(start + r) * a.I + col] = f32_to_bf16(silu_mul(g, u));
+        } else {
+          const int64_t p = start + r;
+          const int64_t t = a.rows[p], j = a.cols[p];
+          const float wt = bf16_to_f32(a.w[t * a.k + j]);
+          const int64_t orow = a.out_mode == 0 ? t * a.k + j : p;
+          a.out[orow * a.H + col] = f32_to_bf16(bf16r(acc[mt][0][q]) * wt);
+        }
+      }
+    }
+  }
+}
+
 // Small experts (at most 64 rows), one launch for a list of mixed sizes so that together they
 // fill the GPU: up to 16 rows the skinny scheme, 17-64 rows the mid scheme.  MTMAX = 1 when no
 // expert of the list has more than 16 rows: then only the skinny scheme is compiled in and a
@@ -632,7 +658,7 @@ __device__ __forceinline__ void down_skinny_t(const FfnArgs& a, int li, int64_t 
 template <int MTMAX>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void ffn_up_skinny(FfnArgs a) {
   // MTMAX = 1: the K-reduction buffer (8 KiB) and four 4 KiB weight tiles
-  __shared__ __attribute__((aligned(1024))) char sm[MTMAX > 1 ? 2 * kMidBuf : 8192 + 4 * 4096];
+  __shared__ __attribute__((aligned(1024))) char sm[MTMAX > 1 ? kMidLds : 8192 + 4 * 4096];
   const int li = blockIdx.y;
   if (li >= a.list.n) return;
   const int e = a.list.expert[li];
@@ -649,9 +675,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void f
   }
   if constexpr (MTMAX > 1) {
     if (n > 32) {
-      ffn_mid_body<0, 4>(a, li, start, n, blockIdx.x, sm);
+      ffn_mid_body_t<0, 4>(a, li, start, n, blockIdx.x, sm);
     } else if (n > 16) {
-      ffn_mid_body<0, 2>(a, li, start, n, blockIdx.x, sm);
+      ffn_mid_body_t<0, 2>(a, li, start, n, blockIdx.x, sm);
     } else if (a.H % 256 == 0) {
 #pragma unroll 1
       for (int j = 0; j < 4; ++j) {
@@ -660,14 +686,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void f
         __syncthreads();   // the K-reduction buffer is free again
       }
     } else {
-      ffn_mid_body<0, 1>(a, li, start, n, blockIdx.x, sm);
+      ffn_mid_body_t<0, 1>(a, li, start, n, blockIdx.x, sm);
     }
   }
 }
 template <int MTMAX>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void ffn_down_skinny(FfnArgs a) {
   // the K-reduction buffer (16 KiB) and four 4 KiB weight tiles
-  __shared__ __attribute__((aligned(1024))) char sm[MTMAX > 1 ? 2 * kMidBuf : 16384 + 4 * 4096];
+  __shared__ __attribute__((aligned(1024))) char sm[MTMAX > 1 ? kMidLds : 16384 + 4 * 4096];
   const int li = blockIdx.y;
   if (li >= a.list.n) return;
   const int e = a.list.expert[li];
@@ -684,9 +710,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void f
   }
   if constexpr (MTMAX > 1) {
     if (n > 32)
-      ffn_mid_body<1, 4>(a, li, start, n, blockIdx.x, sm);
+      ffn_mid_body_t<1, 4>(a, li, start, n, blockIdx.x, sm);
     else
-      ffn_mid_body<1, 2>(a, li, start, n, blockIdx.x, sm);
+      ffn_mid_body_t<1, 2>(a, li, start, n, blockIdx.x, sm);
   }
 }
 
