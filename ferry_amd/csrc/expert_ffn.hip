@@ -876,22 +876,25 @@ __global__ __launch_bounds__(kTiledThreads, 1) void ffn_tiled(FfnArgs a) {
     const int vrows = n - m0;                                          // > 0
     const int nfa = __builtin_amdgcn_readfirstlane(
         vrows >= wm * 128 + 128 ? 4 : (vrows > wm * 128 ? (vrows - wm * 128 + 31) / 32 : 0));
-    if (MODE == 1) {
-      // per-row output row and routing weight for the epilogue
-      for (int r = tid; r < BM; r += kTiledThreads) {
-        const int rr = m0 + r;
-        int64_t orow = 0;
-        float wt = 0.f;
-        if (rr < n) {
-          const int64_t p = start + rr;
-          const int64_t t = a.rows[p], j = a.cols[p];
-          wt = bf16_to_f32(a.w[t * a.k + j]);
-          orow = a.out_mode == 0 ? t * a.k + j : p;
+    // per-row output row and routing weight for the phase-2 epilogue; run after the first
+    // stage's direct loads are issued, so that its dependent loads overlap them
+    auto row_meta = [&]() {
+      if (MODE == 1) {
+        for (int r = tid; r < BM; r += kTiledThreads) {
+          const int rr = m0 + r;
+          int64_t orow = 0;
+          float wt = 0.f;
+          if (rr < n) {
+            const int64_t p = start + rr;
+            const int64_t t = a.rows[p], j = a.cols[p];
+            wt = bf16_to_f32(a.w[t * a.k + j]);
+            orow = a.out_mode == 0 ? t * a.k + j : p;
+          }
+          orow_s[r] = orow;
+          wt_s[r] = wt;
         }
-        orow_s[r] = orow;
-        wt_s[r] = wt;
       }
-    }
+    };
 
     floatx16 acc[4][2];
 #pragma unroll
@@ -958,6 +961,7 @@ __global__ __launch_bounds__(kTiledThreads, 1) void ffn_tiled(FfnArgs a) {
     // sub-step are read while the MFMAs of the current one run
     bf16x8 f0a[4], f0b[2], f1a[4], f1b[2];
     issue(0);
+    row_meta();
     wait_vmcnt0();
     wg_barrier();
     if (1 < KT) issue(1);
