@@ -485,6 +485,241 @@ __device__ __forceinline__ void vmcnt_tie(bf16x8 (&r)[4]) {
   asm volatile("s_waitcnt vmcnt(%4)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]) : "n"(N) : "memory");
 }
 
+// f(integral_constant<int, i>) for i = B .. E - 1, unrolled at compile time
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+template <int OFF>
+__device__ __forceinline__ void gload16o(bf16x8& v, const void* sbase, uint32_t voff) {
+  asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3"
+               : "=v"(v)
+               : "v"(voff), "s"(sbase), "n"(OFF)
+               : "memory");
+}
+
+// Phase 1, skinny, at most 16 rows, H = 512 * NB: up_skinny_t's tile scheme with the K range of
+// each wavefront walked in NB batches of two 64-element chunks, software-pipelined -- the loads
+// of batch b + 1 are issued before batch b goes through the tile and the matrix cores, so that a
+// wavefront always has a batch in flight.  All loads are inline asm (saddr + 32-bit lane offset:
+// two registers per batch set instead of a 64-bit address per load), 12 per batch in a fixed
+// order (8 weight loads, then 4 token-row loads; padding rows load token row 0 and are zeroed
+// after the wait), so each wait has a fixed count of younger loads.  The batch loop is fully
+// unrolled: no loop-carried register holds a load in flight.
+template <int NB>
+__device__ __forceinline__ void up_skinny_p(const FfnArgs& a, int li, int64_t start, int n, int bx,
+                                            floatx4* red, char* tile) {
+  static_assert(NB >= 2 && NB % 2 == 0, "an even number of batches");
+  constexpr int H = 512 * NB;
+  const int lane = threadIdx.x & 63, ks = threadIdx.x >> 6;
+  const int i0 = bx * 16;
+  const bf16_t* wg = uniform_ptr(a.cache + (int64_t)a.list.slot[li] * 3 * H * a.I);
+  const bf16_t* xs = uniform_ptr(a.x);
+  const int lr = lane >> 3, lc = lane & 7, r16 = lane & 15, kg = (lane >> 4) * 8;
+  // byte offsets of the wavefront's K range: row group g = rows 8 (g & 1) + lr of the gate
+  // (g < 2) or up (g >= 2) projection; the group offsets are wavefront-uniform
+  const int kb = ks * (H / 4);
+  const uint32_t wrow = (uint32_t)(((i0 + lr) * H + lc * 8 + kb) * 2);
+  const uint32_t gup = (uint32_t)(H * a.I * 2);
+  uint32_t woff[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int row = 8 * g + lr;
+    woff[g] = (uint32_t)(row * 128 + ((lc ^ ((row >> 1) & 7)) << 4));
+  }
+  uint32_t roff[2][2];
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int row = 16 * j + r16;
+      roff[st][j] = (uint32_t)(row * 128 + (((4 * st + (lane >> 4)) ^ ((row >> 1) & 7)) << 4));
+    }
+  const bool okx = r16 < n;
+  floatx4 acc[2] = {floatx4{0, 0, 0, 0}, floatx4{0, 0, 0, 0}};
+  const bf16x8 zero8 = {};
+  // batch b: weights w[4 ch + g] (chunk ch of row group g), token rows xa[st] (K step st)
+  uint32_t xrow;
+  auto load_w = [&](auto b, bf16x8 (&w)[8]) {
+    constexpr uint32_t kbyte = decltype(b)::value * 256;
+    gload16o<0>(w[0], wg, wrow + kbyte);
+    gload16o<0>(w[1], wg, wrow + kbyte + 16 * H);
+    gload16o<0>(w[2], wg, wrow + kbyte + gup);
+    gload16o<0>(w[3], wg, wrow + kbyte + gup + 16 * H);
+    gload16o<128>(w[4], wg, wrow + kbyte);
+    gload16o<128>(w[5], wg, wrow + kbyte + 16 * H);
+    gload16o<128>(w[6], wg, wrow + kbyte + gup);
+    gload16o<128>(w[7], wg, wrow + kbyte + gup + 16 * H);
+  };
+  auto load_x = [&](auto b, bf16x8 (&xa)[4]) {
+    constexpr uint32_t kbyte = decltype(b)::value * 256;
+    gload16o<0>(xa[0], xs, xrow + kbyte);
+    gload16o<64>(xa[1], xs, xrow + kbyte);
+    gload16o<128>(xa[2], xs, xrow + kbyte);
+    gload16o<192>(xa[3], xs, xrow + kbyte);
+  };
+  auto mma = [&](bf16x8 (&w)[8], bf16x8 (&xa)[4]) {
+#pragma unroll
+    for (int st = 0; st < 4; ++st) xa[st] = okx ? xa[st] : zero8;
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) *reinterpret_cast<bf16x8*>(tile + woff[g]) = w[4 * ch + g];
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const bf16x8 bg = *reinterpret_cast<const bf16x8*>(tile + roff[st][0]);
+        const bf16x8 bu = *reinterpret_cast<const bf16x8*>(tile + roff[st][1]);
+        acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[2 * ch + st], bg, acc[0], 0, 0, 0);
+        acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[2 * ch + st], bu, acc[1], 0, 0, 0);
+      }
+    }
+  };
+  auto load = [&](auto b, bf16x8 (&w)[8], bf16x8 (&xa)[4]) {
+    load_w(b, w);
+    load_x(b, xa);
+  };
+  // the token row of each lane (padding rows: row 0) is loaded ahead of the first weights and
+  // awaited behind them, so the first batch keeps the fixed order of 8 weight and 4 row loads
+  // (the low word suffices: token indices times H stay below 2^31)
+  uint32_t trow;
+  asm volatile("global_load_dword %0, %1, %2"
+               : "=v"(trow)
+               : "v"((uint32_t)((okx ? r16 : 0) * 8)), "s"(uniform_ptr(a.rows + start))
+               : "memory");
+  bf16x8 wA[8], wB[8], xA[4], xB[4];
+  load_w(std::integral_constant<int, 0>{}, wA);
+  asm volatile("s_waitcnt vmcnt(8)" : "+v"(trow) : : "memory");
+  xrow = (trow * H + kg + kb) * 2;
+  load_x(std::integral_constant<int, 0>{}, xA);
+  static_for<0, NB / 2 - 1>([&](auto j) {
+    load(std::integral_constant<int, 2 * decltype(j)::value + 1>{}, wB, xB);
+    vmcnt_tie<12>(wA);
+    vmcnt_tie<12>(xA);
+    mma(wA, xA);
+    load(std::integral_constant<int, 2 * decltype(j)::value + 2>{}, wA, xA);
+    vmcnt_tie<12>(wB);
+    vmcnt_tie<12>(xB);
+    mma(wB, xB);
+  });
+  load(std::integral_constant<int, NB - 1>{}, wB, xB);
+  vmcnt_tie<12>(wA);
+  vmcnt_tie<12>(xA);
+  mma(wA, xA);
+  vmcnt_tie<0>(wB);
+  vmcnt_tie<0>(xB);
+  mma(wB, xB);
+  floatx4 accm[1][2] = {{acc[0], acc[1]}};
+  if (!skinny_reduce<4, 1>(accm, ks, 0, lane, red)) return;
+  const int col = i0 + (lane & 15);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = (lane >> 4) * 4 + q;
+    if (r < n) {
+      const float g = bf16r(accm[0][0][q]), u = bf16r(accm[0][1][q]);
+      a.act[(start + r) * a.I + col] = f32_to_bf16(silu_mul(g, u));
+    }
+  }
+}
+
+// Phase 2, skinny, at most 16 rows, I = 256 * NC: down_skinny_t's tile scheme with each
+// wavefront's K range walked one 64-element chunk at a time, software-pipelined over two register
+// sets -- chunk c + 1 is loaded while chunk c goes through the tile and the matrix cores.  Ten
+// asm loads per chunk in a fixed order (eight 8-row weight groups, then two activation loads;
+// padding rows load the expert's first row and are zeroed after the wait).  Fully unrolled.
+template <int NC>
+__device__ __forceinline__ void down_skinny_p(const FfnArgs& a, int li, int64_t start, int n, int bx,
+                                              floatx4* red, char* tile) {
+  constexpr int I = 256 * NC;
+  const int lane = threadIdx.x & 63, ks = threadIdx.x >> 6;
+  const int h0 = bx * 64;
+  const bf16_t* wd =
+      uniform_ptr(a.cache + (int64_t)a.list.slot[li] * 3 * a.H * I + 2 * a.H * I);
+  const bf16_t* as = uniform_ptr(a.act + start * I);
+  const int lr = lane >> 3, lc = lane & 7, r16 = lane & 15, kg = (lane >> 4) * 8;
+  const int kb = ks * (I / 4);
+  // row group g (< 8): rows h0 + 8g + lr, byte offset wrow + g * 16 I; tile row (8g + lr) % 32
+  const uint32_t wrow = (uint32_t)(((h0 + lr) * I + lc * 8 + kb) * 2);
+  uint32_t woff[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int row = 8 * g + lr;
+    woff[g] = (uint32_t)(row * 128 + ((lc ^ ((row >> 1) & 7)) << 4));
+  }
+  uint32_t roff[2][2];
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int row = 16 * j + r16;
+      roff[st][j] = (uint32_t)(row * 128 + (((4 * st + (lane >> 4)) ^ ((row >> 1) & 7)) << 4));
+    }
+  const bool oka = r16 < n;
+  const uint32_t arow = (uint32_t)(((oka ? r16 : 0) * I + kg + kb) * 2);
+  floatx4 acc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) acc[c] = floatx4{0, 0, 0, 0};
+  const bf16x8 zero8 = {};
+  auto load = [&](auto c, bf16x8 (&w)[8], bf16x8 (&xa)[2]) {
+    constexpr uint32_t kbyte = decltype(c)::value * 128;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) gload16o<0>(w[g], wd, wrow + kbyte + g * 16 * I);
+    gload16o<0>(xa[0], as, arow + kbyte);
+    gload16o<64>(xa[1], as, arow + kbyte);
+  };
+  auto mma = [&](bf16x8 (&w)[8], bf16x8 (&xa)[2]) {
+#pragma unroll
+    for (int st = 0; st < 2; ++st) xa[st] = oka ? xa[st] : zero8;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) *reinterpret_cast<bf16x8*>(tile + woff[g]) = w[4 * h + g];
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const bf16x8 b0 = *reinterpret_cast<const bf16x8*>(tile + roff[st][0]);
+        const bf16x8 b1 = *reinterpret_cast<const bf16x8*>(tile + roff[st][1]);
+        acc[2 * h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[st], b0, acc[2 * h], 0, 0, 0);
+        acc[2 * h + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[st], b1, acc[2 * h + 1], 0, 0, 0);
+      }
+    }
+  };
+  bf16x8 wA[8], wB[8], xA[2], xB[2];
+  load(std::integral_constant<int, 0>{}, wA, xA);
+  static_for<0, NC>([&](auto c) {
+    constexpr int C = decltype(c)::value;
+    auto& wc = (C % 2 == 0) ? wA : wB;
+    auto& xc = (C % 2 == 0) ? xA : xB;
+    auto& wn = (C % 2 == 0) ? wB : wA;
+    auto& xn = (C % 2 == 0) ? xB : xA;
+    if constexpr (C + 1 < NC) {
+      load(std::integral_constant<int, C + 1>{}, wn, xn);
+      vmcnt_tie<10>(wc);
+      vmcnt_tie<10>(xc);
+    } else {
+      vmcnt_tie<0>(wc);
+      vmcnt_tie<0>(xc);
+    }
+    mma(wc, xc);
+  });
+  floatx4 accm[1][4] = {{acc[0], acc[1], acc[2], acc[3]}};
+  if (!skinny_reduce<4, 1>(accm, ks, 0, lane, red)) return;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = (lane >> 4) * 4 + q;
+    if (r < n) {
+      const int64_t p = start + r;
+      const int64_t t = a.rows[p], j = a.cols[p];
+      const float wt = bf16_to_f32(a.w[t * a.k + j]);
+      const int64_t orow = a.out_mode == 0 ? t * a.k + j : p;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        a.out[orow * a.H + h0 + 16 * c + (lane & 15)] = f32_to_bf16(bf16r(accm[0][c][q]) * wt);
+    }
+  }
+}
+
 // =============================================================================================
 // Mid kernels
 // =============================================================================================
@@ -666,7 +901,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void f
   const int n = (int)(a.starts[e + 1] - start);
   if (n == 0 || n > 16 * MTMAX) return;
   if (MTMAX == 1) {
-    if (a.H % 256 == 0)
+    if (a.H == 2048)
+      up_skinny_p<4>(a, li, start, n, blockIdx.x, reinterpret_cast<floatx4*>(sm),
+                  sm + 8192 + (threadIdx.x >> 6) * 4096);
+    else if (a.H % 256 == 0)
       up_skinny_t<4>(a, li, start, n, blockIdx.x, reinterpret_cast<floatx4*>(sm),
                      sm + 8192 + (threadIdx.x >> 6) * 4096);
     else
@@ -701,7 +939,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void f
   const int n = (int)(a.starts[e + 1] - start);
   if (n == 0 || n > 16 * MTMAX) return;
   if (MTMAX == 1 || n <= 16) {
-    if (a.I % 256 == 0)
+    if (a.I == 768)
+      down_skinny_p<3>(a, li, start, n, blockIdx.x, reinterpret_cast<floatx4*>(sm),
+                       sm + 16384 + (threadIdx.x >> 6) * 4096);
+    else if (a.I % 256 == 0)
       down_skinny_t<2>(a, li, start, n, blockIdx.x, reinterpret_cast<floatx4*>(sm),
                        sm + 16384 + (threadIdx.x >> 6) * 4096);
     else

@@ -231,6 +231,10 @@ def test_expert_ffn_and_combine_vs_oracle(device, T, E, k, H, I, zipf):
     (2048, 768, [1, 5, 16, 17, 31, 32, 33, 47, 64, 3, 0, 64], False),
     (2048, 768, [1, 5, 16, 17, 31, 32, 33, 47, 64, 3, 0, 64], True),
     (2048, 768, [1, 2, 3, 4, 8, 12, 16, 16], True),          # decode: skinny kernels only
+    # other multiples of 256: the unpipelined 8-row x 128-byte phase-1 path (the pipelined one
+    # serves H = 2048)
+    (1024, 256, [1, 3, 16, 9], True),
+    (512, 256, [2, 16, 5], True),
     # H, I not multiples of 256: the skinny kernels' fragment-order loads
     (384, 128, [1, 9, 16, 20, 40, 64, 2], False),
     (384, 128, [1, 9, 16, 7], True),
