@@ -13,7 +13,9 @@
 //    (phase 2) weight rows and splits K over its four wavefronts; the partial sums meet in
 //    LDS.  The weights are loaded 8 rows x 128 B per instruction and turned into MFMA B
 //    fragments through a small per-wavefront LDS tile; x rows come from L2.
-//    v_mfma_f32_16x16x32_bf16.
+//    v_mfma_f32_16x16x32_bf16.  For the decode shapes (H = 2048 up, I = 768 down) the K walk
+//    is software-pipelined with inline-asm loads: the next batch is in flight while the
+//    current one is multiplied.
 //  * mid (16 < n_e <= 64, prefill): bandwidth-bound.  A workgroup owns 64 output columns over
 //    the full K; the expert's token rows are staged once per workgroup in LDS, the weights
 //    stream into MFMA B registers.  Launched together with the skinny experts of a list.
