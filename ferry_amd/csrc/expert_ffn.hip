@@ -1324,6 +1324,9 @@ extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t h
                   "hidden must be a multiple of 256 when an expert has more than %d rows",
                   kSkinnyMax);
   FERRY_CHECK_ARG(rows_in * topk < (int64_t)1 << 31, "rows*topk must be < 2^31");
+  // the kernels address weights with 32-bit byte offsets from the expert's cache row
+  FERRY_CHECK_ARG(3 * hidden * inter * 2 < ((int64_t)1 << 32),
+                  "an expert's cache row (3 * hidden * intermediate bf16) must be under 4 GiB");
   // the tiled kernels address A rows with 32-bit byte offsets
   FERRY_CHECK_ARG(rows_in * hidden < ((int64_t)1 << 31) &&
                       rows_in * topk * inter < ((int64_t)1 << 31),

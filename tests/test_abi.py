@@ -52,6 +52,10 @@ def test_abi_version_and_errors():
     assert L.ferry_expert_ffn(None, 1, 256, 128, None, 100, 1, None, None, None, None, None, 1, None,
                               1, 10, 11, None, None, 0, 3, None) != 0
     assert 'min_rows_per_expert' in last_error()
+    # weights are addressed with 32-bit offsets inside an expert's cache row
+    assert L.ferry_expert_ffn(None, 1, 65536, 32768, None, 100, 1, None, None, None, None, None,
+                              1, None, 1, 10, 0, None, None, 0, 3, None) != 0
+    assert '4 GiB' in last_error()
     assert L.ferry_combine_add(None, None, 4, 2, 64, None, None, None) != 0
     assert 'addend' in last_error()
 
