@@ -88,7 +88,8 @@ int ferry_layout(const int64_t* selected, const void* weights_bf16, int64_t toke
  * when max_rows_per_expert > 16, 16 otherwise), larger ones the tiled MFMA kernels; a launch is
  * skipped when the bounds show that no listed expert needs it (e.g. min_rows_per_expert > 64).
  * phases: 1 = gate/up projection + SwiGLU (writes act), 2 = down projection + routing weight
- * (reads act, writes out), 3 = both.
+ * (reads act, writes out), 3 = both.  An expert's cache row (3 * H * I bf16) must be smaller
+ * than 4 GiB.
  */
 enum { FERRY_MAX_EXPERTS = 512 };
 int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t hidden, int64_t inter,
