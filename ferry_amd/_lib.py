@@ -28,6 +28,9 @@ SIGNATURES = [
      [_c_p, _i64, _i64, _i64, _c_p, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _i32, _c_p, _i64,
       _i64, _i64, _c_p, _c_p, _i32, _i32, _c_p]),
     ('ferry_combine', ctypes.c_int, [_c_p, _c_p, _i64, _i64, _i64, _c_p, _c_p]),
+    ('ferry_pack_dispatch', ctypes.c_int,
+     [_c_p, _i64, _i64, _c_p, _c_p, _i64, _c_p, _c_p, _i64, _i64, _i64, _c_p, _c_p]),
+    ('ferry_unpack_dispatch', ctypes.c_int, [_c_p, _i64, _i64, _i64, _c_p, _c_p, _c_p]),
     ('ferry_combine_add', ctypes.c_int, [_c_p, _c_p, _i64, _i64, _i64, _c_p, _c_p, _c_p]),
     ('ferry_history_update', ctypes.c_int,
      [_c_p, _i64, _i64, _i64, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p]),

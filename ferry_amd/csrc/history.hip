@@ -18,7 +18,8 @@ constexpr int kMaxE = 512;
 constexpr int kThreads = 256;
 constexpr int kIdsPerBlock = kThreads * 16;
 
-// Block 0 updates the window of `layer`; blocks >= 1 write the uint8 copy of selected.
+// Block 0 updates the window of `layer`; blocks >= 1 write the uint8 copy of selected, with
+// 0xFF for an ID outside [0, E) (E <= 255 then, so the host planner rejects it).
 __global__ __launch_bounds__(kThreads) void history_kernel(
     const int64_t* __restrict__ selected, int64_t tokens, int k, int E, int W, int64_t layer,
     int32_t* __restrict__ ring, int32_t* __restrict__ counts, int32_t* __restrict__ meta,
@@ -26,8 +27,10 @@ __global__ __launch_bounds__(kThreads) void history_kernel(
   if (blockIdx.x > 0) {
     const int64_t n = tokens * k;
     const int64_t i0 = (int64_t)(blockIdx.x - 1) * kIdsPerBlock;
-    for (int64_t i = i0 + threadIdx.x; i < n && i < i0 + kIdsPerBlock; i += kThreads)
-      ids_out[i] = (uint8_t)selected[i];
+    for (int64_t i = i0 + threadIdx.x; i < n && i < i0 + kIdsPerBlock; i += kThreads) {
+      const int64_t e = selected[i];
+      ids_out[i] = (e >= 0 && e < E) ? (uint8_t)e : (uint8_t)0xFF;
+    }
     return;
   }
   __shared__ int32_t c[kMaxE];
@@ -86,7 +89,7 @@ extern "C" int ferry_history_update(const int64_t* selected, int64_t tokens, int
   clear_error();
   FERRY_CHECK_ARG(tokens >= 0 && topk >= 1 && layer >= 0, "bad sizes");
   FERRY_CHECK_ARG(experts >= 1 && experts <= kMaxE, "experts must be in [1, %d]", kMaxE);
-  FERRY_CHECK_ARG(experts <= 256 || ids_out == nullptr, "uint8 IDs need experts <= 256");
+  FERRY_CHECK_ARG(experts <= 255 || ids_out == nullptr, "uint8 IDs need experts <= 255");
   FERRY_CHECK_ARG(window >= 1 && window <= (1 << 20), "window must be in [1, 2^20]");
   FERRY_CHECK_ARG(ring && counts && meta && scores_out, "null pointer argument");
   FERRY_CHECK_ARG(tokens == 0 || selected, "null pointer argument");

@@ -30,7 +30,9 @@ struct TokenIds {
 };
 
 // Load one token's k IDs and weights and sort them by ID (IDs of a token are distinct, so any
-// sort gives the insertion-sort result); padding entries carry the key kMaxE.
+// sort gives the insertion-sort result); out-of-range entries carry the key kMaxE, padding
+// entries kMaxE + 1.  `bad` is set for a token with an out-of-range or a repeated ID: such a
+// token breaks the layout's contract (its entries would share one permutation slot).
 __device__ __forceinline__ void load_sorted(const int64_t* __restrict__ selected,
                                             const bf16_t* __restrict__ weights, int64_t t, int k,
                                             int E, TokenIds& s, bool& bad) {
@@ -61,6 +63,8 @@ __device__ __forceinline__ void load_sorted(const int64_t* __restrict__ selected
       }
     }
   }
+#pragma unroll
+  for (int j = 0; j + 1 < kMaxK; ++j) bad |= (j + 1 < k && s.id[j] < E && s.id[j] == s.id[j + 1]);
 }
 
 struct LayoutShared {

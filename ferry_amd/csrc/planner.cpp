@@ -52,17 +52,29 @@ extern "C" int64_t ferry_plan_layer(int64_t event, int64_t layer, const int64_t*
     ferry::set_error("plan_layer: bad sizes");
     return -1;
   }
+  // validate the routing before any state changes: every ID in [0, E), none repeated within
+  // a token (the reference's demand count and layout assume both)
+  std::vector<int64_t> seen((size_t)experts, -1);
+  for (int64_t t = 0; t < tokens; ++t) {
+    for (int64_t j = 0; j < topk; ++j) {
+      const int64_t e = selected[t * topk + j];
+      if (e < 0 || e >= experts) {
+        ferry::set_error("plan_layer: expert id %lld of token %lld is out of range [0, %lld)",
+                         (long long)e, (long long)t, (long long)experts);
+        return -3;
+      }
+      if (seen[(size_t)e] == t) {
+        ferry::set_error("plan_layer: expert id %lld repeated in token %lld", (long long)e,
+                         (long long)t);
+        return -3;
+      }
+      seen[(size_t)e] = t;
+    }
+  }
   const int64_t base = layer * experts;
   std::memcpy(scores + base, gate_scores, (size_t)experts * sizeof(float));
   std::vector<uint8_t> active((size_t)experts, 0);
-  for (int64_t i = 0; i < tokens * topk; ++i) {
-    const int64_t e = selected[i];
-    if (e < 0 || e >= experts) {
-      ferry::set_error("plan_layer: expert id %lld out of range", (long long)e);
-      return -1;
-    }
-    active[(size_t)e] = 1;
-  }
+  for (int64_t i = 0; i < tokens * topk; ++i) active[(size_t)selected[i]] = 1;
   std::vector<int64_t> misses;
   misses.reserve((size_t)experts);
   for (int64_t e = 0; e < experts; ++e)

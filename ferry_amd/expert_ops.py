@@ -11,6 +11,7 @@ import numpy as np
 import torch
 
 from ._lib import check, lib
+from ._lib import check as _check_status
 from .h2d import H2DEngine
 
 __all__ = ['execute_experts', 'pack_dispatch', 'unpack_dispatch', 'reduce_partials',
@@ -106,8 +107,18 @@ def layout_workspace_bytes(tokens, topk, experts):
     return int(lib().ferry_layout_workspace_bytes(tokens, topk, experts))
 
 
-def layout(selected, weights, experts, out=None):
-    """Sorted packet IDs/weights, per-expert starts and the stable (rows, cols) permutation."""
+def layout_errors(lay):
+    """Number of tokens of the last ``layout`` call into ``lay`` that had an expert ID outside
+    [0, experts) or a repeated ID (waits for that call)."""
+    return int(lay.workspace[:4].view(torch.int32).item())
+
+
+def layout(selected, weights, experts, out=None, check=False):
+    """Sorted packet IDs/weights, per-expert starts and the stable (rows, cols) permutation.
+
+    Every token's IDs must be distinct and in [0, experts).  The kernel counts the tokens that
+    break this; ``check=True`` waits for the result and raises RuntimeError when any did.
+    """
     T, k = selected.shape
     dev = selected.device
     lay = out if out is not None else Layout()
@@ -121,12 +132,17 @@ def layout(selected, weights, experts, out=None):
         lay.workspace = torch.empty(layout_workspace_bytes(T, k, experts), dtype=torch.uint8,
                                     device=dev)
     lay.tokens, lay.topk, lay.experts = T, k, experts
-    check(lib().ferry_layout(
+    _check_status(lib().ferry_layout(
         _dev(selected, 'selected', torch.int64),
         _dev(weights, 'weights', torch.bfloat16) if weights is not None else None,
         T, k, experts, lay.send_ids.data_ptr(), lay.w_sorted.data_ptr(), lay.starts.data_ptr(),
         lay.rows.data_ptr(), lay.cols.data_ptr(), lay.pair_pos.data_ptr(),
         lay.workspace.data_ptr(), lay.workspace.numel(), current_stream(dev)), 'layout')
+    if check:
+        bad = layout_errors(lay)
+        if bad:
+            raise RuntimeError(f'layout: {bad} token(s) with an expert ID out of [0, {experts}) '
+                               'or repeated')
     return lay
 
 
@@ -294,28 +310,33 @@ def execute_experts(cache, input, routing_weights, slots, rows, cols, hidden, in
 def pack_dispatch(hidden, selected, weights, send_idx, send_ids, experts):
     """Dispatch packet rows ``[x (2H B) | weights in send_ids order (2k B) | IDs (k B)]``.
 
-    Reference: expert_ops.cpp:50-66.  At world = 1 the packet never leaves the GPU; this
-    builds the same byte format for API compatibility (the fused path reads the routing
-    weights in send_ids order straight from the layout kernel instead).
+    Reference: expert_ops.cpp:88-104, on the ``ferry_pack_dispatch`` kernel.  At world = 1 the
+    packet never leaves the GPU (the fused path reads the routing weights in send_ids order
+    straight from the layout kernel); this gives callers of the reference's Transport the same
+    bytes.
     """
     n, k = send_ids.shape
-    dense = torch.zeros((hidden.shape[0], experts), dtype=torch.float32, device=hidden.device)
-    dense.scatter_add_(1, selected, weights.float())
-    dense = dense.to(torch.bfloat16)
-    valid = send_ids.ge(0)
-    pw = dense[send_idx.unsqueeze(1), send_ids.clamp_min(0)] * valid
-    payload = torch.empty((n, 2 * hidden.shape[1] + 3 * k), dtype=torch.uint8, device=hidden.device)
-    payload[:, :2 * hidden.shape[1]] = hidden.index_select(0, send_idx).view(torch.uint8)
-    payload[:, 2 * hidden.shape[1]:2 * hidden.shape[1] + 2 * k] = pw.contiguous().view(torch.uint8)
-    payload[:, 2 * hidden.shape[1] + 2 * k:] = send_ids.to(torch.uint8)
+    T, H = hidden.shape
+    payload = torch.empty((n, 2 * H + 3 * k), dtype=torch.uint8, device=hidden.device)
+    check(lib().ferry_pack_dispatch(
+        _dev(hidden, 'hidden', torch.bfloat16), T, H, _dev(selected, 'selected', torch.int64),
+        _dev(weights, 'weights', torch.bfloat16), selected.shape[1],
+        _dev(send_idx, 'send_idx', torch.int64), _dev(send_ids, 'send_ids', torch.int64), n, k,
+        experts, payload.data_ptr(), current_stream(hidden.device)), 'pack_dispatch')
     return payload
 
 
 def unpack_dispatch(raw, hidden, topk):
-    """Split packet rows back into bf16 [m, H] hidden states and [m, k] weights (:68-73)."""
+    """Split packet rows back into bf16 [m, H] hidden states and [m, k] weights
+    (expert_ops.cpp:106-111), as two strided device copies."""
     m = raw.shape[0]
-    x = raw[:, :2 * hidden].contiguous().view(torch.bfloat16).view(m, hidden)
-    w = raw[:, 2 * hidden:2 * hidden + 2 * topk].contiguous().view(torch.bfloat16).view(m, topk)
+    if raw.dim() != 2 or raw.shape[1] != 2 * hidden + 3 * topk:
+        raise RuntimeError('raw must be uint8 [m, 2 * hidden + 3 * topk]')
+    x = torch.empty((m, hidden), dtype=torch.bfloat16, device=raw.device)
+    w = torch.empty((m, topk), dtype=torch.bfloat16, device=raw.device)
+    check(lib().ferry_unpack_dispatch(_dev(raw, 'raw', torch.uint8), m, hidden, topk,
+                                      x.data_ptr(), w.data_ptr(), current_stream(raw.device)),
+          'unpack_dispatch')
     return [x, w]
 
 

@@ -29,7 +29,7 @@ def device_layout(selected, destinations, tokens_per_rank, rank, experts, slot_o
         raise NotImplementedError('ferry_amd runs on one GPU (world = 1)')
     if destinations is not None and np.any(np.asarray(destinations) != 0):
         raise AssertionError('expert scheduled on this rank is not cached here')
-    lay = ops.layout(sel, weights, experts)
+    lay = ops.layout(sel, weights, experts, check=True)   # the reference's index checks
     starts = lay.starts.cpu().numpy()
     groups = []
     for e in np.flatnonzero(starts[1:] > starts[:-1]):

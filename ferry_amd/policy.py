@@ -11,6 +11,7 @@ import numpy as np
 from ._lib import last_error, lib
 
 FERRY, RANDOM = 0, 1
+INVALID_ROUTING = -3   # planner status: an expert ID out of range or repeated within a token
 POLICIES = {'ferry': FERRY, 'random': RANDOM}
 
 
@@ -51,6 +52,8 @@ def plan_layer(event, layer, selected, origins, gate_scores, policy, slots, capa
                                slots.ctypes.data, int(capacities[0]), _c(owner, np.int64),
                                _c(last, np.int64), _c(scores, np.float32), experts,
                                fetches.ctypes.data, destinations.ctypes.data)
+    if m == INVALID_ROUTING:
+        raise RuntimeError(last_error())
     if m < 0:
         # the reference fails an assert here (quota.py:63 / policy.py:177)
         raise AssertionError(last_error())
@@ -107,6 +110,8 @@ class Controller:
                                    self._fetch_buf.ctypes.data, None, h2d_handle)
         if m == -1:
             raise AssertionError(last_error())
+        if m == INVALID_ROUTING:
+            raise RuntimeError(last_error())
         if m < 0:
             raise RuntimeError(f'plan_fetch: {last_error()}')
         return self._fetch_buf[:m], np.array([m], np.int64)

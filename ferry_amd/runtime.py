@@ -218,7 +218,7 @@ class OffloadRuntime:
         self.event += 1
 
         # 5. combine (+ the shared experts' output)
-        out = self.transport.combine(hidden, buf['part'], dict(layout=lay), addend=shared_out)
+        out = self.ops.combine(buf['part'], T, k, spec.hidden, addend=shared_out)
         if self.timing:
             h = self.host_ns
             h['enqueue_before_wait'] += t_sync - t_enter

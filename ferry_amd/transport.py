@@ -1,10 +1,12 @@
 """Dispatch / combine at world = 1 (reference: ferry/transport.py).
 
-With one GPU the all-to-all exchanges are identities: dispatch hands the hidden states and the
-routing weights in sorted-ID order to the experts, combine sums the expert outputs per token
-(fp32, ascending expert ID) and casts to bf16.  Cross-GPU bytes stay zero.
+``Transport`` keeps the reference's exchange protocol: dispatch packs the token packets
+(``pack_dispatch``), exchanges them and unpacks them (``unpack_dispatch``); combine sums the
+expert outputs of every received row (``reduce_partials``), sends them back and adds them to
+their tokens (``scatter_returned``).  With one GPU each exchange is the identity, so no byte
+crosses a device and the byte counters stay 0.  The fused runtime path skips the packets and
+runs the layout kernel's token-major combine instead (``expert_ops.combine``).
 """
-from . import expert_ops as ops
 
 
 class Transport:
@@ -13,11 +15,24 @@ class Transport:
         self.rank = 0
         self.dispatch_bytes = self.combine_bytes = 0
 
-    def dispatch(self, hidden, selected, weights, layout):
-        lay = layout['layout']
-        return hidden, lay.w_sorted
+    def _exchange(self, x, send_counts, recv_counts):
+        """The all-to-all of one rank: everything it sends is what it receives."""
+        if list(send_counts) != list(recv_counts) or len(send_counts) != 1:
+            raise NotImplementedError('ferry_amd runs on one GPU (world = 1)')
+        return x
 
-    def combine(self, hidden, parts, layout, addend=None):
-        """``parts`` is the token-major [T*k, H] bf16 output of the expert FFN; ``addend``
-        (bf16 [T, H], optional) is added to the bf16 result in fp32."""
-        return ops.combine(parts, hidden.shape[0], self.topk, hidden.shape[1], addend=addend)
+    def dispatch(self, hidden, selected, weights, layout):
+        """Token packets to the experts: (received hidden rows, their packet weights)
+        (transport.py:22-29)."""
+        packets = self.ops.pack_dispatch(hidden, selected, weights, layout['send_idx'],
+                                         layout['send_ids'], self.experts)
+        received = self._exchange(packets, layout['send_counts'], layout['recv_counts'])
+        return self.ops.unpack_dispatch(received, hidden.shape[1], self.topk)
+
+    def combine(self, hidden, parts, layout):
+        """Expert outputs back to their tokens, fp32 sums in expert order (transport.py:31-38)."""
+        rows = [g[1] for g in layout['groups']]
+        partial = self.ops.reduce_partials(parts, rows, sum(layout['recv_counts']),
+                                           hidden.shape[1], hidden)
+        returned = self._exchange(partial, layout['recv_counts'], layout['send_counts'])
+        return self.ops.scatter_returned(returned, layout['send_idx'], hidden.shape[0])

@@ -64,7 +64,10 @@ int ferry_router_topk(const void* logits, int32_t logits_dtype, int64_t tokens, 
  *   rows[T*k]       int64  token of each (expert, rank) entry, ascending token per expert
  *   cols[T*k]       int64  position of that expert in the token's sorted ID list
  *   pair_pos[T*k]   int32  inverse map: pair_pos[t*k+j] = grouped position (nullable)
- * `workspace` must hold ferry_layout_workspace_bytes(T, k, E) bytes of device memory.
+ * `workspace` must hold ferry_layout_workspace_bytes(T, k, E) bytes of device memory.  Every
+ * token's IDs must be distinct and in [0, E); after the call the first 4 bytes of `workspace`
+ * hold an int32 count of the tokens that break this (their entries are left out of the
+ * permutation), for the caller to read when it wants the check.
  */
 int64_t ferry_layout_workspace_bytes(int64_t tokens, int64_t topk, int64_t experts);
 int ferry_layout(const int64_t* selected, const void* weights_bf16, int64_t tokens, int64_t topk,
@@ -119,13 +122,31 @@ int ferry_combine_add(const void* part, const int32_t* pair_pos, int64_t tokens,
                       int64_t hidden, const void* addend, void* out, void* stream);
 
 /*
+ * Dispatch packets (the reference's exchange format).  Replaces ferry/csrc/expert_ops.cpp:88-104
+ * (pack_dispatch) and :106-111 (unpack_dispatch), called from ferry/transport.py:22-29.
+ * Packet row i (2H + 3k bytes) = [hidden[send_idx[i]] (bf16 H) | packet weights (bf16 k) |
+ * uint8(send_ids[i])], where packet weight j = bf16(sum of fp32(weights[t, q]) over the q with
+ * selected[t, q] == send_ids[i, j]) for t = send_idx[i], times (send_ids[i, j] >= 0).
+ * selected / weights are the router outputs [tokens, topk_selected]; send_idx [packets] and
+ * send_ids [packets, topk] come from the layout; a packet whose send_idx is outside
+ * [0, tokens) is left unwritten.  unpack_dispatch splits packet rows back into
+ * hidden_out bf16 [packets, H] and weights_out bf16 [packets, topk].
+ */
+int ferry_pack_dispatch(const void* hidden, int64_t tokens, int64_t hidden_size,
+                        const int64_t* selected, const void* weights_bf16, int64_t topk_selected,
+                        const int64_t* send_idx, const int64_t* send_ids, int64_t packets,
+                        int64_t topk, int64_t experts, void* payload, void* stream);
+int ferry_unpack_dispatch(const void* payload, int64_t packets, int64_t hidden_size, int64_t topk,
+                          void* hidden_out, void* weights_out, void* stream);
+
+/*
  * Selection-frequency history on the device.  Replaces ferry/metadata.py:15-38 (GateHistory
  * update/scores over one-hot rows built by RouteGather.collect, ferry/metadata.py:67-83).
  * State per layer (device memory, caller-owned, zero-initialised):
  *   ring[L, W, k] int32, counts[L, E] int32, meta[L, 2] int32 (count, head).
  * Update with the last min(T, W) tokens of selected[T, k]; then scores_out[E] =
- * float32(count_e / max(1, n)).  ids_out (nullable) receives selected as uint8 [T*k]
- * (the D2H payload of the host planner).
+ * float32(count_e / max(1, n)).  ids_out (nullable, needs E <= 255) receives selected as
+ * uint8 [T*k] (the D2H payload of the host planner), with 0xFF for an ID outside [0, E).
  */
 int ferry_history_update(const int64_t* selected, int64_t tokens, int64_t topk, int64_t experts,
                          int64_t window, int64_t layer, int32_t* ring, int32_t* counts,
@@ -138,7 +159,8 @@ int ferry_history_update(const int64_t* selected, int64_t tokens, int64_t topk, 
  *   slots[cap], owner[L*E], last[L*E] int64; scores[L*E] float32.
  * Returns the number of misses m (fetches_out receives m rows of (0, key, slot) in ascending
  * expert order), or -1 with ferry_last_error() set when the misses exceed the admission
- * capacity.  destinations_out (nullable) receives owner[layer*E + selected[t,j]].
+ * capacity, or -3 (state untouched) when an expert ID is outside [0, E) or repeated within a
+ * token.  destinations_out (nullable) receives owner[layer*E + selected[t,j]].
  */
 int64_t ferry_plan_layer(int64_t event, int64_t layer, const int64_t* selected, int64_t tokens,
                          int64_t topk, const float* gate_scores, int64_t* slots, int64_t cap,
@@ -182,7 +204,8 @@ void* ferry_h2d_stream(ferry_h2d* h);
  * e.g. straight from the mapped staging buffer that ferry_history_update writes; the other
  * arguments are those of ferry_plan_layer, plus the fetch engine (nullable: plan only).
  * Returns the number of misses m (fetches_out rows as in ferry_plan_layer, their copies queued),
- * -1 when the misses exceed the admission capacity, -2 when the fetch fails; errors set
+ * -1 when the misses exceed the admission capacity, -2 when the fetch fails, -3 when an ID is
+ * outside [0, E) (0xFF from ferry_history_update) or repeated within a token; errors set
  * ferry_last_error().
  */
 int64_t ferry_plan_fetch(int64_t event, int64_t layer, const uint8_t* ids, int64_t tokens,

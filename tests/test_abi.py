@@ -164,6 +164,31 @@ def test_product_planner_overflow_raises_assertion():
         ctl.plan(0, 0, np.array([[0, 1, 2]]), np.zeros(1, np.int64), np.zeros(8, np.float32))
 
 
+def test_planner_rejects_invalid_routing_ids():
+    """An expert ID outside [0, E) or repeated within a token is rejected with RuntimeError
+    before any planner state changes, through both the int64 and the fused uint8 entry points
+    (0xFF is what the history kernel writes for an out-of-range ID)."""
+    from ferry_amd.policy import Controller
+    from ferry_amd.quota import Topology
+    E = 16
+    ctl = Controller(_Spec(2, E), [4], 'ferry', Topology.uniform(1, E))
+    ctl.plan(0, 0, np.array([[1, 2], [3, 1]]), np.zeros(2, np.int64), np.zeros(E, np.float32))
+    state = (ctl.slots.copy(), ctl.owner.copy(), ctl.last.copy(), ctl.scores.copy())
+    gs = np.ones(E, np.float32)
+    for bad in ([[1, 16]], [[-1, 2]], [[5, 5]], [[0, 1], [2, 2]]):
+        with pytest.raises(RuntimeError, match='out of range|repeated'):
+            ctl.plan(1, 1, np.array(bad), np.zeros(len(bad), np.int64), gs)
+    for bad in ([1, 0xFF], [7, 7]):
+        ids = np.array(bad, np.uint8)
+        with pytest.raises(RuntimeError, match='out of range|repeated'):
+            ctl.plan_fetch(1, 1, ids.ctypes.data, 1, 2, gs.ctypes.data, None)
+    for a, b in zip(state, (ctl.slots, ctl.owner, ctl.last, ctl.scores)):
+        assert np.array_equal(a, b)
+    # the same state still plans valid routing
+    f, _, _ = ctl.plan(1, 1, np.array([[0, 5]]), np.zeros(1, np.int64), gs)
+    assert f[:, 1].tolist() == [E + 0, E + 5]
+
+
 def test_world_gt_1_rejected():
     from ferry_amd.policy import Controller
     from ferry_amd.quota import Topology

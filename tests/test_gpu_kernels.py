@@ -153,6 +153,48 @@ def test_layout_bit_exact(device, T, E, k):
     assert np.array_equal(lay.pair_pos.cpu().numpy(), ref['pair_pos'])
 
 
+@pytest.mark.parametrize('T', [5, 3000])   # one-block and three-kernel layouts
+def test_layout_flags_invalid_ids(device, T):
+    """Tokens with an out-of-range or a repeated expert ID are counted by the kernel and
+    ``layout(check=True)`` raises; valid routing passes the check with a zero count."""
+    ops = _ops()
+    E, k = 32, 4
+    sel = _selected(T, E, k, seed=T)
+    lay = ops.layout(sel.to(device), None, E, check=True)
+    assert ops.layout_errors(lay) == 0
+    for bad, count in (((0, 1), 40), ((T - 1, 2), -1), ((1, 0), 1)):
+        s = sel.clone()
+        (t, j), v = bad, count
+        s[t, j] = v if v != 1 else s[t, 3]          # 40 / -1: out of range; else a repeat
+        with pytest.raises(RuntimeError, match='out of'):
+            ops.layout(s.to(device), None, E, check=True)
+        assert ops.layout_errors(ops.layout(s.to(device), None, E)) == 1
+
+
+def test_runtime_rejects_invalid_ids(device):
+    """OffloadRuntime.execute raises RuntimeError on an out-of-range or repeated ID: the host
+    planner validates the IDs it reads back for planning, before any expert is computed."""
+    from ferry_amd.model import ModelSpec
+    from ferry_amd.quota import Topology
+    from ferry_amd.runtime import OffloadRuntime
+    from ferry_amd import workloads
+    spec = ModelSpec('qwen3_moe', (0,), 16, 4, 256, 128)
+    pool = workloads.make_pool(spec, 1, seed=0)
+    rt = OffloadRuntime(spec, pool, [16], 'ferry', Topology.uniform(1, 16))
+    x = torch.randn((3, 256)).to(torch.bfloat16).to(device)
+    w = torch.full((3, 4), 0.25, dtype=torch.bfloat16, device=device)
+    good = torch.tensor([[0, 1, 2, 3], [4, 5, 6, 7], [1, 3, 5, 7]], device=device)
+    rt.execute(0, x, good, w, None)
+    for bad in ([[0, 1, 2, 16], [4, 5, 6, 7], [1, 3, 5, 7]],
+                [[0, 1, 2, 3], [4, 5, 6, 4], [1, 3, 5, 7]]):
+        with pytest.raises(RuntimeError, match='out of range|repeated'):
+            rt.execute(0, x, torch.tensor(bad, device=device), w, None)
+    out = rt.execute(0, x, good, w, None)   # the runtime still works afterwards
+    torch.cuda.synchronize()
+    assert out.shape == (3, 256)
+    rt.close()
+
+
 # ---------------------------------------------------------------------------------------------
 # device history
 # ---------------------------------------------------------------------------------------------

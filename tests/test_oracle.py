@@ -296,3 +296,34 @@ def test_execute_experts_ref_weights_rows_cols():
     out = execute_experts_ref([row], x, rw, [r], [c], H, I)[0]
     unit = execute_experts_ref([row], x, torch.ones_like(rw), [r], [c], H, I)[0]
     torch.testing.assert_close(out.float(), (unit.float() * torch.tensor([[2.0], [1.0]])).bfloat16().float())
+
+
+def test_pack_dispatch_oracle_matches_closed_form():
+    """The restated packet bytes (dense scatter / gather of expert_ops.cpp:88-104) equal the
+    world-1 closed form [hidden | weights in sorted-ID order | sorted IDs] for distinct IDs, and
+    unpacking returns the hidden rows and sorted weights; repeated IDs add their weights and a
+    -1 packet ID gives weight 0 and the ID byte 255."""
+    import torch
+    from oracle.layout import layout_closed_form
+    from oracle.transport import pack_dispatch_ref, packets_closed_form, unpack_dispatch_ref
+    g = torch.Generator().manual_seed(0)
+    for T, E, k, H in ((1, 8, 2, 16), (37, 64, 6, 64), (200, 128, 8, 32)):
+        sel = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)])
+        w = torch.softmax(torch.randn((T, k), generator=g), -1).to(torch.bfloat16)
+        x = torch.randn((T, H), generator=g).to(torch.bfloat16)
+        lay = layout_closed_form(sel.numpy(), E, w.view(torch.int16).numpy())
+        send_ids = torch.from_numpy(lay['send_ids'])
+        got = pack_dispatch_ref(x, sel, w, torch.arange(T), send_ids, E)
+        assert got.dtype == torch.uint8 and got.shape == (T, 2 * H + 3 * k)
+        assert np.array_equal(got.numpy(), packets_closed_form(x, lay['send_ids'], lay['w_sorted']))
+        ux, uw = unpack_dispatch_ref(got, H, k)
+        assert torch.equal(ux, x)
+        assert np.array_equal(uw.view(torch.int16).numpy(), lay['w_sorted'])
+    # repeated IDs add (fp32, then bf16); an invalid packet ID reads weight 0, ID byte 255
+    x = torch.zeros((1, 4), dtype=torch.bfloat16)
+    sel = torch.tensor([[2, 2, 5]])
+    w = torch.tensor([[0.25, 0.5, 0.125]]).to(torch.bfloat16)
+    p = pack_dispatch_ref(x, sel, w, torch.tensor([0]), torch.tensor([[2, 5, -1]]), 8)
+    _, pw = unpack_dispatch_ref(p, 4, 3)
+    assert pw.float().tolist() == [[0.75, 0.125, 0.0]]
+    assert p[0, -3:].tolist() == [2, 5, 255]
