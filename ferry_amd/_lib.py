@@ -24,6 +24,8 @@ SIGNATURES = [
     ('ferry_layout_workspace_bytes', _i64, [_i64, _i64, _i64]),
     ('ferry_layout', ctypes.c_int,
      [_c_p, _c_p, _i64, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _i64, _c_p]),
+    ('ferry_layout_noalloc', ctypes.c_int,
+     [_c_p, _c_p, _i64, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p]),
     ('ferry_expert_ffn', ctypes.c_int,
      [_c_p, _i64, _i64, _i64, _c_p, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _i32, _c_p, _i64,
       _i64, _i64, _c_p, _c_p, _i32, _i32, _c_p]),

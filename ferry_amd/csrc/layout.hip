@@ -16,6 +16,8 @@
 // larger T uses count -> scan -> scatter launches.
 #include "common.h"
 
+#include <mutex>
+
 namespace ferry {
 namespace {
 
@@ -213,6 +215,33 @@ __global__ __launch_bounds__(kBlockTokens) void layout_scatter(
   }
 }
 
+// The workspace of ferry_layout_noalloc: a file-scope device array instead of caller memory.
+// Each GPU holds its own copy for the life of the process; its device address is looked up
+// once per device (hipGetSymbolAddress) and only that address is handed to kernels.  Nothing in
+// it needs clearing between calls: the error counter is zeroed by the layout kernels themselves
+// and the per-block histograms are fully rewritten by every multi-block call.
+constexpr int64_t kScratchBytes = 256 + 128 * (int64_t)kMaxE * (int64_t)sizeof(int32_t);
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices];  // device address of `scratch` on each device, or null
+
+// Device address of `scratch` on the current device (resolved on first use per device).
+int scratch_address(void** out) {
+  int dev = -1;
+  FERRY_HIP(hipGetDevice(&dev));
+  FERRY_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    FERRY_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return 0;
+}
+
 }  // namespace
 }  // namespace ferry
 
@@ -263,4 +292,26 @@ extern "C" int ferry_layout(const int64_t* selected, const void* weights_bf16, i
                      E, hist, starts, send_ids, ws, rows, cols, pair_pos, err);
   FERRY_LAUNCHED("layout_scatter");
   return 0;
+}
+
+extern "C" int ferry_layout_noalloc(const int64_t* selected, const void* weights_bf16,
+                                    int64_t tokens, int64_t topk, int64_t experts,
+                                    int64_t* send_ids, void* w_sorted_bf16, int64_t* starts,
+                                    int64_t* rows, int64_t* cols, int32_t* pair_pos,
+                                    void* stream) {
+  clear_error();
+  FERRY_CHECK_ARG(tokens >= 0, "tokens must be >= 0");
+  FERRY_CHECK_ARG(experts >= 1 && experts <= kMaxE, "experts must be in [1, %d]", kMaxE);
+  const int64_t need = ferry_layout_workspace_bytes(tokens, topk, experts);
+  FERRY_CHECK_ARG(need <= kScratchBytes,
+                  "layout_noalloc: %lld tokens x %lld experts need %lld scratch bytes, the static "
+                  "buffer holds %lld (at most %lld tokens at this expert count)",
+                  (long long)tokens, (long long)experts, (long long)need, (long long)kScratchBytes,
+                  (long long)((kScratchBytes - 256) / (experts * (int64_t)sizeof(int32_t)) *
+                              kBlockTokens));
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc != 0) return rc;
+  return ferry_layout(selected, weights_bf16, tokens, topk, experts, send_ids, w_sorted_bf16,
+                      starts, rows, cols, pair_pos, ws, kScratchBytes, stream);
 }

@@ -74,6 +74,22 @@ int ferry_layout(const int64_t* selected, const void* weights_bf16, int64_t toke
                  int64_t experts, int64_t* send_ids, void* w_sorted_bf16, int64_t* starts,
                  int64_t* rows, int64_t* cols, int32_t* pair_pos, void* workspace,
                  int64_t workspace_bytes, void* stream);
+/*
+ * ferry_layout with no workspace argument and no allocation.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  The workspace is a static device buffer of
+ * 262,400 bytes per GPU (256 + 128 * 512 * 4), held until the process ends, which bounds the
+ * layout to ferry_layout_workspace_bytes(T, k, E) <= 262,400: at most 524,288 tokens with 128
+ * experts, 131,072 with 512.  Larger calls fail with an error before any launch.  Every call on
+ * one GPU shares that buffer, so calls that overlap on one GPU (on different streams, or from
+ * different threads) race; calls ordered on one stream do not.  The device of the calling
+ * thread must be the one `stream` belongs to.  Outputs and errors as ferry_layout; the
+ * invalid-ID count stays in the static buffer.
+ */
+int ferry_layout_noalloc(const int64_t* selected, const void* weights_bf16, int64_t tokens,
+                         int64_t topk, int64_t experts, int64_t* send_ids, void* w_sorted_bf16,
+                         int64_t* starts, int64_t* rows, int64_t* cols, int32_t* pair_pos,
+                         void* stream);
 
 /*
  * Grouped SwiGLU over resident cache slots.  Replaces ferry/csrc/expert_ops.cpp:13-45
