@@ -3,12 +3,19 @@
 // Reference: ferry/model.py:141-146 (Qwen3 hook) and the greedy DeepSeek-V2 gate feeding
 // ferry/model.py:151-157.  torch.topk there selects on the fp32 probabilities with torch's
 // CPU algorithm (std::nth_element + std::sort of the first k-1 entries when k*64 > E, else
-// std::partial_sort; comparator on values only, NaN first).  Softmax is strictly increasing
-// in the logit, so the comparison outcomes -- ties included -- are those of the logits while
-// the probabilities compared are normal fp32 numbers; a row holding a NaN or +inf logit has
-// all-NaN probabilities, i.e. all elements compare equal.  Selection therefore runs on
-// order-preserving uint32 keys of the logits (all equal for such rows), which makes the tie
-// pattern independent of the exp implementation.
+// std::partial_sort; comparator on values only, NaN first).  Two distinct logits can round to
+// the same probability, which torch then treats as a tie, so the selection must run on the
+// probabilities themselves, bit for bit.  The kernel therefore computes them exactly as
+// torch's CPU softmax does (ATen/native/cpu/SoftMaxKernel.cpp, vectorized last-dim path):
+//   m = max of the row; e_i = exp(x_i - m) with SLEEF's expf_u10 (the exp of
+//   Vectorized<float>, ATen/cpu/vec/vec512/vec512_float.h:307-309), restated in sleef_expf;
+//   s = their sum in vec::reduce_all's order for 16-lane vectors (ATen/cpu/vec/
+//   functional_base.h:185-203 and the AVX-512 VecReduceAllSIMD at :78-98); p_i = e_i * (1/s).
+// The renormalising sum of the Qwen3 hook, w.sum(-1), follows torch's CPU sum kernel for a
+// short contiguous last dimension (see topk_weight_sum).  Both orders were identified on
+// torch 2.10's CPU build and are checked against it bit for bit by the tests.  A row holding
+// a NaN or +inf logit has all-NaN probabilities, i.e. all elements compare equal.
+// Selection runs on order-preserving uint32 keys of the probabilities.
 //
 // Fast path (sorted output, nth_element regime, all top-k keys distinct and the k-th above
 // the (k+1)-th): the selection is unique and comes out in descending order; k wavefront
@@ -24,6 +31,9 @@
 //  * the rare remainder (introselect depth limit reached -> heap select; partial_sort regime
 //    k*64 <= n; k - 1 > 16) runs the sequential algorithm on lane 0 over the row in LDS.
 #include "common.h"
+
+// every rounding step below is the reference's: no contraction of a*b+c into one FMA
+#pragma clang fp contract(off)
 
 namespace ferry {
 namespace {
@@ -516,15 +526,6 @@ __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp_asf(dpp_u<0x143, 0xc>(u, u)));
   return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(v), 63));
 }
-__device__ __forceinline__ float wave_sum(float v) {
-  v += dpp_asf(dpp_u<0xB1>(0u, __float_as_uint(v)));
-  v += dpp_asf(dpp_u<0x4E>(0u, __float_as_uint(v)));
-  v += dpp_asf(dpp_u<0x141>(0u, __float_as_uint(v)));
-  v += dpp_asf(dpp_u<0x140>(0u, __float_as_uint(v)));
-  v += dpp_asf(dpp_u<0x142, 0xa>(0u, __float_as_uint(v)));
-  v += dpp_asf(dpp_u<0x143, 0xc>(0u, __float_as_uint(v)));
-  return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(v), 63));
-}
 __device__ __forceinline__ uint32_t umax_(uint32_t a, uint32_t b) { return a > b ? a : b; }
 __device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
   v = umax_(v, dpp_u<0xB1>(v, v));
@@ -534,6 +535,89 @@ __device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
   v = umax_(v, dpp_u<0x142, 0xa>(v, v));
   v = umax_(v, dpp_u<0x143, 0xc>(v, v));
   return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// SLEEF's single-precision exp with 1.0-ulp bound (xexpf of SLEEF 3, sleefsimdsp.c; the
+// published Cody-Waite reduction by ln 2 in two parts, a degree-6 polynomial for e^s - 1 - s in
+// Horner form with fused multiply-adds, and a two-step scaling by 2^q).  Restated from that
+// method; checked against the SLEEF routine torch calls on all 2^32 fp32 inputs.
+__device__ __forceinline__ float pow2i_(int q) { return __uint_as_float((uint32_t)(q + 0x7f) << 23); }
+__device__ __forceinline__ float sleef_expf(float d) {
+  if (d != d) return d;
+  if (d < -104.f) return 0.f;
+  if (d > 100.f) return INFINITY;
+  const float kRln2 = 1.442695040888963407359924681001892137f;
+  const float kL2U = 0.693145751953125f, kL2L = 1.428606765330187045e-06f;
+  const int q = (int)__builtin_rintf(d * kRln2);
+  float s = __builtin_fmaf((float)q, -kL2U, d);
+  s = __builtin_fmaf((float)q, -kL2L, s);
+  float u = 0.000198527617612853646278381f;
+  u = __builtin_fmaf(u, s, 0.00139304355252534151077271f);
+  u = __builtin_fmaf(u, s, 0.00833336077630519866943359f);
+  u = __builtin_fmaf(u, s, 0.0416664853692054748535156f);
+  u = __builtin_fmaf(u, s, 0.166666671633720397949219f);
+  u = __builtin_fmaf(u, s, 0.5f);
+  u = 1.0f + __builtin_fmaf(s * s, u, s);
+  return u * pow2i_(q >> 1) * pow2i_(q - (q >> 1));
+}
+
+// Sum of e[0..n) (in LDS) in the order of torch's vec::reduce_all(+) for 16-lane vectors:
+// n < 16: left to right; otherwise lane l of an accumulator vector adds e[16c + l] over the
+// full chunks c in order, the tail chunk adds into its first n % 16 lanes, and the 16 lanes are
+// combined by the halving butterfly (l + 8, then l + 4, l + 2, l + 1).  Wave-uniform result.
+__device__ __forceinline__ float torch_softmax_sum(const float* e, int n, int lane) {
+  float acc = 0.f;
+  if (n < 16) {
+    if (lane == 0) {
+      acc = e[0];
+      for (int i = 1; i < n; ++i) acc += e[i];
+    }
+  } else if (lane < 16) {
+    acc = e[lane];
+    const int full = n - n % 16;
+    for (int c = 16; c < full; c += 16) acc += e[c + lane];
+    if (lane < n - full) acc += e[full + lane];
+  }
+  if (n >= 16) {
+#pragma unroll
+    for (int h = 8; h >= 1; h >>= 1) acc += __shfl_down(acc, h, 16);
+  }
+  return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(acc), 0));
+}
+
+// torch's CPU sum over a contiguous last dimension of k <= 32 fp32 values (the renormalising
+// w.sum(-1) of the Qwen3 hook), w_j held by lane j.  torch runs its 8-lane (AVX2) reduction
+// kernel here: for k < 8 a scalar sum with four interleaved partial sums (partial j takes
+// w[4i + j], the tail w[4 * (k / 4)..] goes into partial 0, then partial 0 + 1 + 2 + 3); for
+// k >= 8, lane l of an 8-lane vector sums w[8i + l] over the k / 8 full vectors, and the result
+// is the sum, left to right, of the scalar tail w[8 * (k / 8)..] followed by the 8 lanes.
+// Identified by testing against torch's CPU sum for every k <= 32; wave-uniform result.
+__device__ __forceinline__ float topk_weight_sum(float wv, int kk) {
+  auto at = [&](int j) {
+    return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(wv), j));
+  };
+  if (kk < 8) {
+    float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
+    int i = 0;
+    if (kk >= 4) {
+      p0 = at(0);
+      p1 = at(1);
+      p2 = at(2);
+      p3 = at(3);
+      i = 4;
+    }
+    for (; i < kk; ++i) p0 += at(i);
+    return ((p0 + p1) + p2) + p3;
+  }
+  const int nv = kk / 8;
+  float acc = 0.f;
+  for (int i = 8 * nv; i < kk; ++i) acc += at(i);
+  for (int l = 0; l < 8; ++l) {
+    float lane_sum = at(l);
+    for (int v = 1; v < nv; ++v) lane_sum += at(8 * v + l);
+    acc += lane_sum;
+  }
+  return acc;
 }
 
 template <typename T>
@@ -567,19 +651,21 @@ __global__ __launch_bounds__(64 * kWaves) void router_kernel(
       bad |= (e < n) && (x[s] != x[s] || x[s] == INFINITY);
     }
     const bool row_bad = __any(bad);  // softmax of this row is all NaN
-    // softmax in fp32
+    // softmax in fp32, rounding step for rounding step as torch's CPU kernel
     float m = x[0];
 #pragma unroll
     for (int s = 1; s < NS; ++s) m = fmaxf(m, x[s]);
     m = wave_max(m);
-    float ex[NS], part = 0.f;
+    float ex[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       const int e = s * 64 + lane;
-      ex[s] = e < n ? expf(x[s] - m) : 0.f;
-      part += ex[s];
+      ex[s] = e < n ? sleef_expf(x[s] - m) : 0.f;
+      if (e < n) ws.prob[e] = ex[s];
     }
-    const float sum = wave_sum(part);
+    wave_sync_lds();
+    const float sum = torch_softmax_sum(ws.prob, n, lane);
+    wave_sync_lds();
     const float inv = 1.0f / sum;
     uint32_t key[NS];
     int32_t ix[NS];
@@ -591,7 +677,7 @@ __global__ __launch_bounds__(64 * kWaves) void router_kernel(
         ws.prob[e] = p;
         if (probs_out) probs_out[row * n + e] = p;
       }
-      key[s] = e < n ? (row_bad ? 0xffffffffu : ordered_key(x[s])) : 0u;
+      key[s] = e < n ? (row_bad ? 0xffffffffu : ordered_key(p)) : 0u;
       ix[s] = e;
     }
     // fast path: kk arg-max rounds on distinct keys (nth_element regime, sorted output)
@@ -638,8 +724,7 @@ __global__ __launch_bounds__(64 * kWaves) void router_kernel(
       e = ws.sel[lane];
       wv = ws.prob[e];
     }
-    float tot = 0.f;
-    for (int j = 0; j < kk; ++j) tot += __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(wv), j));  // j-ascending like the reference sum
+    const float tot = renorm ? topk_weight_sum(wv, kk) : 0.f;
     if (lane < kk) {
       float w = renorm ? wv / tot : wv;
       w = w * scale;

@@ -25,6 +25,12 @@ def lib():
         h.oracle_plan_layer.restype = i64
         h.oracle_layer_slots.argtypes = [p, i64, i64, i64, p]
         h.oracle_layer_slots.restype = None
+        h.oracle_softmax.argtypes = [p, i64, i64, p]
+        h.oracle_softmax.restype = None
+        h.oracle_weight_sum.argtypes = [p, i64, i64, p]
+        h.oracle_weight_sum.restype = None
+        h.oracle_expf.argtypes = [ctypes.c_float]
+        h.oracle_expf.restype = ctypes.c_float
         _lib = h
     return _lib
 
@@ -39,3 +45,21 @@ def topk(values, k, largest=True, sorted=True):
                          oi.ctypes.data) != 0:
         raise ValueError('bad topk arguments')
     return ov, oi
+
+
+def softmax(x):
+    """torch's CPU softmax over the last dim of fp32 rows, restated (softmax.c)."""
+    v = np.ascontiguousarray(x, np.float32)
+    rows, n = v.shape
+    out = np.empty_like(v)
+    lib().oracle_softmax(v.ctypes.data, rows, n, out.ctypes.data)
+    return out
+
+
+def weight_sum(w):
+    """torch's CPU sum over the last dim of fp32 rows of k <= 32, restated (softmax.c)."""
+    v = np.ascontiguousarray(w, np.float32)
+    rows, k = v.shape
+    out = np.empty(rows, np.float32)
+    lib().oracle_weight_sum(v.ctypes.data, rows, k, out.ctypes.data)
+    return out

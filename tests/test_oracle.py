@@ -327,3 +327,132 @@ def test_pack_dispatch_oracle_matches_closed_form():
     _, pw = unpack_dispatch_ref(p, 4, 3)
     assert pw.float().tolist() == [[0.75, 0.125, 0.0]]
     assert p[0, -3:].tolist() == [2, 5, 255]
+
+
+# ---------------------------------------------------------------------------------------------
+# torch's CPU softmax and renormalising sum, restated bit for bit (oracle/softmax.c)
+# ---------------------------------------------------------------------------------------------
+
+def _rows(E, rows, seed, dtype, scale=3.0):
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((rows, E), generator=g) * scale
+    if rows > 8:
+        x[0, 0] = float('-inf')                     # exp underflows to 0
+        x[1, :] = x[1, 0]                           # all equal
+        x[2, E // 2] = 200.0                        # the others underflow
+        x[3, -1] = -150.0
+    return x.to(dtype)
+
+
+@pytest.mark.parametrize('E', [1, 2, 7, 8, 15, 16, 17, 20, 64, 100, 128, 200, 256])
+def test_softmax_restatement_bit_exact_vs_torch(E):
+    """The restated softmax (SLEEF expf_u10, reduce_all's 16-lane sum order, reciprocal
+    multiply) equals torch.softmax on the CPU bit for bit, for fp32 and bf16 logits."""
+    import torch
+    from oracle.native import softmax
+    for dtype in (torch.float32, torch.bfloat16):
+        for scale in (0.5, 3.0, 30.0):
+            x = _rows(E, 600, seed=E + int(scale * 10), dtype=dtype, scale=scale)
+            ref = torch.softmax(x, -1, dtype=torch.float32).numpy()
+            got = softmax(x.float().numpy())
+            assert np.array_equal(got.view(np.int32), ref.view(np.int32)), (E, dtype, scale)
+
+
+def test_softmax_restatement_special_rows():
+    """NaN and +inf logits make the whole row NaN; -inf logits give probability 0."""
+    import torch
+    from oracle.native import softmax
+    x = torch.tensor([[1.0, float('nan'), 0.0, 2.0], [float('inf'), 0.0, 1.0, 1.0],
+                      [float('-inf'), 0.0, 1.0, float('-inf')], [float('-inf')] * 4])
+    ref = torch.softmax(x, -1).numpy()
+    got = softmax(x.numpy())
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    assert np.array_equal(got[ok].view(np.int32), ref[ok].view(np.int32))
+
+
+def test_expf_restatement_within_one_ulp():
+    """The restated SLEEF expf is within 1 ulp of the correctly rounded exp on a dense sweep of
+    the softmax range [-104, 0] (its published error bound), and exact at the end points."""
+    from oracle.native import lib
+    d = np.linspace(-104.0, 0.0, 200001).astype(np.float32)
+    got = np.array([lib().oracle_expf(float(v)) for v in d[::7]], np.float32)
+    exact = np.exp(d[::7].astype(np.float64)).astype(np.float32)
+    ulp = np.abs(got.view(np.int32).astype(np.int64) - exact.view(np.int32).astype(np.int64))
+    assert ulp.max() <= 1
+    assert lib().oracle_expf(0.0) == 1.0 and lib().oracle_expf(-105.0) == 0.0
+
+
+@pytest.mark.parametrize('k', list(range(1, 33)))
+def test_weight_sum_restatement_bit_exact_vs_torch(k):
+    """The restated renormalising sum equals torch's CPU w.sum(-1) for every k <= 32, on top-k
+    values in both the sorted and the unsorted output order."""
+    import torch
+    from oracle.native import weight_sum
+    g = torch.Generator().manual_seed(k)
+    p = torch.softmax(torch.randn((3000, 256), generator=g) * 2, -1)
+    for srt in (True, False):
+        w, _ = torch.topk(p, k, dim=-1, sorted=srt)
+        ref = w.sum(-1).numpy()
+        got = weight_sum(w.numpy())
+        assert np.array_equal(got.view(np.int32), ref.view(np.int32)), (k, srt)
+
+
+def fp32_near_tie_rows(T, E, k, seed):
+    """fp32 logits with a pair of distinct values one ulp apart straddling the top-k boundary
+    (positions k - 1 and k of the descending order), the case where torch's softmax can round
+    two different logits to the same probability."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((T, E)).astype(np.float32)
+    order = np.argsort(-x, axis=1, kind='stable')
+    for t in range(T):
+        a, b = order[t, k - 1], order[t, k]
+        x[t, b] = np.nextafter(x[t, a], np.float32(-np.inf))
+    return x
+
+
+def test_fp32_near_ties_collapse_in_torch_and_restatement():
+    """Distinct fp32 logits one ulp apart at the k boundary: torch's softmax maps many such
+    pairs to equal probabilities (then torch.topk breaks the tie by its algorithm, not by the
+    logit order), and the restated softmax reproduces exactly which pairs collapse."""
+    import torch
+    from oracle.native import softmax, topk
+    for E, k in ((64, 6), (128, 8)):
+        x = fp32_near_tie_rows(4000, E, k, seed=E)
+        p_ref = torch.softmax(torch.from_numpy(x), -1).numpy()
+        p = softmax(x)
+        assert np.array_equal(p.view(np.int32), p_ref.view(np.int32))
+        order = np.argsort(-x, axis=1, kind='stable')
+        a = np.take_along_axis(p, order[:, k - 1:k], 1)[:, 0]
+        b = np.take_along_axis(p, order[:, k:k + 1], 1)[:, 0]
+        collapsed = a == b
+        assert collapsed.sum() > 100, collapsed.sum()
+        # on those rows the CPU top-k set is not the logit order's set in some rows
+        _, idx = torch.topk(torch.from_numpy(p_ref), k, dim=-1)
+        by_logit = np.sort(order[:, :k], axis=1)
+        differs = (np.sort(idx.numpy(), axis=1) != by_logit).any(1)
+        assert differs.sum() > 0 and not differs[~collapsed].any()
+        # and the topk restatement follows torch on the collapsed probabilities
+        _, oi = topk(p_ref, k, sorted=True)
+        assert np.array_equal(oi, idx.numpy())
+
+
+def test_router_oracle_equals_torch_op_sequence():
+    """The router oracle (restated softmax and sum) equals the reference's torch op sequence
+    run on this CPU: softmax(fp32), topk, w / w.sum(-1), bf16 -- indices, weights and
+    probabilities bit for bit."""
+    import torch
+    from oracle.router import deepseek_router, qwen3_router
+    g = torch.Generator().manual_seed(21)
+    for E, k, dtype in ((128, 8, torch.bfloat16), (64, 6, torch.float32), (256, 32, torch.bfloat16),
+                        (16, 5, torch.float32)):
+        x = (torch.randn((2000, E), generator=g) * 2).to(dtype)
+        w, sel, p = qwen3_router(x, k)
+        p_t = torch.softmax(x, -1, dtype=torch.float32)
+        w_t, sel_t = torch.topk(p_t, k, dim=-1)
+        w_t = (w_t / w_t.sum(-1, keepdim=True)).to(torch.bfloat16)
+        assert torch.equal(p, p_t) and torch.equal(sel, sel_t) and torch.equal(w, w_t)
+        w2, sel2, _ = deepseek_router(x.float(), k)
+        w2_t, sel2_t = torch.topk(torch.softmax(x.float(), -1), k, dim=-1, sorted=False)
+        assert torch.equal(sel2, sel2_t) and torch.equal(w2, w2_t.to(torch.bfloat16))
