@@ -1,33 +1,36 @@
 """Benchmark of the per-GPU MoE hot path on one MI355X.
 
-Default workload (the headline metric): the Qwen3-30B-A3B-shaped MoE layer in decode --
-16 tokens per step, 128 experts top-8 (renormalised softmax), hidden 2048, SwiGLU
-intermediate 768, bf16, a 38-slot expert cache with the other experts in pinned host memory,
-router logits N(0, 1) + log Zipf(1.1) popularity (seed 1).  One step = one layer call:
-router kernel -> device history + D2H of the IDs -> host planner -> H2D fetch of the misses
--> layout -> grouped SwiGLU (resident experts first) -> combine.
+Headline (``value``): the Qwen3-30B-A3B-shaped MoE layer in decode -- 16 tokens per step, 128
+experts top-8 (renormalised softmax), hidden 2048, SwiGLU intermediate 768, bf16, a 38-slot
+expert cache with the other experts in pinned host memory, router logits N(0, 1) + log
+Zipf(1.1) popularity (seed 1).  One step = one layer call: router kernel -> device history +
+routing IDs to the host -> host planner -> H2D fetch of the misses -> layout -> grouped SwiGLU
+(resident experts first) -> combine.  The timed pass runs without instrumentation; a second
+pass over the same stream (from an empty cache again) collects per-launch kernel times, fetch
+events and host phase times.
 
-The timed pass runs without instrumentation; a second pass over the same stream (from an empty
-cache again) collects per-launch kernel times, fetch events and host phase times.
-
-Also reported on the same line:
-  * roofline: the decode expert FFN phase-1 kernel (ffn_up_skinny: gate/up projection +
-    SwiGLU, 2/3 of the expert bytes), achieved GB/s on its algorithmic bytes vs 8 TB/s,
-    from HIP events around each launch on the compute stream; traffic from the committed
-    FETCH_SIZE / WRITE_SIZE profile of that kernel;
-  * prefill: the Qwen3-shaped 8192-token layer (experts resident), tokens/s and MFMA
-    utilisation of the grouped GEMMs vs 2.5 PFLOP/s;
-  * prefill_deepseek: the DeepSeek-V2-Lite-shaped 65,536-token layer with its two shared
-    experts (experts resident), the same figures;
-  * fetch: H2D GB/s of the expert copies and the fraction hidden behind compute;
-  * cpu_baseline: the oracle's torch-CPU restatement of the reference op order on the host
-    cores, on a bounded sample of the same decode stream.
-With --decode-loop: the 48-layer Qwen3 decode loop (1024-token prefill, then 64-token steps,
-pooled cache of 1,843 slots) as a decode_loop block.
+Also on the line:
+  * roofline: the decode FFN phase-1 kernel (ffn_up_skinny), achieved GB/s on its algorithmic
+    bytes vs 8 TB/s: bytes per launch / the mean of the per-launch HIP-event durations of all
+    its launches in the instrumented pass; traffic from the committed FETCH_SIZE / WRITE_SIZE
+    profile of that kernel;
+  * roofline_prefill: the tiled up-projection GEMM (ffn_tiled_up) of the Qwen3 prefill layer,
+    TFLOP/s vs 2.5 PFLOP/s bf16, measured the same way;
+  * prefill / prefill_deepseek: the Qwen3 8192-token layer and the DeepSeek-V2-Lite
+    65,536-token layer (with its two shared experts), experts resident;
+  * prefill_stack / prefill_stack_deepseek: those layers over the whole stack (48 / 26 layers,
+    distinct seeded weights and routing per layer) through OffloadRuntime with the pooled 30 %
+    cache (1,843 / 499 slots) from cold, so every layer fetches its missing experts over PCIe;
+  * decode_loop: the 48-layer Qwen3 decode loop (1024-token prefill, then 64-token steps,
+    pooled cache of 1,843, W = 128 eviction), ``--loop-steps`` steps (default 8, bounded);
+  * cpu_baseline: the reference's op order in torch on the host cores (all cores of the
+    process's affinity), median of >= 5 repeats on the decode stream, plus one config-3 prefill
+    layer with the 48-layer extrapolation.
 """
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 from dataclasses import replace
@@ -43,16 +46,15 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 PCIE_PEAK_GBS = 64.0
 
-
 TRAFFIC_PROFILE = ROOT / 'profiles' / 'ffn_up_skinny_decode_qwen3_t16_hbm_traffic.md'
+TILED_TRAFFIC_PROFILE = ROOT / 'profiles' / 'ffn_tiled_prefill_qwen3_t8192_hbm_traffic.md'
 
 
-def traffic_ratio():
-    """HBM traffic / algorithmic bytes of ffn_up_skinny, from the committed counter profile
-    (FETCH_SIZE + WRITE_SIZE, each scaled by a copy kernel of known size), or None."""
+def profile_value(path, key):
+    """``key = value`` line of a committed profile summary, or None."""
     try:
-        for line in TRAFFIC_PROFILE.read_text().splitlines():
-            if line.startswith('traffic_over_algorithmic'):
+        for line in path.read_text().splitlines():
+            if line.startswith(key):
                 return float(line.split('=')[1])
     except OSError:
         pass
@@ -66,18 +68,28 @@ def parse():
     p.add_argument('--warmup', type=int, default=30)
     p.add_argument('--prefill-reps', type=int, default=10)
     p.add_argument('--no-prefill', action='store_true')
+    p.add_argument('--no-stacks', action='store_true',
+                   help='skip the prefill stacks and the decode loop (they build 54 + 29 GB of '
+                        'pinned expert pools)')
     p.add_argument('--no-cpu-baseline', action='store_true')
-    p.add_argument('--cpu-seconds', type=float, default=15.0)
-    p.add_argument('--decode-loop', action='store_true',
-                   help='also run the 48-layer decode loop (1024-token prefill, then 64-token '
-                        'steps; pooled 30%% cache, W = 128 eviction; a 58 GB pinned pool)')
-    p.add_argument('--loop-steps', type=int, default=64)
+    p.add_argument('--cpu-seconds', type=float, default=20.0,
+                   help='CPU time budget of the decode-stream baseline (5 repeats)')
+    p.add_argument('--loop-steps', type=int, default=8, help='decode-loop steps (config 5 runs 64)')
     p.add_argument('--copy-calibration-mib', type=int, default=0,
                    help='run one plain device copy kernel of this many MiB (read and written) '
-                        'before the decode loop: the reference dispatch for scaling HBM byte '
+                        'before the decode pass: the reference dispatch for scaling HBM byte '
                         'counters (FETCH_SIZE / WRITE_SIZE) in profiler runs')
     return p.parse_args()
 
+
+def launch_stats(ops, name):
+    n, ms = ops.timing_summary(name)
+    return dict(launches=n, total_ms=ms, avg_us=ms / n * 1e3 if n else None)
+
+
+# ---------------------------------------------------------------------------------------------
+# config 2: the decode layer (headline)
+# ---------------------------------------------------------------------------------------------
 
 def decode_stream(w, steps, device):
     """Feasible steps of the seeded decode stream: (logits bf16 [T, E], x bf16 [T, H])."""
@@ -102,8 +114,7 @@ def run_decode(args, device):
     w = workloads.CONFIGS[2]
     spec = w.spec
     pool = workloads.make_pool(spec, 1, seed=0)
-    rt = OffloadRuntime(spec, pool, [w.cache_slots], 'ferry', Topology.uniform(1, spec.experts),
-                        timing=False)
+    rt = OffloadRuntime(spec, pool, [w.cache_slots], 'ferry', Topology.uniform(1, spec.experts))
     stream = decode_stream(w, args.warmup + args.steps, device)
 
     def step(lg, x):
@@ -136,24 +147,60 @@ def run_decode(args, device):
     torch.cuda.synchronize()
     t3 = time.perf_counter()
     ks = dict(rt.kernel_bytes)
-    ks['up_launches'], ks['up_ms'] = ops.timing_summary('ffn_up_skinny')
-    ks['down_launches'], ks['down_ms'] = ops.timing_summary('ffn_down_skinny')
-    ks['kernels'] = {name: ops.timing_summary(name) for name in
-                     ('router_kernel', 'history_kernel', 'layout_single', 'ffn_up_skinny',
-                      'ffn_down_skinny', 'combine_kernel')}
+    names = ('router_kernel', 'history_kernel', 'layout_single', 'ffn_up_skinny', 'ffn_down_skinny',
+             'combine_kernel')
+    ks['launch'] = {name: launch_stats(ops, name) for name in names}
     fetch_ms, exposed_ms, overlap_ms = rt.fetch_timing()   # reads the launch log: before disabling
     ops.timing_enable(False)
-    elapsed = t1 - t0
-    tokens = w.tokens * args.steps
-    res = dict(workload=w, elapsed=elapsed, instrumented_elapsed=t3 - t2, tokens=tokens,
-               copies=copies, kernels=ks, fetch_ms=fetch_ms, exposed_ms=exposed_ms,
-               overlap_ms=overlap_ms,
-               expert_bytes=spec.expert_bytes, samples=stream[args.warmup:],
-               host_ns=dict(rt.host_ns))
+    res = dict(workload=w, elapsed=t1 - t0, instrumented_elapsed=t3 - t2,
+               tokens=w.tokens * args.steps, copies=copies, kernels=ks, fetch_ms=fetch_ms,
+               exposed_ms=exposed_ms, overlap_ms=overlap_ms, expert_bytes=spec.expert_bytes,
+               samples=stream[args.warmup:], host_ns=dict(rt.host_ns))
     rt.close()
     del pool
     return res
 
+
+def decode_block(dec, args):
+    ks = dec['kernels']
+    up, down = ks['launch']['ffn_up_skinny'], ks['launch']['ffn_down_skinny']
+    up_gbs = ks['up'] / (up['total_ms'] * 1e-3) / 1e9
+    down_gbs = ks['down'] / (down['total_ms'] * 1e-3) / 1e9
+    ffn_ms = up['total_ms'] + down['total_ms']
+    ffn_gbs = (ks['up'] + ks['down']) / (ffn_ms * 1e-3) / 1e9
+    fetch_bytes = dec['copies'] * dec['expert_bytes']
+    h2d_gbs = fetch_bytes / (dec['fetch_ms'] * 1e-3) / 1e9 if dec['fetch_ms'] else None
+    ratio = profile_value(TRAFFIC_PROFILE, 'traffic_over_algorithmic')
+    bytes_per_launch = ks['up'] / max(1, up['launches'])
+    roofline = dict(kernel='ffn_up_skinny (decode gate/up + SwiGLU)', bound='hbm', achieved=up_gbs,
+                    peak=HBM_PEAK_GBS, unit='GB/s', frac=up_gbs / HBM_PEAK_GBS,
+                    traffic=bytes_per_launch * ratio if ratio else None,
+                    traffic_over_algorithmic=ratio,
+                    traffic_source=TRAFFIC_PROFILE.name if ratio else None,
+                    launches=up['launches'], avg_launch_us=up['avg_us'],
+                    bytes_per_launch=bytes_per_launch,
+                    average='mean of per-launch HIP-event durations (compute stream) over every '
+                            'launch of the instrumented pass; warmup launches excluded')
+    block = dict(ffn_up_gbs=up_gbs, ffn_down_gbs=down_gbs, ffn_gbs=ffn_gbs,
+                 ffn_frac=ffn_gbs / HBM_PEAK_GBS, ffn_ms_per_step=ffn_ms / args.steps,
+                 active_experts_per_step=ks['experts'] / args.steps,
+                 misses_per_step=dec['copies'] / args.steps,
+                 h2d_gbs=h2d_gbs, h2d_frac=(h2d_gbs / PCIE_PEAK_GBS) if h2d_gbs else None,
+                 fetch_ms_per_step=dec['fetch_ms'] / args.steps,
+                 fetch_hidden_frac=dec['overlap_ms'] / dec['fetch_ms'] if dec['fetch_ms'] else None,
+                 fetch_exposed_frac=dec['exposed_ms'] / dec['fetch_ms'] if dec['fetch_ms'] else None,
+                 hidden_cap=min(1.0, ffn_ms / dec['fetch_ms']) if dec['fetch_ms'] else None,
+                 kernel_us_per_step={n: v['total_ms'] / args.steps * 1e3
+                                     for n, v in ks['launch'].items()},
+                 kernel_avg_launch_us={n: v['avg_us'] for n, v in ks['launch'].items()},
+                 host_us_per_step={n: v / args.steps / 1e3 for n, v in dec['host_ns'].items()},
+                 instrumented_ms_per_step=dec['instrumented_elapsed'] / args.steps * 1e3)
+    return roofline, block
+
+
+# ---------------------------------------------------------------------------------------------
+# configs 3 / 4: one prefill layer, experts resident
+# ---------------------------------------------------------------------------------------------
 
 def run_prefill(args, device, config=3):
     """One prefill layer with every expert resident in HBM: the Qwen3-shaped 8192-token layer
@@ -197,42 +244,120 @@ def run_prefill(args, device, config=3):
     for _ in range(args.prefill_reps):
         layer()
     torch.cuda.synchronize()
-    kern = {name: ops.timing_summary(name) for name in
-            ('router_kernel', 'layout_count', 'layout_scan', 'layout_scatter', 'ffn_up_skinny',
-             'ffn_tiled_up', 'ffn_down_skinny', 'ffn_tiled_down', 'combine_kernel')}
+    names = ('router_kernel', 'layout_count', 'layout_scan', 'layout_scatter', 'ffn_up_skinny',
+             'ffn_tiled_up', 'ffn_down_skinny', 'ffn_tiled_down', 'combine_kernel')
+    kern = {name: launch_stats(ops, name) for name in names}
     ops.timing_enable(False)
-    per = lambda name: kern[name][1] / max(1, args.prefill_reps)  # noqa: E731
+    per = lambda name: kern[name]['total_ms'] / max(1, args.prefill_reps)  # noqa: E731
     up_ms = per('ffn_up_skinny') + per('ffn_tiled_up')
     down_ms = per('ffn_down_skinny') + per('ffn_tiled_down')
     flops = 2 * 3 * H * I * int(counts.sum()) + (2 * 3 * H * Is * T if Is else 0)
+    tiled_rows = int(counts[counts > 64].sum()) + (T if Is else 0)
+    tiled_up_flops = 2 * 2 * H * (I * int(counts[counts > 64].sum()) + (Is * T if Is else 0))
     gemm_ms = up_ms + down_ms
     name = ('qwen3_30b_a3b_moe_prefill_t8192_layer_resident' if config == 3 else
             'deepseek_v2_lite_moe_prefill_t65536_layer_resident_shared2')
+    tu = kern['ffn_tiled_up']
+    # the shared experts' launches add to the tiled kernel's launch count (one per layer call)
+    tiled_up_launch_flops = tiled_up_flops / max(1, tu['launches'] / args.prefill_reps)
     return dict(workload=name, tokens=T, tokens_per_s=T / ((t1 - t0) / args.prefill_reps),
                 layer_ms=(t1 - t0) / args.prefill_reps * 1e3,
                 gemm_ms=gemm_ms, up_ms=up_ms, down_ms=down_ms, gemm_tflop=flops / 1e12,
                 mfma_tflops=flops / (gemm_ms * 1e-3) / 1e12,
                 mfma_util=flops / (gemm_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
                 active_experts=int((counts > 0).sum()), max_rows=int(counts.max()),
-                median_rows=float(np.median(counts[counts > 0])),
-                kernel_ms={name: per(name) for name in kern})
+                median_rows=float(np.median(counts[counts > 0])), tiled_rows=tiled_rows,
+                tiled_up_launch_tflop=tiled_up_launch_flops / 1e12,
+                tiled_up_avg_us=tu['avg_us'],
+                kernel_ms={n: per(n) for n in kern},
+                kernel_avg_launch_us={n: v['avg_us'] for n, v in kern.items()})
 
 
-def run_decode_loop(args, device):
+def prefill_roofline(pre):
+    """MFMA roofline of the tiled up-projection launch of the Qwen3 prefill layer."""
+    tflops = pre['tiled_up_launch_tflop'] / (pre['tiled_up_avg_us'] * 1e-6)
+    ratio = profile_value(TILED_TRAFFIC_PROFILE, 'up_traffic_over_algorithmic')
+    return dict(kernel='ffn_tiled_up (prefill gate/up GEMM + SwiGLU, experts > 64 rows)',
+                bound='mfma', achieved=tflops, peak=BF16_PEAK_TFLOPS, unit='TFLOP/s',
+                frac=tflops / BF16_PEAK_TFLOPS, traffic_over_algorithmic=ratio,
+                traffic_source=TILED_TRAFFIC_PROFILE.name if ratio else None,
+                flop_per_launch=pre['tiled_up_launch_tflop'] * 1e12,
+                avg_launch_us=pre['tiled_up_avg_us'],
+                average='mean of per-launch HIP-event durations over the instrumented repeats')
+
+
+# ---------------------------------------------------------------------------------------------
+# configs 3 / 4 over the whole stack, and config 5
+# ---------------------------------------------------------------------------------------------
+
+def run_prefill_stack(device, config, pool):
+    """Every MoE layer of the model on one prefill batch through OffloadRuntime with the pooled
+    30 % cache, from cold.  Pass 1 is timed; pass 2 (after a reset) records fetch events."""
+    from ferry_amd import expert_ops as ops
+    from ferry_amd import workloads
+    from ferry_amd.quota import Topology
+    from ferry_amd.runtime import OffloadRuntime
+    w = workloads.CONFIGS[config]
+    spec = w.spec
+    L, E, k, H, T = w.layers, spec.experts, spec.topk, spec.hidden, w.tokens
+    gen = workloads.RouterLogits(w, device)
+    logits = [gen.next(layer, T) for layer in range(L)]
+    x = workloads.hidden_states(T, H, seed=w.seed + 7, device=device)
+    shared = None
+    if w.shared_intermediate:
+        rows = workloads.shared_rows(L, H, w.shared_intermediate, seed=w.seed, device=device)
+        shared = [ops.SharedExpert(rows[layer], H, w.shared_intermediate) for layer in range(L)]
+    rt = OffloadRuntime(spec, pool, [w.cache_slots], 'ferry', Topology.uniform(1, E))
+
+    def stack():
+        for layer in range(L):
+            wts, sel = ops.router_topk(logits[layer], k, renorm=w.renorm, sorted=w.sorted,
+                                       scale=1.0)
+            rt.execute(layer, x, sel, wts, None, shared=shared[layer] if shared else None)
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    stack()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    copies = rt.h2d.copies
+    rt.reset()
+    rt.timing = True
+    ops.timing_enable(True)
+    t2 = time.perf_counter()
+    stack()
+    torch.cuda.synchronize()
+    t3 = time.perf_counter()
+    fetch_ms, exposed_ms, overlap_ms = rt.fetch_timing()
+    ffn_ms = sum(ops.timing_summary(n)[1] for n in
+                 ('ffn_up_skinny', 'ffn_tiled_up', 'ffn_down_skinny', 'ffn_tiled_down'))
+    ops.timing_enable(False)
+    flops = rt.kernel_bytes['flops'] + (2 * 3 * H * w.shared_intermediate * T * L if shared else 0)
+    rt.close()
+    return dict(workload=w.name, layers=L, tokens=T, cache_slots=w.cache_slots,
+                stack_ms=(t1 - t0) * 1e3, tokens_per_s=T / (t1 - t0),
+                instrumented_stack_ms=(t3 - t2) * 1e3, misses_per_layer=copies / L,
+                h2d_gbs=copies * spec.expert_bytes / (fetch_ms * 1e-3) / 1e9 if fetch_ms else None,
+                fetch_ms_per_layer=fetch_ms / L, ffn_ms_per_layer=ffn_ms / L,
+                gemm_tflop_per_layer=flops / L / 1e12,
+                fetch_hidden_frac=overlap_ms / fetch_ms if fetch_ms else None,
+                fetch_exposed_frac=exposed_ms / fetch_ms if fetch_ms else None,
+                hidden_cap=min(1.0, ffn_ms / fetch_ms) if fetch_ms else None)
+
+
+def run_decode_loop(device, steps, pool):
     """Qwen3-30B-A3B decode loop over all 48 MoE layers: a 1024-token prefill layer pass, then
-    ``loop_steps`` steps of 64 tokens, routing from the seeded temporal-locality process, a pooled
+    ``steps`` steps of 64 tokens, routing from the seeded temporal-locality process, a pooled
     cache of 1,843 slots with GateHistory W = 128 eviction."""
     import hashlib
+    from ferry_amd import expert_ops as ops
     from ferry_amd import workloads
     from ferry_amd.quota import Topology
     from ferry_amd.runtime import OffloadRuntime
     w = workloads.CONFIGS[5]
     spec = w.spec
-    L, E, k, H, I = w.layers, spec.experts, spec.topk, spec.hidden, spec.intermediate
-    t0 = time.perf_counter()
-    routing = workloads.decode_loop_routing(w, steps=args.loop_steps)
-    pool = workloads.make_pool(spec, L, seed=w.seed)
-    setup_s = time.perf_counter() - t0
+    L, E, H = w.layers, spec.experts, spec.hidden
+    routing = workloads.decode_loop_routing(w, steps=steps)
     rt = OffloadRuntime(spec, pool, [w.cache_slots], 'ferry', Topology.uniform(1, E))
     g = torch.Generator(device=device)
     g.manual_seed(w.seed)
@@ -248,78 +373,133 @@ def run_decode_loop(args, device):
     t1 = time.perf_counter()
     prefill_copies = rt.h2d.copies
     rt.timing = True
-    from ferry_amd import expert_ops as ops_timing
-    ops_timing.timing_enable(True)
+    ops.timing_enable(True)
     t2 = time.perf_counter()
-    for s in range(args.loop_steps):
+    for s in range(steps):
         for layer in range(L):
             sel = torch.from_numpy(routing['decode'][s, layer]).to(device)
             rt.execute(layer, xs[w.tokens], sel, routing['decode_weights'][s, layer].to(device), None)
         digest.update(rt.controller.slots[0].tobytes())
     torch.cuda.synchronize()
     t3 = time.perf_counter()
-    up = ops_timing.timing_summary('ffn_up_skinny')[1] + ops_timing.timing_summary('ffn_tiled_up')[1]
-    down = (ops_timing.timing_summary('ffn_down_skinny')[1]
-            + ops_timing.timing_summary('ffn_tiled_down')[1])
-    fetch_ms, exposed_ms, overlap_ms = rt.fetch_timing()   # reads the launch log: before disabling
-    ops_timing.timing_enable(False)
+    ffn = sum(ops.timing_summary(n)[1] for n in
+              ('ffn_up_skinny', 'ffn_tiled_up', 'ffn_down_skinny', 'ffn_tiled_down'))
+    fetch_ms, exposed_ms, overlap_ms = rt.fetch_timing()
+    ops.timing_enable(False)
     copies = rt.h2d.copies - prefill_copies
-    calls = args.loop_steps * L
+    calls = steps * L
     res = dict(
-        workload=w.name, layers=L, steps=args.loop_steps, tokens_per_step=w.tokens,
-        cache_slots=w.cache_slots, setup_s=setup_s,
+        workload=w.name, layers=L, steps=steps, tokens_per_step=w.tokens, cache_slots=w.cache_slots,
         prefill_ms_per_layer=(t1 - t0) / L * 1e3, prefill_fetches=prefill_copies,
-        decode_tokens_per_s=w.tokens * args.loop_steps / (t3 - t2),
+        decode_tokens_per_s=w.tokens * steps / (t3 - t2),
         decode_ms_per_layer_step=(t3 - t2) / calls * 1e3,
         misses_per_layer_step=copies / calls,
         h2d_gbs=copies * spec.expert_bytes / (fetch_ms * 1e-3) / 1e9 if fetch_ms else None,
         fetch_ms_per_layer_step=fetch_ms / calls,
         fetch_hidden_frac=overlap_ms / fetch_ms if fetch_ms else None,
         fetch_exposed_frac=exposed_ms / fetch_ms if fetch_ms else None,
-        ffn_ms_per_layer_step=(up + down) / calls,
-        hidden_cap=min(1.0, (up + down) / fetch_ms) if fetch_ms else None,
-        eviction_state_sha1=digest.hexdigest())
+        ffn_ms_per_layer_step=ffn / calls,
+        hidden_cap=min(1.0, ffn / fetch_ms) if fetch_ms else None,
+        eviction_state_sha1=digest.hexdigest(),
+        note='decode steps timed with per-launch instrumentation on; config 5 runs 64 steps')
     rt.close()
-    del pool
     return res
 
 
-def cpu_baseline(dec, seconds):
-    """The oracle's torch-CPU restatement of the reference op order on the decode stream."""
+# ---------------------------------------------------------------------------------------------
+# CPU baseline: the reference's op order in torch on the host cores
+# ---------------------------------------------------------------------------------------------
+
+def cpu_model():
+    try:
+        for line in Path('/proc/cpuinfo').read_text().splitlines():
+            if line.startswith('model name'):
+                return line.split(':', 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def cpu_layer(logits, x, pool_rows, planner, hist, step, E, k, H, I, renorm=True):
+    """One layer call in the reference's op order (model.py:141-146, metadata.py, policy.py,
+    layout.py, expert_ops.cpp:54-121) with torch / numpy on the CPU."""
     from oracle.experts import execute_experts_ref, reduce_partials_ref
-    from oracle.history import GateHistoryRef, frequency_rows
+    from oracle.history import frequency_rows
     from oracle.layout import layout_closed_form
+    probs = torch.softmax(logits, dim=-1, dtype=torch.float32)
+    wts, sel = torch.topk(probs, k, dim=-1)
+    if renorm:
+        wts = wts / wts.sum(-1, keepdim=True)
+    wts = wts.to(torch.bfloat16)
+    if planner is not None:
+        hist.update(0, frequency_rows(sel.numpy(), E, 128))
+        planner.plan(step, 0, sel.numpy(), hist.scores(0))
+    lay = layout_closed_form(sel.numpy(), E, wts.float().numpy())
+    w_sorted = torch.from_numpy(lay['w_sorted']).to(torch.bfloat16)
+    groups = [e for e in range(E) if lay['counts'][e] > 0]
+    rows = [torch.from_numpy(lay['rows'][lay['starts'][e]:lay['starts'][e + 1]]) for e in groups]
+    cols = [torch.from_numpy(lay['cols'][lay['starts'][e]:lay['starts'][e + 1]]) for e in groups]
+    parts = execute_experts_ref([pool_rows(e) for e in groups], x, w_sorted, rows, cols, H, I)
+    return reduce_partials_ref(parts, rows, x.shape[0], H)
+
+
+def cpu_baseline(dec, seconds, device, with_prefill=True):
+    from oracle.history import GateHistoryRef
     from oracle.policy import PlannerRef
-    from oracle.router import qwen3_router
     from ferry_amd import workloads
     w = dec['workload']
     spec = w.spec
-    cores = min(16, len(os.sched_getaffinity(0)))
+    cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     E, k, H, I = spec.experts, spec.topk, spec.hidden, spec.intermediate
     pool = workloads.make_pool(spec, 1, seed=0).cpu()   # same rows as the GPU pool
-    planner = PlannerRef(1, E, w.cache_slots)
-    hist = GateHistoryRef(1, E, 128)
     samples = [(lg.cpu(), x.cpu()) for lg, x in dec['samples']]
-    steps = 0
+    planner, hist = PlannerRef(1, E, w.cache_slots), GateHistoryRef(1, E, 128)
+    step = 0
+
+    def run(n):
+        nonlocal step
+        for _ in range(n):
+            lg, x = samples[step % len(samples)]
+            cpu_layer(lg, x, lambda e: pool[e], planner, hist, step, E, k, H, I)
+            step += 1
+
+    run(3)   # warm-up
     t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        lg, x = samples[steps % len(samples)]
-        wts, sel, _ = qwen3_router(lg, k)
-        hist.update(0, frequency_rows(sel.numpy(), E, 128))
-        planner.plan(steps, 0, sel.numpy(), hist.scores(0))
-        lay = layout_closed_form(sel.numpy(), E, wts.float().numpy())
-        w_sorted = torch.from_numpy(lay['w_sorted']).to(torch.bfloat16)
-        groups = [e for e in range(E) if lay['counts'][e] > 0]
-        rows = [torch.from_numpy(lay['rows'][lay['starts'][e]:lay['starts'][e + 1]]) for e in groups]
-        cols = [torch.from_numpy(lay['cols'][lay['starts'][e]:lay['starts'][e + 1]]) for e in groups]
-        parts = execute_experts_ref([pool[e] for e in groups], x, w_sorted, rows, cols, H, I)
-        reduce_partials_ref(parts, rows, x.shape[0], H)
-        steps += 1
-    el = time.perf_counter() - t0
-    return dict(value=steps * w.tokens / el, unit='tokens/s', cores=cores, kind='port',
-                sample=f'{steps} decode steps ({steps * w.tokens} tokens) cycling over the same seeded stream, '
-                       f'{el:.1f} s; experts read from host memory (no H2D copy on the CPU path)')
+    run(5)
+    per_step = (time.perf_counter() - t0) / 5
+    n = max(5, int(seconds / 5 / per_step))
+    rates = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        run(n)
+        rates.append(n * w.tokens / (time.perf_counter() - t0))
+    out = dict(value=statistics.median(rates), unit='tokens/s', cores=cores, kind='port',
+               cpu_model=cpu_model(), repeats=[round(r, 1) for r in rates], statistic='median of 5',
+               sample=f'5 repeats x {n} decode steps ({n * w.tokens} tokens) of the same seeded '
+                      f'stream (config 2); experts read from host memory (no H2D copy on the CPU '
+                      f'path)')
+    if with_prefill:
+        # one config-3 prefill layer (8192 tokens, experts resident in host memory)
+        w3 = workloads.CONFIGS[3]
+        T = w3.tokens
+        lg = workloads.RouterLogits(replace(w3, layers=1), device).next(0, T).cpu()
+        x = workloads.hidden_states(T, H, seed=w3.seed + 7, device=device).cpu()
+        rows3 = workloads.expert_rows(range(E), spec.expert_elements, seed=w3.seed, device=device).cpu()
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            cpu_layer(lg, x, lambda e: rows3[e], None, None, 0, E, k, H, I)
+            times.append(time.perf_counter() - t0)
+        layer_s = statistics.median(times)
+        out['prefill_layer'] = dict(
+            workload='qwen3_30b_a3b_moe_prefill_t8192_layer_resident', layer_s=layer_s,
+            tokens_per_s=T / layer_s, repeats_s=[round(t, 3) for t in times],
+            statistic='median of 3',
+            stack_48_layers_s=48 * layer_s,
+            extrapolation='48 x the median layer time (each layer has the same shape; fetches '
+                          'are not modelled on the CPU path)')
+    return out
 
 
 def main():
@@ -340,56 +520,42 @@ def main():
         del src, dst
     dec = run_decode(args, device)
     w = dec['workload']
-    ks = dec['kernels']
-    up_gbs = ks['up'] / (ks['up_ms'] * 1e-3) / 1e9
-    down_gbs = ks['down'] / (ks['down_ms'] * 1e-3) / 1e9
-    ffn_gbs = (ks['up'] + ks['down']) / ((ks['up_ms'] + ks['down_ms']) * 1e-3) / 1e9
-    value = dec['tokens'] / dec['elapsed']
-    fetch_bytes = dec['copies'] * dec['expert_bytes']
-    h2d_gbs = fetch_bytes / (dec['fetch_ms'] * 1e-3) / 1e9 if dec['fetch_ms'] else None
-    # fraction of the fetch time covered by compute kernels queued while the misses copy
-    hidden = dec['overlap_ms'] / dec['fetch_ms'] if dec['fetch_ms'] else None
-    exposed = dec['exposed_ms'] / dec['fetch_ms'] if dec['fetch_ms'] else None
-    compute_ms = ks['up_ms'] + ks['down_ms']
-    ratio = traffic_ratio()
-    bytes_per_launch = ks['up'] / max(1, ks['up_launches'])
+    roofline, block = decode_block(dec, args)
     line = dict(
         metric='MoE-layer tokens/sec (Qwen3-30B-A3B-shaped decode layer, 16 tok/step, 38/128 cached)',
-        value=value, unit='tokens/s', n_gpus=1, steps=args.steps, warmup=args.warmup,
-        ms_per_step=dec['elapsed'] / args.steps * 1e3, higher_is_better=True, scaling='weak',
-        vs_baseline=None, dtype='bf16', data='synthetic',
+        value=dec['tokens'] / dec['elapsed'], unit='tokens/s', n_gpus=1, steps=args.steps,
+        warmup=args.warmup, ms_per_step=dec['elapsed'] / args.steps * 1e3, higher_is_better=True,
+        scaling='weak', vs_baseline=None, dtype='bf16', data='synthetic',
         config=dict(workload=w.name, tokens_per_step=w.tokens, experts=w.spec.experts,
                     topk=w.spec.topk, hidden=w.spec.hidden, intermediate=w.spec.intermediate,
                     cache_slots=w.cache_slots, router='N(0,1)+log Zipf(1.1), seed 1',
                     parallelism='single GPU (one expert-parallel share)'),
-        roofline=dict(kernel='ffn_up_skinny (decode gate/up + SwiGLU)', bound='hbm',
-                      achieved=up_gbs, peak=HBM_PEAK_GBS, unit='GB/s', frac=up_gbs / HBM_PEAK_GBS,
-                      traffic=bytes_per_launch * ratio if ratio else None,
-                      traffic_over_algorithmic=ratio,
-                      traffic_source=TRAFFIC_PROFILE.name if ratio else None,
-                      launches=ks['up_launches'],
-                      avg_launch_us=ks['up_ms'] / max(1, ks['up_launches']) * 1e3,
-                      bytes_per_launch=bytes_per_launch),
-        decode=dict(ffn_down_gbs=down_gbs, ffn_gbs=ffn_gbs, ffn_frac=ffn_gbs / HBM_PEAK_GBS,
-                    ffn_ms_per_step=compute_ms / args.steps,
-                    active_experts_per_step=ks['experts'] / args.steps,
-                    misses_per_step=dec['copies'] / args.steps,
-                    h2d_gbs=h2d_gbs, h2d_frac=(h2d_gbs / PCIE_PEAK_GBS) if h2d_gbs else None,
-                    fetch_ms_per_step=dec['fetch_ms'] / args.steps,
-                    fetch_hidden_frac=hidden,
-                    fetch_exposed_frac=exposed,
-                    kernel_us_per_step={n: v[1] / args.steps * 1e3 for n, v in ks['kernels'].items()},
-                    host_us_per_step={n: v / args.steps / 1e3 for n, v in dec['host_ns'].items()},
-                    instrumented_ms_per_step=dec['instrumented_elapsed'] / args.steps * 1e3,
-                    hidden_cap=min(1.0, compute_ms / dec['fetch_ms']) if dec['fetch_ms'] else None),
-    )
+        roofline=roofline, decode=block)
+    print(f'# decode done: {line["value"]:.0f} tokens/s', file=sys.stderr, flush=True)
     if not args.no_prefill:
         line['prefill'] = run_prefill(args, device, 3)
+        line['roofline_prefill'] = prefill_roofline(line['prefill'])
         line['prefill_deepseek'] = run_prefill(args, device, 4)
-    if args.decode_loop:
-        line['decode_loop'] = run_decode_loop(args, device)
+        print('# prefill layers done', file=sys.stderr, flush=True)
+    if not args.no_stacks:
+        from ferry_amd import workloads
+        t0 = time.perf_counter()
+        pool = workloads.make_pool(workloads.CONFIGS[3].spec, 48, seed=workloads.CONFIGS[3].seed)
+        pool_s = time.perf_counter() - t0
+        line['prefill_stack'] = run_prefill_stack(device, 3, pool)
+        line['prefill_stack']['pool_build_s'] = pool_s
+        print('# qwen3 prefill stack done', file=sys.stderr, flush=True)
+        line['decode_loop'] = run_decode_loop(device, args.loop_steps, pool)
+        print('# decode loop done', file=sys.stderr, flush=True)
+        del pool
+        w4 = workloads.CONFIGS[4]
+        pool = workloads.make_pool(w4.spec, w4.layers, seed=w4.seed)
+        line['prefill_stack_deepseek'] = run_prefill_stack(device, 4, pool)
+        del pool
+        print('# deepseek prefill stack done', file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
-        line['cpu_baseline'] = cpu_baseline(dec, args.cpu_seconds)
+        line['cpu_baseline'] = cpu_baseline(dec, args.cpu_seconds, device,
+                                            with_prefill=not args.no_prefill)
     print(json.dumps(line), flush=True)
 
 

@@ -54,6 +54,7 @@ SIGNATURES = [
     ('ferry_timing_enable', ctypes.c_int, [_i32]),
     ('ferry_timing_mark', _i64, []),
     ('ferry_timing_range', ctypes.c_int, [_i64, _i64, _c_p]),
+    ('ferry_timing_overlap', ctypes.c_int, [_i64, _i64, _c_p, _c_p, _c_p]),
     ('ferry_timing_summary', ctypes.c_int,
      [ctypes.c_char_p, ctypes.POINTER(_i64), ctypes.POINTER(ctypes.c_double)]),
 ]

@@ -106,6 +106,32 @@ extern "C" int ferry_timing_range(int64_t begin, int64_t end, double* total_ms) 
   return 0;
 }
 
+// Summed overlap in ms of the timed launches at log positions [begin, end) with the window
+// between two caller events t0 and t1 (timing-enabled hipEvent_t, on any stream): for each
+// launch, the length of [start, stop] inside [t0, t1].  Launches of one stream do not overlap
+// each other, so for one stream this is the time the window was covered by its kernels.
+extern "C" int ferry_timing_overlap(int64_t begin, int64_t end, void* t0, void* t1,
+                                    double* total_ms) {
+  std::lock_guard<std::mutex> lock(ferry::g_timing_mu);
+  hipEvent_t a = (hipEvent_t)t0, b = (hipEvent_t)t1;
+  if (hipEventSynchronize(b) != hipSuccess) return 3;
+  float win = 0.f;
+  if (hipEventElapsedTime(&win, a, b) != hipSuccess) return 3;
+  const int64_t n = (int64_t)ferry::g_launches.size();
+  double ms = 0.0;
+  for (int64_t i = begin < 0 ? 0 : begin; i < end && i < n; ++i) {
+    const auto& l = ferry::g_launches[(size_t)i];
+    if (hipEventSynchronize(l.stop) != hipSuccess) return 3;
+    float s = 0.f, e = 0.f;
+    if (hipEventElapsedTime(&s, a, l.start) != hipSuccess) return 3;   // negative if before t0
+    if (hipEventElapsedTime(&e, a, l.stop) != hipSuccess) return 3;
+    const float lo = s > 0.f ? s : 0.f, hi = e < win ? e : win;
+    if (hi > lo) ms += hi - lo;
+  }
+  *total_ms = ms;
+  return 0;
+}
+
 extern "C" const char* ferry_last_error(void) { return ferry::g_last_error.c_str(); }
 
 extern "C" int32_t ferry_abi_version(void) { return 2; }

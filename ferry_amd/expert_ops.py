@@ -51,6 +51,16 @@ def timing_range(begin, end):
     return float(ms.value)
 
 
+def timing_overlap(begin, end, t0, t1):
+    """ms that the timed launches at log positions [begin, end) overlap the window between
+    two timing-enabled torch.cuda.Events (e.g. the first and last copy of a fetch)."""
+    import ctypes
+    ms = ctypes.c_double()
+    check(lib().ferry_timing_overlap(int(begin), int(end), t0.cuda_event, t1.cuda_event,
+                                     ctypes.byref(ms)), 'timing_overlap')
+    return float(ms.value)
+
+
 def current_stream(device=None):
     return torch.cuda.current_stream(device).cuda_stream
 

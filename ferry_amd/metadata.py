@@ -14,30 +14,32 @@ from . import expert_ops as ops
 
 
 class GateHistory:
-    """Per-layer mean of the history rows of the W most recent routed tokens (metadata.py:15-38)."""
+    """Window of the W most recent history rows of every layer; scores = their mean
+    (reference: metadata.py:15-38).  State, as the reference keeps it: ``rows`` float64
+    [layers, W, E] (a ring), ``count`` / ``head`` int64 [layers], ``window``."""
 
     def __init__(self, layers, experts, window=128):
         self.window = window
-        self.rows = np.zeros((layers, window, experts), np.float64)
-        self.count = np.zeros(layers, np.int64)
-        self.head = np.zeros(layers, np.int64)
+        self.rows = np.zeros((layers, window, experts), dtype=np.float64)
+        self.count = np.zeros(layers, dtype=np.int64)
+        self.head = np.zeros(layers, dtype=np.int64)
 
     def update(self, layer, probs):
-        w = self.window
-        probs = np.asarray(probs, np.float64)
-        if len(probs) >= w:
-            self.rows[layer] = probs[-w:]
-            self.count[layer] = w
-            self.head[layer] = 0
+        """Append a batch of rows; a batch of W rows or more replaces the window by its last W."""
+        batch = np.asarray(probs, dtype=np.float64)
+        W, n = self.window, len(batch)
+        if n >= W:
+            self.rows[layer] = batch[n - W:]
+            self.count[layer], self.head[layer] = W, 0
             return
-        for row in probs:
-            self.rows[layer, self.head[layer]] = row
-            self.head[layer] = (self.head[layer] + 1) % w
-            self.count[layer] = min(w, self.count[layer] + 1)
+        ring = (self.head[layer] + np.arange(n)) % W     # n < W: distinct positions
+        self.rows[layer, ring] = batch
+        self.head[layer] = (self.head[layer] + n) % W
+        self.count[layer] = min(W, self.count[layer] + n)
 
     def scores(self, layer):
-        n = max(1, int(self.count[layer]))
-        return (self.rows[layer].sum(0) / n).astype(np.float32)
+        """float32 of the float64 window mean of ``layer``."""
+        return (self.rows[layer].sum(axis=0) / max(1, int(self.count[layer]))).astype(np.float32)
 
 
 class DeviceGateHistory:

@@ -70,28 +70,35 @@ def layer_slots(slots_row, capacity, layer, experts):
 
 
 class Controller:
+    """Placement state of the pooled expert cache and the per-layer planner call
+    (reference: policy.py:208-228).  State arrays, in the reference's shapes: ``slots``
+    [world, cap] (pool key per slot, -1 empty), ``owner`` / ``last`` [layers * experts]
+    (rank holding the key or -1; last-use tick), ``scores`` float32 [layers, experts]."""
+
     def __init__(self, spec, capacities, policy, topology, balance_tol_bps=200, salt=1):
-        self.spec = spec
-        self.policy = POLICIES[policy]
-        self.capacities = np.asarray(capacities, np.int64)
-        if len(self.capacities) != 1:
+        caps = np.asarray(capacities, dtype=np.int64)
+        if caps.size != 1:
             raise NotImplementedError('ferry_amd runs on one GPU (world = 1)')
-        self.balance_tol_bps = int(balance_tol_bps)
-        self.salt = int(salt)
+        self.spec, self.capacities = spec, caps
+        self.policy = POLICIES[policy]
+        self.balance_tol_bps, self.salt = int(balance_tol_bps), int(salt)
         self.masks, self.seconds, self.lut = topology.masks, topology.seconds, topology.lut
         self.reset()
 
     def reset(self):
-        world, layers, experts = len(self.capacities), self.spec.layers, self.spec.experts
-        self.slots = np.full((world, int(self.capacities.max())), -1, np.int64)
-        self.owner = np.full(layers * experts, -1, np.int64)
-        self.last = np.zeros(layers * experts, np.int64)
-        self.scores = np.zeros((layers, experts), np.float32)
+        """Empty cache, nothing used, zero scores."""
+        keys = self.spec.layers * self.spec.experts
+        self.slots = np.full((1, int(self.capacities[0])), -1, dtype=np.int64)
+        self.owner = np.full(keys, -1, dtype=np.int64)
+        self.last = np.zeros(keys, dtype=np.int64)
+        self.scores = np.zeros((self.spec.layers, self.spec.experts), dtype=np.float32)
+        # raw addresses of the state arrays for the fused native call (they never reallocate)
         self._slots_ptr, self._owner_ptr = self.slots.ctypes.data, self.owner.ctypes.data
         self._last_ptr, self._scores_ptr = self.last.ctypes.data, self.scores.ctypes.data
         self._fetch_buf = None
 
     def plan(self, event, layer, selected, origins, gate_scores):
+        """plan_layer on this state: (fetches [m, 3], destinations, per-rank fetch counts)."""
         return plan_layer(event, layer, selected, origins, gate_scores, self.policy, self.slots,
                           self.capacities, self.owner, self.last, self.scores, self.lut,
                           self.masks, self.seconds, self.balance_tol_bps, self.salt)

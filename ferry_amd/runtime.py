@@ -11,7 +11,9 @@ Per MoE layer call (world = 1):
      own stream;
   4. experts already resident run first; the compute stream then waits on the GPU for the
      copies and runs the fetched experts (``overlap=False`` restores the reference's serial
-     host wait);
+     host wait).  A prefill-sized call copies its misses in a few groups, heaviest expert
+     first, and computes each group as soon as its copies land, so that only the lightest
+     group's compute is left after the last copy;
   5. the combine kernel sums each token's k expert rows in fp32 (ascending expert ID).
 """
 import time
@@ -25,6 +27,14 @@ from .hostmem import mapped_buffer
 from .metadata import DeviceGateHistory, GateHistory, RouteGather
 from .policy import Controller, layer_slots
 from .transport import Transport
+
+
+# A layer call with at least this many (token, expert) pairs fetches its misses in up to CHUNKS
+# groups, heaviest first, and computes each group as soon as its copies land.  Decode calls
+# (few pairs, little compute per expert) keep one group: extra launches would cost more than
+# the overlap gains.
+CHUNK_MIN_PAIRS = 16384
+CHUNKS = 6
 
 
 def expert_ops():
@@ -147,74 +157,80 @@ class OffloadRuntime:
         t_sync = time.perf_counter_ns()
         d2h.synchronize()
         t_ready = time.perf_counter_ns()
+        chunked = T * k >= CHUNK_MIN_PAIRS
+        # with chunks or timing the copies are queued here; otherwise the planner's native call
+        # queues them itself, right after planning
+        queue_here = chunked or self.timing
         if frequency:
-            # the planner reads the IDs and scores where the history kernel wrote them and
-            # queues the misses' copies in the same native call (with timing on, the copies
-            # are queued separately, after an event that marks their start on the copy stream)
             fetches, counts = self.controller.plan_fetch(
                 self.event, layer, self._stage_ptr + 4 * E, T, k, self._stage_ptr,
-                None if self.timing else self.h2d.handle)
-            t_plan = time.perf_counter_ns()
-            if self.timing and len(fetches):
-                copy_stream = self.h2d.stream
-                ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
-                ev[0].record(copy_stream)
-                self.h2d.fetch(fetches[:, 2], fetches[:, 1])
+                None if queue_here else self.h2d.handle)
         else:
             self.history.update(layer, tail_host.numpy())
             scores = self.history.scores(layer)
             ids = stage_host.numpy()[4 * E:].astype(np.int64).reshape(T, k)
             fetches, _, counts = self.controller.plan(self.event, layer, ids, np.zeros(T, np.int64),
                                                       scores)
-            t_plan = time.perf_counter_ns()
-            if self.timing and len(fetches):
-                copy_stream = self.h2d.stream
-                ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
-                ev[0].record(copy_stream)
-            self.h2d.fetch(fetches[:, 2], fetches[:, 1])
+            queue_here = True
+        t_plan = time.perf_counter_ns()
+        ids = stage_host.numpy()[4 * E:].astype(np.int64).reshape(T, k)
+        counts_e = np.bincount(ids.reshape(-1), minlength=E)
+        missing_keys = fetches[:, 1] - layer * E
+        # copy order: heaviest expert first, so that the compute left after the last copy is
+        # the lightest (the planner's slot choices do not depend on the order of the copies)
+        if chunked and len(fetches) > 1:
+            order = np.argsort(-counts_e[missing_keys], kind='stable')
+            groups = [g for g in np.array_split(order, min(CHUNKS, len(fetches))) if len(g)]
+        else:
+            groups = [np.arange(len(fetches))]
+        timing = self.timing and len(fetches) > 0
+        if timing:
+            copy_stream = self.h2d.stream
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+            ev[0].record(copy_stream)
+        if queue_here and len(fetches):
+            for g in groups:
+                self.h2d.fetch(fetches[g, 2], fetches[g, 1])
         t_fetch = time.perf_counter_ns()
         self.fetches_per_rank += counts
         if self.event >= spec.layers:
             self.decode_fetches_per_rank += counts
-        fetch_slots = fetches[:, 2].copy()
-        missing_keys = fetches[:, 1] - layer * E
-        timing = self.timing and len(fetch_slots) > 0
         if timing:
             ev[1].record(copy_stream)
-        ids = stage_host.numpy()[4 * E:].astype(np.int64).reshape(T, k)
 
-        # 4. experts: resident first, then the fetched ones
+        # 4. experts: resident first, then the fetched ones (chunk by chunk as they land)
         slot_of = layer_slots(self.controller.slots[0], self.cap, layer, E)
-        active = np.zeros(E, bool)
-        active[ids.reshape(-1)] = True
+        active = counts_e > 0
         missing = np.zeros(E, bool)
         missing[missing_keys] = True
         resident_list = np.flatnonzero(active & ~missing)
-        missing_list = np.flatnonzero(missing)
         slot32 = slot_of.astype(np.int32)
-        counts_e = np.bincount(ids.reshape(-1), minlength=E)
         common = (self.cache, hidden.contiguous(), lay.w_sorted, lay.starts, lay.rows, lay.cols)
-        if not self.overlap and len(fetch_slots):
+        if not self.overlap and len(fetches):
             started = time.perf_counter_ns()
-            self.h2d.wait_host(fetch_slots)
+            self.h2d.wait_host(fetches[:, 2])
             self.serial_wait_ns += time.perf_counter_ns() - started
         mark = self.ops.timing_mark() if timing else 0
         if len(resident_list):
             self.h2d.wait_stream(slot_of[resident_list], stream)
             self._ffn(common, resident_list, slot32, buf, stream, counts_e)
         shared_out = shared(common[1], out=self._shared_out(T)) if shared is not None else None
-        # the launches between the two marks are the compute queued while the misses copy
-        overlap_marks = (mark, self.ops.timing_mark() if timing else 0)
-        if len(missing_list):
-            if timing:
-                ev[2].record(stream)
-            self.h2d.wait_stream(fetch_slots, stream)
-            if timing:
-                ev[3].record(stream)
-            self._ffn(common, missing_list, slot32, buf, stream, counts_e)
+        waits = []
+        if len(fetches):
+            for g in groups:
+                w0 = w1 = None
+                if timing:
+                    w0 = torch.cuda.Event(enable_timing=True)
+                    w0.record(stream)
+                self.h2d.wait_stream(fetches[g, 2], stream)
+                if timing:
+                    w1 = torch.cuda.Event(enable_timing=True)
+                    w1.record(stream)
+                    waits.append((w0, w1))
+                self._ffn(common, np.sort(missing_keys[g]), slot32, buf, stream, counts_e)
         self.h2d.mark_used(slot_of[np.flatnonzero(active)], stream)
         if timing:
-            self.timings.append((ev, overlap_marks))
+            self.timings.append((ev, waits, (mark, self.ops.timing_mark())))
         self.event += 1
 
         # 5. combine (+ the shared experts' output)
@@ -255,16 +271,16 @@ class OffloadRuntime:
     def fetch_timing(self):
         """(total fetch ms, exposed wait ms, overlapped compute ms) over the layer calls recorded
         with timing=True.  fetch: first copy start to last copy end on the copy stream.  exposed:
-        how long the compute stream waited for the copies.  overlapped: per call, the kernel time
-        of the resident experts (and shared experts) queued while the misses copy, at most that
-        call's fetch time; it needs the library's per-launch timing (expert_ops.timing_enable)."""
+        how long the compute stream stalled on the copies.  overlapped: the time, inside each
+        call's fetch window, covered by the compute kernels of that call (resident experts,
+        shared experts, and missing experts whose copies landed early); it needs the library's
+        per-launch timing (expert_ops.timing_enable)."""
         torch.cuda.synchronize(self.device)
         fetch = exposed = overlapped = 0.0
-        for ev, (m0, m1) in self.timings:
-            f = ev[0].elapsed_time(ev[1])
-            fetch += f
-            exposed += max(0.0, ev[2].elapsed_time(ev[3]))
-            overlapped += min(f, self.ops.timing_range(m0, m1))
+        for ev, waits, (m0, m1) in self.timings:
+            fetch += ev[0].elapsed_time(ev[1])
+            exposed += sum(max(0.0, a.elapsed_time(b)) for a, b in waits)
+            overlapped += self.ops.timing_overlap(m0, m1, ev[0], ev[1])
         return fetch, exposed, overlapped
 
     def close(self):

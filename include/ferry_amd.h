@@ -35,6 +35,10 @@ int ferry_timing_enable(int32_t enable);
 int ferry_timing_summary(const char* kernel, int64_t* launches, double* total_ms);
 int64_t ferry_timing_mark(void);
 int ferry_timing_range(int64_t begin, int64_t end, double* total_ms);
+/* time in ms that the launches at log positions [begin, end) overlap the window between the
+ * caller's timing events t0 and t1 (hipEvent_t): the compute that ran while copies were in
+ * flight, when t0 / t1 bracket the copies */
+int ferry_timing_overlap(int64_t begin, int64_t end, void* t0, void* t1, double* total_ms);
 
 enum { FERRY_BF16 = 0, FERRY_F32 = 1 };
 

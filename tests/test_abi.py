@@ -255,3 +255,27 @@ def test_bench_rejects_more_than_one_gpu():
     r = subprocess.run([sys.executable, str(ROOT / 'bench.py'), '--gpus', '2'], capture_output=True,
                        text=True, timeout=300)
     assert r.returncode == 2 and 'one GPU' in r.stdout
+
+
+def test_topology_file_round_trip(tmp_path):
+    """The world-1 topology document the H2D profiler writes loads into Topology like the
+    reference's file (ferry/quota.py:80-90): one domain, quota_lut[m] = [m]; a file for another
+    world size or a table too short for the model is rejected."""
+    import json
+    from ferry_amd.h2dprof import topology_document
+    from ferry_amd.quota import Topology
+    measured = dict(engine=52.5, single_stream=44.0, samples=dict(engine=[52.5], single_stream=[44.0]))
+    doc = topology_document(measured, 9437184, 128, 'qwen3_moe')
+    path = tmp_path / 'topo.json'
+    path.write_text(json.dumps(doc))
+    topo = Topology(path, 1, 128)
+    assert topo.masks.tolist() == [1] and abs(topo.seconds[0] - 1 / 52.5) < 1e-15
+    assert topo.lut.shape == (129, 1) and topo.lut[:, 0].tolist() == list(range(129))
+    uni = Topology.uniform(1, 128)
+    assert np.array_equal(uni.lut, topo.lut) and uni.masks.tolist() == [1]
+    with pytest.raises(ValueError, match='rebuild'):
+        Topology(path, 1, 200)
+    doc['world'] = 2
+    path.write_text(json.dumps(doc))
+    with pytest.raises(ValueError, match='2 GPUs'):
+        Topology(path, 1, 128)

@@ -87,3 +87,18 @@ def test_runtime_qwen3_decode_shape(device):
     rt, skipped = _run(device, spec, cap=38, calls=24, tokens_of=lambda c: 16, seed=1, zipf=1.1,
                        check_every=3, gate_scale=0.0)
     assert skipped < 4 and rt.h2d.copies > 38
+
+
+def test_h2d_profiler_writes_loadable_topology(device, tmp_path):
+    """The H2D profiler measures expert-sized copies through the fetch engine and on one stream
+    and writes a topology file that Topology and OffloadRuntime accept."""
+    from ferry_amd.h2dprof import main
+    from ferry_amd.quota import Topology
+    out = tmp_path / 'topo.json'
+    doc = main(['--output', str(out), '--expert-bytes', str(4 << 20), '--experts', '16',
+                '--copies', '16', '--repeats', '3'])
+    m = doc['measured']
+    assert 1.0 < m['engine_gib_per_s'] < 200.0 and 1.0 < m['single_stream_gib_per_s'] < 200.0
+    assert len(m['samples']['engine']) == 3
+    topo = Topology(out, 1, 16)
+    assert topo.lut[:, 0].tolist() == list(range(17))
