@@ -10,10 +10,10 @@ pass over the same stream (from an empty cache again) collects per-launch kernel
 events and host phase times.
 
 Also on the line:
-  * roofline: the decode FFN phase-1 kernel (ffn_up_skinny), achieved GB/s on its algorithmic
-    bytes vs 8 TB/s: bytes per launch / the mean of the per-launch HIP-event durations of all
-    its launches in the instrumented pass; traffic from the committed FETCH_SIZE / WRITE_SIZE
-    profile of that kernel;
+  * roofline: the decode FFN kernel (ffn_skinny_fused: gate/up + SwiGLU + down in one launch),
+    achieved GB/s on its algorithmic bytes vs 8 TB/s: bytes per launch / the mean of the
+    per-launch HIP-event durations of all its launches in the instrumented pass; traffic from
+    the committed FETCH_SIZE / WRITE_SIZE profile of that kernel;
   * roofline_prefill: the tiled up-projection GEMM (ffn_tiled_up) of the Qwen3 prefill layer,
     TFLOP/s vs 2.5 PFLOP/s bf16, measured the same way;
   * prefill / prefill_deepseek: the Qwen3 8192-token layer and the DeepSeek-V2-Lite
@@ -48,6 +48,7 @@ PCIE_PEAK_GBS = 64.0
 
 TRAFFIC_PROFILE = ROOT / 'profiles' / 'ffn_up_skinny_decode_qwen3_t16_hbm_traffic.md'
 TILED_TRAFFIC_PROFILE = ROOT / 'profiles' / 'ffn_tiled_prefill_qwen3_t8192_hbm_traffic.md'
+FUSED_TRAFFIC_PROFILE = ROOT / 'profiles' / 'ffn_skinny_fused_decode_qwen3_t16_hbm_traffic.md'
 
 
 def profile_value(path, key):
@@ -147,12 +148,13 @@ def run_decode(args, device):
     torch.cuda.synchronize()
     t3 = time.perf_counter()
     ks = dict(rt.kernel_bytes)
-    names = ('router_kernel', 'history_kernel', 'layout_single', 'ffn_up_skinny', 'ffn_down_skinny',
-             'combine_kernel')
+    names = ('router_kernel', 'history_kernel', 'layout_single', 'ffn_skinny_fused', 'ffn_up_skinny',
+             'ffn_down_skinny', 'combine_kernel')
     ks['launch'] = {name: launch_stats(ops, name) for name in names}
     fetch_ms, exposed_ms, overlap_ms = rt.fetch_timing()   # reads the launch log: before disabling
     ops.timing_enable(False)
     res = dict(workload=w, elapsed=t1 - t0, instrumented_elapsed=t3 - t2,
+               sync_timeouts=ops.ffn_sync_timeouts(),
                tokens=w.tokens * args.steps, copies=copies, kernels=ks, fetch_ms=fetch_ms,
                exposed_ms=exposed_ms, overlap_ms=overlap_ms, expert_bytes=spec.expert_bytes,
                samples=stream[args.warmup:], host_ns=dict(rt.host_ns))
@@ -163,26 +165,35 @@ def run_decode(args, device):
 
 def decode_block(dec, args):
     ks = dec['kernels']
-    up, down = ks['launch']['ffn_up_skinny'], ks['launch']['ffn_down_skinny']
-    up_gbs = ks['up'] / (up['total_ms'] * 1e-3) / 1e9
-    down_gbs = ks['down'] / (down['total_ms'] * 1e-3) / 1e9
-    ffn_ms = up['total_ms'] + down['total_ms']
+    lk = ks['launch']
+    fused, up, down = lk['ffn_skinny_fused'], lk['ffn_up_skinny'], lk['ffn_down_skinny']
+    ffn_ms = fused['total_ms'] + up['total_ms'] + down['total_ms']
     ffn_gbs = (ks['up'] + ks['down']) / (ffn_ms * 1e-3) / 1e9
     fetch_bytes = dec['copies'] * dec['expert_bytes']
     h2d_gbs = fetch_bytes / (dec['fetch_ms'] * 1e-3) / 1e9 if dec['fetch_ms'] else None
-    ratio = profile_value(TRAFFIC_PROFILE, 'traffic_over_algorithmic')
-    bytes_per_launch = ks['up'] / max(1, up['launches'])
-    roofline = dict(kernel='ffn_up_skinny (decode gate/up + SwiGLU)', bound='hbm', achieved=up_gbs,
-                    peak=HBM_PEAK_GBS, unit='GB/s', frac=up_gbs / HBM_PEAK_GBS,
+    if fused['launches']:
+        # every decode call runs both phases in the one-launch kernel
+        ratio = profile_value(FUSED_TRAFFIC_PROFILE, 'traffic_over_algorithmic')
+        source = FUSED_TRAFFIC_PROFILE
+        kern, name = fused, 'ffn_skinny_fused (decode gate/up + SwiGLU + down, one launch)'
+        kbytes = ks['up'] + ks['down']
+    else:
+        ratio = profile_value(TRAFFIC_PROFILE, 'traffic_over_algorithmic')
+        source = TRAFFIC_PROFILE
+        kern, name, kbytes = up, 'ffn_up_skinny (decode gate/up + SwiGLU)', ks['up']
+    achieved = kbytes / (kern['total_ms'] * 1e-3) / 1e9
+    bytes_per_launch = kbytes / max(1, kern['launches'])
+    roofline = dict(kernel=name, bound='hbm', achieved=achieved,
+                    peak=HBM_PEAK_GBS, unit='GB/s', frac=achieved / HBM_PEAK_GBS,
                     traffic=bytes_per_launch * ratio if ratio else None,
                     traffic_over_algorithmic=ratio,
-                    traffic_source=TRAFFIC_PROFILE.name if ratio else None,
-                    launches=up['launches'], avg_launch_us=up['avg_us'],
+                    traffic_source=source.name if ratio else None,
+                    launches=kern['launches'], avg_launch_us=kern['avg_us'],
                     bytes_per_launch=bytes_per_launch,
                     average='mean of per-launch HIP-event durations (compute stream) over every '
                             'launch of the instrumented pass; warmup launches excluded')
-    block = dict(ffn_up_gbs=up_gbs, ffn_down_gbs=down_gbs, ffn_gbs=ffn_gbs,
-                 ffn_frac=ffn_gbs / HBM_PEAK_GBS, ffn_ms_per_step=ffn_ms / args.steps,
+    block = dict(ffn_gbs=ffn_gbs, ffn_frac=ffn_gbs / HBM_PEAK_GBS, ffn_ms_per_step=ffn_ms / args.steps,
+                 ffn_sync_timeouts=dec.get('sync_timeouts'),
                  active_experts_per_step=ks['experts'] / args.steps,
                  misses_per_step=dec['copies'] / args.steps,
                  h2d_gbs=h2d_gbs, h2d_frac=(h2d_gbs / PCIE_PEAK_GBS) if h2d_gbs else None,
@@ -330,7 +341,8 @@ def run_prefill_stack(device, config, pool):
     t3 = time.perf_counter()
     fetch_ms, exposed_ms, overlap_ms = rt.fetch_timing()
     ffn_ms = sum(ops.timing_summary(n)[1] for n in
-                 ('ffn_up_skinny', 'ffn_tiled_up', 'ffn_down_skinny', 'ffn_tiled_down'))
+                 ('ffn_skinny_fused', 'ffn_up_skinny', 'ffn_tiled_up', 'ffn_down_skinny',
+                  'ffn_tiled_down'))
     ops.timing_enable(False)
     flops = rt.kernel_bytes['flops'] + (2 * 3 * H * w.shared_intermediate * T * L if shared else 0)
     rt.close()
@@ -383,7 +395,8 @@ def run_decode_loop(device, steps, pool):
     torch.cuda.synchronize()
     t3 = time.perf_counter()
     ffn = sum(ops.timing_summary(n)[1] for n in
-              ('ffn_up_skinny', 'ffn_tiled_up', 'ffn_down_skinny', 'ffn_tiled_down'))
+              ('ffn_skinny_fused', 'ffn_up_skinny', 'ffn_tiled_up', 'ffn_down_skinny',
+               'ffn_tiled_down'))
     fetch_ms, exposed_ms, overlap_ms = rt.fetch_timing()
     ops.timing_enable(False)
     copies = rt.h2d.copies - prefill_copies

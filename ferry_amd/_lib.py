@@ -29,6 +29,7 @@ SIGNATURES = [
     ('ferry_expert_ffn', ctypes.c_int,
      [_c_p, _i64, _i64, _i64, _c_p, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _i32, _c_p, _i64,
       _i64, _i64, _c_p, _c_p, _i32, _i32, _c_p]),
+    ('ferry_expert_ffn_sync_timeouts', ctypes.c_int, [_c_p]),
     ('ferry_combine', ctypes.c_int, [_c_p, _c_p, _i64, _i64, _i64, _c_p, _c_p]),
     ('ferry_pack_dispatch', ctypes.c_int,
      [_c_p, _i64, _i64, _c_p, _c_p, _i64, _c_p, _c_p, _i64, _i64, _i64, _c_p, _c_p]),

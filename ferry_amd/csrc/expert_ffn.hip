@@ -29,6 +29,8 @@
 
 #include "common.h"
 
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 
 namespace ferry {
@@ -72,6 +74,30 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 
 __device__ __forceinline__ bf16x8 load8(const bf16_t* p) {
   return *reinterpret_cast<const bf16x8*>(p);
+}
+
+// Activation rows of the one-launch decode kernel (ffn_skinny_fused) are written by one
+// workgroup and read by others, on any XCD, inside one launch.  With COH their stores and loads
+// are agent-coherent (relaxed agent-scope atomic accesses: sc1), so that no L2 write-back or
+// invalidate is needed between the two phases; the other kernels use plain accesses.
+template <bool COH>
+__device__ __forceinline__ void store_act(bf16_t* p, bf16_t v) {
+  if constexpr (COH)
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    *p = v;
+}
+template <bool COH>
+__device__ __forceinline__ bf16x8 load_act8(const bf16_t* p) {
+  if constexpr (COH) {
+    const uint64_t* q = reinterpret_cast<const uint64_t*>(p);
+    const uint64_t lo = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t hi = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    struct { uint64_t a, b; } both = {lo, hi};
+    return __builtin_bit_cast(bf16x8, both);
+  } else {
+    return load8(p);
+  }
 }
 
 // =============================================================================================
@@ -144,7 +170,7 @@ __device__ __forceinline__ void wg_barrier() {
 // at a higher rate (every 128-byte line fetched by one instruction, not two), and reorder the
 // data into fragments through LDS.
 
-template <int U, int MT, int NB>
+template <int U, int MT, int NB, bool COH = false>
 __device__ __forceinline__ void skinny_batch(const bf16_t* const (&pb)[NB], const bf16_t* const (&px)[MT],
                                              const bool (&okx)[MT], int k0,
                                              floatx4 (&acc)[MT][NB]) {
@@ -157,7 +183,7 @@ __device__ __forceinline__ void skinny_batch(const bf16_t* const (&pb)[NB], cons
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int s = 0; s < U; ++s) ax[mt][s] = okx[mt] ? load8(px[mt] + k0 + s * 32) : zero8;
+    for (int s = 0; s < U; ++s) ax[mt][s] = okx[mt] ? load_act8<COH>(px[mt] + k0 + s * 32) : zero8;
 #pragma unroll
   for (int s = 0; s < U; ++s)
 #pragma unroll
@@ -167,13 +193,13 @@ __device__ __forceinline__ void skinny_batch(const bf16_t* const (&pb)[NB], cons
         acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax[mt][s], b[j][s], acc[mt][j], 0, 0, 0);
 }
 // K steps [k0, kend) (multiples of 32) in batches of U, then of 2 and 1 for the remainder
-template <int U, int MT, int NB>
+template <int U, int MT, int NB, bool COH = false>
 __device__ __forceinline__ void skinny_k_range(const bf16_t* const (&pb)[NB], const bf16_t* const (&px)[MT],
                                                const bool (&okx)[MT], int k0, int kend,
                                                floatx4 (&acc)[MT][NB]) {
-  for (; k0 + U * 32 <= kend; k0 += U * 32) skinny_batch<U>(pb, px, okx, k0, acc);
-  for (; k0 + 2 * 32 <= kend; k0 += 2 * 32) skinny_batch<2>(pb, px, okx, k0, acc);
-  if (k0 < kend) skinny_batch<1>(pb, px, okx, k0, acc);
+  for (; k0 + U * 32 <= kend; k0 += U * 32) skinny_batch<U, MT, NB, COH>(pb, px, okx, k0, acc);
+  for (; k0 + 2 * 32 <= kend; k0 += 2 * 32) skinny_batch<2, MT, NB, COH>(pb, px, okx, k0, acc);
+  if (k0 < kend) skinny_batch<1, MT, NB, COH>(pb, px, okx, k0, acc);
 }
 // the fixed-order K reduction over the KS wavefronts of a column group nt, through the LDS
 // buffer red (KS*NT*MT*NB*64 entries); the wavefront with ks = 0 returns true with the sums
@@ -204,7 +230,7 @@ __device__ __forceinline__ bool skinny_reduce(floatx4 (&acc)[MT][NB], int ks, in
 // Phase 1, skinny: one workgroup = (expert, 16*NT*NC intermediate columns): NT column groups of
 // NC tiles, each group's K split over KS = 4/NT wavefronts.  MT = number of 16-row M tiles
 // (rows of the expert, <= 16*MT).  B operands j < NC: gate tiles, j >= NC: up tiles.
-template <int NT, int NC, int MT>
+template <int NT, int NC, int MT, bool COH = false>
 __device__ __forceinline__ void up_skinny(const FfnArgs& a, int li, int64_t start, int n, int bx,
                                           floatx4* red) {
   constexpr int KS = 4 / NT;
@@ -250,7 +276,7 @@ __device__ __forceinline__ void up_skinny(const FfnArgs& a, int li, int64_t star
         const int r = mt * 16 + (lane >> 4) * 4 + q;
         if (r < n) {
           const float g = bf16r(acc[mt][c][q]), u = bf16r(acc[mt][NC + c][q]);
-          a.act[(start + r) * a.I + col] = f32_to_bf16(silu_mul(g, u));
+          store_act<COH>(&a.act[(start + r) * a.I + col], f32_to_bf16(silu_mul(g, u)));
         }
       }
     }
@@ -263,7 +289,7 @@ __device__ __forceinline__ void up_skinny(const FfnArgs& a, int li, int64_t star
 // wavefront turns them into B fragments through its own 4 KiB LDS tile, one K chunk of 64 at a
 // time: 32 rows (gate 0-15, up 16-31) x 128 B, chunk c of row r at slot c ^ ((r >> 1) & 7), which
 // keeps the fragment reads free of bank conflicts.  NCH chunks of loads are in flight.
-template <int NCH>
+template <int NCH, bool COH = false>
 __device__ __forceinline__ void up_skinny_t(const FfnArgs& a, int li, int64_t start, int n, int bx,
                                             floatx4* red, char* tile) {
   const int H = (int)a.H;
@@ -329,13 +355,13 @@ __device__ __forceinline__ void up_skinny_t(const FfnArgs& a, int li, int64_t st
     const int r = (lane >> 4) * 4 + q;
     if (r < n) {
       const float g = bf16r(accm[0][0][q]), u = bf16r(accm[0][1][q]);
-      a.act[(start + r) * a.I + col] = f32_to_bf16(silu_mul(g, u));
+      store_act<COH>(&a.act[(start + r) * a.I + col], f32_to_bf16(silu_mul(g, u)));
     }
   }
 }
 
 // Phase 2, skinny: one workgroup = (expert, 16*NT*NC hidden rows), laid out as phase 1.
-template <int NT, int NC, int MT>
+template <int NT, int NC, int MT, bool COH = false>
 __device__ __forceinline__ void down_skinny(const FfnArgs& a, int li, int64_t start, int n, int bx,
                                             floatx4* red) {
   constexpr int KS = 4 / NT;
@@ -363,7 +389,8 @@ __device__ __forceinline__ void down_skinny(const FfnArgs& a, int li, int64_t st
 #pragma unroll
     for (int c = 0; c < NC; ++c) acc[mt][c] = floatx4{0, 0, 0, 0};
   const int steps = I / 32;
-  skinny_k_range<UNR>(pb, pa, oka, ks * steps / KS * 32, (ks + 1) * steps / KS * 32, acc);
+  skinny_k_range<UNR, MT, NC, COH>(pb, pa, oka, ks * steps / KS * 32, (ks + 1) * steps / KS * 32,
+                                   acc);
   if (!skinny_reduce<KS, NT>(acc, ks, nt, lane, red)) return;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
@@ -385,7 +412,7 @@ __device__ __forceinline__ void down_skinny(const FfnArgs& a, int li, int64_t st
 // Phase 2, skinny, at most 16 rows (decode): one workgroup = (expert, 64 hidden rows), K split
 // over the four wavefronts; the weights go through the wavefront's LDS tile as in up_skinny_t,
 // 32 rows (two 16-row column tiles) at a time.
-template <int NCH>
+template <int NCH, bool COH = false>
 __device__ __forceinline__ void down_skinny_t(const FfnArgs& a, int li, int64_t start, int n, int bx,
                                               floatx4* red, char* tile) {
   const int I = (int)a.I;
@@ -425,7 +452,7 @@ __device__ __forceinline__ void down_skinny_t(const FfnArgs& a, int li, int64_t 
       for (int g = 0; g < 8; ++g) w[ch][g] = *reinterpret_cast<const u32x4*>(p0 + g * gstride + k0 + 64 * ch);
     bf16x8 xa[2 * N];
 #pragma unroll
-    for (int st = 0; st < 2 * N; ++st) xa[st] = oka ? load8(pa + k0 + 32 * st) : zero8;
+    for (int st = 0; st < 2 * N; ++st) xa[st] = oka ? load_act8<COH>(pa + k0 + 32 * st) : zero8;
 #pragma unroll
     for (int ch = 0; ch < N; ++ch) {
 #pragma unroll
@@ -502,6 +529,17 @@ __device__ __forceinline__ void gload16o(bf16x8& v, const void* sbase, uint32_t 
                : "v"(voff), "s"(sbase), "n"(OFF)
                : "memory");
 }
+// gload16o for activation rows: agent-coherent (sc1) under COH, see store_act
+template <int OFF, bool COH>
+__device__ __forceinline__ void gload16o_act(bf16x8& v, const void* sbase, uint32_t voff) {
+  if constexpr (COH)
+    asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3 sc1"
+                 : "=v"(v)
+                 : "v"(voff), "s"(sbase), "n"(OFF)
+                 : "memory");
+  else
+    gload16o<OFF>(v, sbase, voff);
+}
 
 // Phase 1, skinny, at most 16 rows, H = 512 * NB: up_skinny_t's tile scheme with the K range of
 // each wavefront walked in NB batches of two 64-element chunks, software-pipelined -- the loads
@@ -511,7 +549,7 @@ __device__ __forceinline__ void gload16o(bf16x8& v, const void* sbase, uint32_t 
 // order (8 weight loads, then 4 token-row loads; padding rows load token row 0 and are zeroed
 // after the wait), so each wait has a fixed count of younger loads.  The batch loop is fully
 // unrolled: no loop-carried register holds a load in flight.
-template <int NB>
+template <int NB, bool COH = false>
 __device__ __forceinline__ void up_skinny_p(const FfnArgs& a, int li, int64_t start, int n, int bx,
                                             floatx4* red, char* tile) {
   static_assert(NB >= 2 && NB % 2 == 0, "an even number of batches");
@@ -621,7 +659,7 @@ __device__ __forceinline__ void up_skinny_p(const FfnArgs& a, int li, int64_t st
     const int r = (lane >> 4) * 4 + q;
     if (r < n) {
       const float g = bf16r(accm[0][0][q]), u = bf16r(accm[0][1][q]);
-      a.act[(start + r) * a.I + col] = f32_to_bf16(silu_mul(g, u));
+      store_act<COH>(&a.act[(start + r) * a.I + col], f32_to_bf16(silu_mul(g, u)));
     }
   }
 }
@@ -631,7 +669,7 @@ __device__ __forceinline__ void up_skinny_p(const FfnArgs& a, int li, int64_t st
 // sets -- chunk c + 1 is loaded while chunk c goes through the tile and the matrix cores.  Ten
 // asm loads per chunk in a fixed order (eight 8-row weight groups, then two activation loads;
 // padding rows load the expert's first row and are zeroed after the wait).  Fully unrolled.
-template <int NC>
+template <int NC, bool COH = false>
 __device__ __forceinline__ void down_skinny_p(const FfnArgs& a, int li, int64_t start, int n, int bx,
                                               floatx4* red, char* tile) {
   constexpr int I = 256 * NC;
@@ -668,8 +706,8 @@ __device__ __forceinline__ void down_skinny_p(const FfnArgs& a, int li, int64_t 
     constexpr uint32_t kbyte = decltype(c)::value * 128;
 #pragma unroll
     for (int g = 0; g < 8; ++g) gload16o<0>(w[g], wd, wrow + kbyte + g * 16 * I);
-    gload16o<0>(xa[0], as, arow + kbyte);
-    gload16o<64>(xa[1], as, arow + kbyte);
+    gload16o_act<0, COH>(xa[0], as, arow + kbyte);
+    gload16o_act<64, COH>(xa[1], as, arow + kbyte);
   };
   auto mma = [&](bf16x8 (&w)[8], bf16x8 (&xa)[2]) {
 #pragma unroll
@@ -957,6 +995,114 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void f
     else
       ffn_mid_body_t<1, 2>(a, li, start, n, blockIdx.x, sm);
   }
+}
+
+// =============================================================================================
+// Decode: both phases of every expert (at most 16 rows each) in one launch
+// =============================================================================================
+
+// The workgroups of ffn_up_skinny<1> (I/16 per expert) come first in the grid, those of
+// ffn_down_skinny<1> (H/64 per expert) after them.  A down workgroup needs every intermediate
+// column of its expert's activation rows, so it waits for all of that expert's up workgroups:
+// each up workgroup, once its rows are stored, sets its arrival flag; a down workgroup's first
+// wavefront waits for all flags of its expert.  The L2s of the XCDs are not coherent with
+// each other, and a release / acquire pair would write back and invalidate a whole L2 for every
+// workgroup (measured: 550 us per launch instead of 30): instead the activation rows themselves
+// are stored and loaded agent-coherently (sc1, see store_act), each wavefront waits for its
+// stores to complete before the workgroup arrives, and the flags are relaxed agent-scope
+// atomic words.  Workgroups are dispatched in index order, so every producer a down
+// workgroup waits for has been dispatched before it: the wait ends.  It is still bounded
+// (kSyncSpinLimit sleeps, about a second); a down workgroup that runs out counts a timeout and
+// skips its expert rather than read unfinished rows.
+//
+// Arrival flags: one 32-bit word per up workgroup, holding the epoch (a number unique to the
+// call) once that workgroup's rows are stored.  A down workgroup's first wavefront checks all
+// flags of its expert at once (one lane per flag) until every one holds the call's epoch.  Flags
+// from earlier calls hold older epochs, so nothing is ever cleared, and no word is written by
+// two workgroups (no read-modify-write contention).  The flags live in a static per-device ring
+// of kSyncSets sets (set = epoch % kSyncSets); calls that run at the same time on one GPU use
+// different sets unless kSyncSets of them overlap.
+constexpr int kSyncSets = 8;
+constexpr int kMaxUpWgs = 128;   // up workgroups per expert (I / 16): I <= 2048
+constexpr int kSyncSpinLimit = 1 << 21;
+static __device__ __align__(256) uint32_t g_sync[kSyncSets][kListMax][kMaxUpWgs];
+static __device__ int32_t g_sync_timeouts;
+
+struct FusedSync {
+  uint32_t* flags;   // the call's flag set (device address of g_sync[epoch % kSyncSets])
+  int32_t* timeouts;
+  uint32_t epoch;
+  int32_t up_wgs;    // up workgroups per expert (I / 16)
+  int32_t down_wgs;  // down workgroups per expert (H / 64)
+};
+
+__device__ __forceinline__ void sync_arrive(const FusedSync& fs, int li, int bx) {
+  __hip_atomic_store(fs.flags + li * kMaxUpWgs + bx, fs.epoch, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// wavefront 0 of a down workgroup: true once every up workgroup of list entry li has arrived,
+// false on timeout
+__device__ __forceinline__ bool sync_wait(const FusedSync& fs, int li) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t* f = fs.flags + li * kMaxUpWgs;
+  int spins = 0;
+  for (;;) {
+    bool mine = true;
+    for (int j = lane; j < fs.up_wgs; j += 64)
+      mine &= __hip_atomic_load(f + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == fs.epoch;
+    if (__all(mine)) return true;
+    if (++spins > kSyncSpinLimit) {
+      if (lane == 0) atomicAdd(fs.timeouts, 1);
+      return false;
+    }
+    __builtin_amdgcn_s_sleep(8);
+  }
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void ffn_skinny_fused(
+    FfnArgs a, FusedSync fs) {
+  // phase 2's K-reduction buffer (16 KiB; phase 1 uses 8) and four 4 KiB weight tiles
+  __shared__ __attribute__((aligned(1024))) char sm[16384 + 4 * 4096];
+  __shared__ int ok_s;
+  const int nup = fs.up_wgs * a.list.n;
+  const bool up = (int)blockIdx.x < nup;
+  const int b = up ? (int)blockIdx.x : (int)blockIdx.x - nup;
+  const int per = up ? fs.up_wgs : fs.down_wgs;
+  const int li = b / per, bx = b % per;
+  const int e = a.list.expert[li];
+  const int64_t start = a.starts[e];
+  const int n = (int)(a.starts[e + 1] - start);
+  if (n == 0 || n > 16) return;   // up and down workgroups of such an expert both skip it
+  if (up) {
+    if (a.H == 2048)
+      up_skinny_p<4, true>(a, li, start, n, bx, reinterpret_cast<floatx4*>(sm),
+                     sm + 16384 + (threadIdx.x >> 6) * 4096);
+    else if (a.H % 256 == 0)
+      up_skinny_t<4, true>(a, li, start, n, bx, reinterpret_cast<floatx4*>(sm),
+                     sm + 16384 + (threadIdx.x >> 6) * 4096);
+    else
+      up_skinny<1, 1, 1, true>(a, li, start, n, bx, reinterpret_cast<floatx4*>(sm));
+    // the agent-coherent activation stores of every wavefront complete before the arrival
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) sync_arrive(fs, li, bx);
+    return;
+  }
+  if (threadIdx.x < 64) {
+    const bool ok = sync_wait(fs, li);
+    if (threadIdx.x == 0) ok_s = ok ? 1 : 0;
+  }
+  __syncthreads();
+  if (!ok_s) return;
+  if (a.I == 768)
+    down_skinny_p<3, true>(a, li, start, n, bx, reinterpret_cast<floatx4*>(sm),
+                     sm + 16384 + (threadIdx.x >> 6) * 4096);
+  else if (a.I % 256 == 0)
+    down_skinny_t<2, true>(a, li, start, n, bx, reinterpret_cast<floatx4*>(sm),
+                     sm + 16384 + (threadIdx.x >> 6) * 4096);
+  else
+    down_skinny<1, 4, 1, true>(a, li, start, n, bx, reinterpret_cast<floatx4*>(sm));
 }
 
 // =============================================================================================
@@ -1295,6 +1441,31 @@ __global__ __launch_bounds__(kTiledThreads, 1) void ffn_tiled(FfnArgs a) {
 
 int g_num_cus = 0;
 
+// Device addresses of g_sync / g_sync_timeouts on each device (resolved on first use there).
+constexpr int kMaxDevices = 64;
+std::mutex g_sync_mu;
+uint32_t* g_sync_dev[kMaxDevices];
+int32_t* g_timeouts_dev[kMaxDevices];
+std::atomic<uint32_t> g_epoch{0};
+
+int sync_addresses(uint32_t** sync, int32_t** timeouts) {
+  int dev = -1;
+  FERRY_HIP(hipGetDevice(&dev));
+  FERRY_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_sync_mu);
+  if (g_sync_dev[dev] == nullptr) {
+    void* ps = nullptr;
+    void* pt = nullptr;
+    FERRY_HIP(hipGetSymbolAddress(&ps, HIP_SYMBOL(g_sync)));
+    FERRY_HIP(hipGetSymbolAddress(&pt, HIP_SYMBOL(g_sync_timeouts)));
+    g_sync_dev[dev] = (uint32_t*)ps;
+    g_timeouts_dev[dev] = (int32_t*)pt;
+  }
+  *sync = g_sync_dev[dev];
+  *timeouts = g_timeouts_dev[dev];
+  return 0;
+}
+
 }  // namespace
 }  // namespace ferry
 
@@ -1378,6 +1549,24 @@ extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t h
     // M tiles over experts with > 64 rows: sum ceil(n/BM) <= pairs/BM + (experts with > 64 rows)
     const int64_t tile_bound = pairs / BM + pairs / (kSkinnyMax + 1) + 1;  // and those are <= pairs/65
     const int64_t grid_cap = (int64_t)g_num_cus;  // one 256x256 workgroup per CU
+    if (phases == 3 && any_small && !any_big && maxn <= 16 && inter / 16 <= kMaxUpWgs) {
+      // decode: both phases in one launch, each expert's down projection as soon as its up
+      // projection is stored
+      FusedSync fs;
+      uint32_t* sync = nullptr;
+      const int rc = sync_addresses(&sync, &fs.timeouts);
+      if (rc != 0) return rc;
+      uint32_t epoch = ++g_epoch;
+      if (epoch == 0) epoch = ++g_epoch;   // epoch 0 would match never-used words
+      fs.epoch = epoch;
+      fs.flags = sync + (int64_t)(epoch % kSyncSets) * kListMax * kMaxUpWgs;
+      fs.up_wgs = (int32_t)(inter / 16);
+      fs.down_wgs = (int32_t)(hidden / 64);
+      launch("ffn_skinny_fused", ffn_skinny_fused,
+             dim3((unsigned)((fs.up_wgs + fs.down_wgs) * cnt)), dim3(256), 0, s, args, fs);
+      FERRY_LAUNCHED("ffn_skinny_fused");
+      continue;
+    }
     if (phases & 1) {
       // 16 intermediate columns per workgroup, K split over the four wavefronts
       if (any_small) {
@@ -1414,5 +1603,20 @@ extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t h
       }
     }
   }
+  return 0;
+}
+
+// Number of fused decode launches whose down phase gave up waiting for its up phase (each such
+// workgroup left its rows unwritten); 0 unless workgroups were not dispatched in index order.
+extern "C" int ferry_expert_ffn_sync_timeouts(int64_t* count) {
+  clear_error();
+  FERRY_CHECK_ARG(count, "null pointer argument");
+  uint32_t* sync = nullptr;
+  int32_t* timeouts = nullptr;
+  const int rc = sync_addresses(&sync, &timeouts);
+  if (rc != 0) return rc;
+  int32_t v = 0;
+  FERRY_HIP(hipMemcpy(&v, timeouts, sizeof(v), hipMemcpyDeviceToHost));
+  *count = v;
   return 0;
 }

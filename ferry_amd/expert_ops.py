@@ -196,6 +196,14 @@ def expert_ffn(cache, x, w_sorted, starts, rows, cols, expert_list, slot_of, hid
     return out
 
 
+def ffn_sync_timeouts():
+    """Waits of the one-launch decode FFN that gave up on the current device (expected 0)."""
+    import ctypes
+    n = ctypes.c_int64()
+    check(lib().ferry_expert_ffn_sync_timeouts(ctypes.byref(n)), 'ffn_sync_timeouts')
+    return int(n.value)
+
+
 def combine(part, tokens, topk, hidden, pair_pos=None, out=None, addend=None):
     """out[t] = bf16(sum_j fp32(part[src(t, j)])), j ascending (expert_ops.cpp:75-92).
 

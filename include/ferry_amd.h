@@ -115,6 +115,15 @@ int ferry_layout_noalloc(const int64_t* selected, const void* weights_bf16, int6
  * than 4 GiB.
  */
 enum { FERRY_MAX_EXPERTS = 512 };
+/* A call with phases = 3 whose experts all have at most 16 rows (decode, intermediate <= 2048)
+ * runs both phases in one launch: an expert's down projection starts once its up projection is
+ * stored, through arrival flags in a static device ring of 8 sets, one per call in turn.  Calls
+ * on one GPU whose kernels run at the same time must number fewer than 8 (calls on one stream
+ * never overlap); more would share a set and could leave outputs unwritten.
+ * ferry_expert_ffn_sync_timeouts (a diagnostic with no counterpart in the reference) returns
+ * how many waits of such launches on the current device gave up: each wait is bounded (about a
+ * second), and the count stays 0 when workgroups are dispatched in index order, as the
+ * hardware does.  A wait that gave up leaves its rows of `out` unwritten. */
 int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t hidden, int64_t inter,
                      const void* x, int64_t rows_in, int64_t topk, const void* w_sorted,
                      const int64_t* starts, const int64_t* rows, const int64_t* cols,
@@ -122,6 +131,7 @@ int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t hidden, int6
                      int64_t experts, int64_t max_rows_per_expert,
                      int64_t min_rows_per_expert, void* act, void* out, int32_t out_mode,
                      int32_t phases, void* stream);
+int ferry_expert_ffn_sync_timeouts(int64_t* count);
 
 /*
  * Combine: out[t, :] = bf16( sum_{j<k} fp32(part[src(t, j), :]) ), j ascending (= ascending

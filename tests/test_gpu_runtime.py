@@ -102,3 +102,41 @@ def test_h2d_profiler_writes_loadable_topology(device, tmp_path):
     assert len(m['samples']['engine']) == 3
     topo = Topology(out, 1, 16)
     assert topo.lut[:, 0].tolist() == list(range(17))
+
+
+@pytest.mark.parametrize('family', ['qwen3', 'deepseek'])
+def test_fused_decode_ffn_matches_two_launch_path(device, family):
+    """The one-launch decode FFN (every expert at most 16 rows, both phases) against the
+    two-launch path (the phases called separately) on the Qwen3-30B-A3B and DeepSeek-V2-Lite
+    expert shapes, bit for bit, over calls that reuse the activation buffer; no wait of the
+    fused launch gave up."""
+    from ferry_amd import expert_ops as ops
+    from ferry_amd import workloads
+    from ferry_amd.model import DEEPSEEK_V2_LITE, QWEN3_30B_A3B
+    spec = QWEN3_30B_A3B if family == 'qwen3' else DEEPSEEK_V2_LITE
+    E, k, H, I = spec.experts, spec.topk, spec.hidden, spec.intermediate
+    cache = workloads.expert_rows(range(40), spec.expert_elements, seed=9, device=device)
+    slot_of = np.full(E, -1, np.int32)
+    experts = np.random.default_rng(0).choice(E, 40, replace=False)
+    slot_of[experts] = np.arange(40)
+    g = torch.Generator(device=device)
+    g.manual_seed(3)
+    act = torch.empty((64 * k, I), dtype=torch.bfloat16, device=device)
+    for T in (16, 1, 64 // 8, 16, 3):
+        sel = torch.stack([torch.from_numpy(np.random.default_rng(T + i).choice(experts, k, replace=False))
+                           for i in range(T)]).to(device)
+        w = torch.softmax(torch.randn((T, k), generator=g, device=device), -1).to(torch.bfloat16)
+        x = torch.randn((T, H), generator=g, device=device).to(torch.bfloat16)
+        lay = ops.layout(sel, w, E, check=True)
+        active = np.unique(sel.cpu().numpy())
+        counts = np.bincount(sel.cpu().numpy().reshape(-1), minlength=E)
+        assert counts.max() <= 16
+        fused = torch.empty((T * k, H), dtype=torch.bfloat16, device=device)
+        two = torch.empty_like(fused)
+        args = (cache, x, lay.w_sorted, lay.starts, lay.rows, lay.cols, active, slot_of, H, I)
+        ops.expert_ffn(*args, act[:T * k], fused, experts=E, counts=counts)
+        ops.expert_ffn(*args, act[:T * k], two, experts=E, counts=counts, phases=ops.PHASE_UP)
+        ops.expert_ffn(*args, act[:T * k], two, experts=E, counts=counts, phases=ops.PHASE_DOWN)
+        torch.cuda.synchronize()
+        assert torch.equal(fused, two), T
+    assert ops.ffn_sync_timeouts() == 0
