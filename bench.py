@@ -46,7 +46,6 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 PCIE_PEAK_GBS = 64.0
 
-TRAFFIC_PROFILE = ROOT / 'profiles' / 'ffn_up_skinny_decode_qwen3_t16_hbm_traffic.md'
 TILED_TRAFFIC_PROFILE = ROOT / 'profiles' / 'ffn_tiled_prefill_qwen3_t8192_hbm_traffic.md'
 FUSED_TRAFFIC_PROFILE = ROOT / 'profiles' / 'ffn_skinny_fused_decode_qwen3_t16_hbm_traffic.md'
 
@@ -178,8 +177,7 @@ def decode_block(dec, args):
         kern, name = fused, 'ffn_skinny_fused (decode gate/up + SwiGLU + down, one launch)'
         kbytes = ks['up'] + ks['down']
     else:
-        ratio = profile_value(TRAFFIC_PROFILE, 'traffic_over_algorithmic')
-        source = TRAFFIC_PROFILE
+        ratio, source = None, None   # no committed traffic profile for the split launches
         kern, name, kbytes = up, 'ffn_up_skinny (decode gate/up + SwiGLU)', ks['up']
     achieved = kbytes / (kern['total_ms'] * 1e-3) / 1e9
     bytes_per_launch = kbytes / max(1, kern['launches'])
@@ -271,6 +269,11 @@ def run_prefill(args, device, config=3):
     tu = kern['ffn_tiled_up']
     # the shared experts' launches add to the tiled kernel's launch count (one per layer call)
     tiled_up_launch_flops = tiled_up_flops / max(1, tu['launches'] / args.prefill_reps)
+    # algorithmic HBM bytes of one routed tiled launch: each tiled expert's weights once, each of
+    # its rows read once and its output rows written once
+    n_tiled, routed_rows = int((counts > 64).sum()), int(counts[counts > 64].sum())
+    tiled_up_bytes = 2 * (n_tiled * 2 * I * H + routed_rows * (H + I))
+    tiled_down_bytes = 2 * (n_tiled * I * H + routed_rows * (I + H))
     return dict(workload=name, tokens=T, tokens_per_s=T / ((t1 - t0) / args.prefill_reps),
                 layer_ms=(t1 - t0) / args.prefill_reps * 1e3,
                 gemm_ms=gemm_ms, up_ms=up_ms, down_ms=down_ms, gemm_tflop=flops / 1e12,
@@ -278,6 +281,8 @@ def run_prefill(args, device, config=3):
                 mfma_util=flops / (gemm_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
                 active_experts=int((counts > 0).sum()), max_rows=int(counts.max()),
                 median_rows=float(np.median(counts[counts > 0])), tiled_rows=tiled_rows,
+                tiled_experts=n_tiled, routed_tiled_up_bytes=tiled_up_bytes,
+                routed_tiled_down_bytes=tiled_down_bytes,
                 tiled_up_launch_tflop=tiled_up_launch_flops / 1e12,
                 tiled_up_avg_us=tu['avg_us'],
                 kernel_ms={n: per(n) for n in kern},
@@ -290,7 +295,9 @@ def prefill_roofline(pre):
     ratio = profile_value(TILED_TRAFFIC_PROFILE, 'up_traffic_over_algorithmic')
     return dict(kernel='ffn_tiled_up (prefill gate/up GEMM + SwiGLU, experts > 64 rows)',
                 bound='mfma', achieved=tflops, peak=BF16_PEAK_TFLOPS, unit='TFLOP/s',
-                frac=tflops / BF16_PEAK_TFLOPS, traffic_over_algorithmic=ratio,
+                frac=tflops / BF16_PEAK_TFLOPS,
+                traffic=pre['routed_tiled_up_bytes'] * ratio if ratio else None,
+                algorithmic_bytes=pre['routed_tiled_up_bytes'], traffic_over_algorithmic=ratio,
                 traffic_source=TILED_TRAFFIC_PROFILE.name if ratio else None,
                 flop_per_launch=pre['tiled_up_launch_tflop'] * 1e12,
                 avg_launch_us=pre['tiled_up_avg_us'],
