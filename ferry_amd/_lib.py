@@ -52,6 +52,9 @@ SIGNATURES = [
     ('ferry_h2d_synchronize', ctypes.c_int, [_c_p]),
     ('ferry_h2d_copies', _i64, [_c_p]),
     ('ferry_h2d_stream', _c_p, [_c_p]),
+    ('ferry_h2d_set_engine', ctypes.c_int, [_c_p, _i32]),
+    ('ferry_h2d_engine', _i32, [_c_p]),
+    ('ferry_h2d_set_kernel_stream', ctypes.c_int, [_c_p, _c_p]),
     ('ferry_timing_enable', ctypes.c_int, [_i32]),
     ('ferry_timing_mark', _i64, []),
     ('ferry_timing_range', ctypes.c_int, [_i64, _i64, _c_p]),

@@ -8,14 +8,20 @@
 // makes a compute stream wait for the copies on the GPU, so that experts that are already
 // resident can run while missing ones are still in flight.
 //
-// Each row is copied as kLanes equal parts on kLanes streams: one DMA stream does not fill the
-// host link (measured on MI355X: ~47 GB/s with one stream, ~56.5 GB/s with two), and splitting
-// every row keeps the lanes balanced whatever the number of misses.  A slot is ready when the
-// copy-done events of all its lanes have fired.  A fetch call forks the lanes from the first
-// stream and joins them back into it, so that the first stream (ferry_h2d_stream) brackets
-// every copy of the call.  Per copy only the hipMemcpyAsync itself is queued: a stream wait or
-// an event between two copies on a DMA stream costs tens of microseconds of idle link.  The
-// engine owns its streams (default priority) and events; it allocates no device memory.
+// Two ways to copy, chosen per engine (ferry_h2d_set_engine):
+//  * FERRY_H2D_KERNEL (the default when the pool has a device mapping and rows are 16-byte
+//    multiples): one launch of h2d_copy_kernel per fetch call on the first stream reads the
+//    pool over PCIe and writes the slots.  One launch has no idle link time between rows.
+//  * FERRY_H2D_DMA: each row is copied as kLanes equal parts by hipMemcpyAsync on kLanes
+//    streams: one DMA stream does not fill the host link (measured on MI355X: ~47 GB/s with one
+//    stream, ~56.5 GB/s with two), and splitting every row keeps the lanes balanced whatever
+//    the number of misses.  A fetch call forks the lanes from the first stream and joins them
+//    back into it.  Per copy only the hipMemcpyAsync itself is queued: a stream wait or an
+//    event between two copies on a DMA stream costs tens of microseconds of idle link.
+// A slot is ready when the copy-done events of all its lanes have fired (in kernel mode every
+// lane's event is the first stream's).  The first stream (ferry_h2d_stream) brackets every copy
+// of a call.  The engine owns its streams (default priority) and events; it allocates no device
+// memory.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -27,6 +33,8 @@
 namespace ferry {
 void set_error(const char* fmt, ...);
 void clear_error();
+hipError_t h2d_copy_launch(const void* pool, void* cache, int64_t row_bytes, const int64_t* keys,
+                           const int64_t* slots, int64_t n, hipStream_t stream);
 }  // namespace ferry
 
 namespace {
@@ -45,6 +53,14 @@ constexpr int kLanes = 2;
 struct ferry_h2d {
   char* cache = nullptr;
   const char* pool = nullptr;
+  const char* pool_dev = nullptr;     // the pool's device mapping (null: DMA copies only)
+  int32_t kind = FERRY_H2D_DMA;
+  hipStream_t kernel_stream = nullptr;  // stream of kernel-mode copies (initially stream[0])
+  std::shared_ptr<Event> last_kernel_copy;  // done event of the latest kernel-mode fetch
+  bool dma_since_kernel = false;      // DMA fetches queued since the latest kernel-mode fetch
+  std::vector<int64_t> batch_of;      // per slot: last kernel-mode launch batch that wrote it
+  int64_t batch = 0;
+  hipStream_t last_kernel_stream = nullptr;  // stream of the latest kernel-mode fetch
   int64_t cache_rows = 0, pool_rows = 0, row_bytes = 0;
   int64_t part[kLanes + 1] = {};      // byte boundaries of the row parts
   int32_t device = 0;
@@ -56,6 +72,13 @@ struct ferry_h2d {
   int64_t seq = 0;
   int64_t copies = 0;
 };
+
+// the copy kernel addresses 16-byte units through 32-bit row indices
+static bool kernel_copy_ok(const ferry_h2d* h) {
+  return h->pool_dev && h->row_bytes % 16 == 0 && (uintptr_t)h->pool_dev % 16 == 0 &&
+         (uintptr_t)h->cache % 16 == 0 && h->pool_rows < (int64_t(1) << 31) &&
+         h->cache_rows < (int64_t(1) << 31);
+}
 
 #define H2D_HIP(expr)                                                                     \
   do {                                                                                    \
@@ -88,6 +111,8 @@ extern "C" int ferry_h2d_create(void* cache, int64_t cache_rows, const void* poo
   h->pool_rows = pool_rows;
   h->row_bytes = row_bytes;
   h->device = device;
+  h->pool_dev = (const char*)attr.devicePointer;
+  if (kernel_copy_ok(h.get())) h->kind = FERRY_H2D_KERNEL;
   for (int l = 0; l <= kLanes; ++l) h->part[l] = row_bytes * l / kLanes / 256 * 256;
   h->part[kLanes] = row_bytes;
   for (int l = 0; l < kLanes; ++l) {
@@ -95,7 +120,10 @@ extern "C" int ferry_h2d_create(void* cache, int64_t cache_rows, const void* poo
     h->copy_done[l].assign((size_t)cache_rows, nullptr);
   }
   H2D_HIP(hipEventCreateWithFlags(&h->join, hipEventDisableTiming));
+  h->kernel_stream = h->stream[0];
+  h->last_kernel_stream = h->stream[0];
   h->copy_seq.assign((size_t)cache_rows, -1);
+  h->batch_of.assign((size_t)cache_rows, 0);
   h->used.assign((size_t)cache_rows, nullptr);
   *out = h.release();
   return 0;
@@ -142,6 +170,50 @@ extern "C" int ferry_h2d_fetch(ferry_h2d* h, const int64_t* slots, const int64_t
       return 3;
     }
   }
+  if (h->kind == FERRY_H2D_KERNEL) {
+    hipStream_t s = h->kernel_stream;
+    for (hipEvent_t e : pending) H2D_HIP(hipStreamWaitEvent(s, e, 0));
+    // copies queued earlier on the DMA lanes, into any slot, end before this launch starts
+    if (s != h->stream[0] && h->dma_since_kernel) {
+      H2D_HIP(hipEventRecord(h->join, h->stream[0]));
+      H2D_HIP(hipStreamWaitEvent(s, h->join, 0));
+    }
+    // and so do kernel-mode copies queued on another stream
+    if (h->last_kernel_copy && s != h->last_kernel_stream)
+      H2D_HIP(hipStreamWaitEvent(s, h->last_kernel_copy->e, 0));
+    h->dma_since_kernel = false;
+    h->last_kernel_stream = s;
+    // rows of one launch run concurrently: a slot named twice in the call starts a new
+    // launch, so that the later row wins, as with copies in stream order
+    int64_t b0 = 0;
+    ++h->batch;
+    for (int64_t i = 0; i <= n; ++i) {
+      if (i < n && h->batch_of[(size_t)slots[i]] != h->batch) {
+        h->batch_of[(size_t)slots[i]] = h->batch;
+        continue;
+      }
+      H2D_HIP(ferry::h2d_copy_launch(h->pool_dev, h->cache, h->row_bytes, keys + b0, slots + b0,
+                                     i - b0, s));
+      if (i < n) {
+        ++h->batch;
+        h->batch_of[(size_t)slots[i]] = h->batch;
+      }
+      b0 = i;
+    }
+    auto ev = std::make_shared<Event>();
+    H2D_HIP(hipEventCreateWithFlags(&ev->e, hipEventDisableTiming));
+    H2D_HIP(hipEventRecord(ev->e, s));
+    for (int l = 0; l < kLanes; ++l)
+      for (int64_t i = 0; i < n; ++i) h->copy_done[l][(size_t)slots[i]] = ev;
+    h->last_kernel_copy = ev;
+    for (int64_t i = 0; i < n; ++i) h->copy_seq[(size_t)slots[i]] = h->seq++;
+    h->copies += n;
+    return 0;
+  }
+  // kernel-mode copies queued on another stream end before these copies start
+  if (h->last_kernel_copy && !h->dma_since_kernel)
+    H2D_HIP(hipStreamWaitEvent(h->stream[0], h->last_kernel_copy->e, 0));
+  h->dma_since_kernel = true;
   // fork: the other lanes start after what is already queued on lane 0, so that events the
   // caller records on lane 0 around the call bracket every copy of it
   for (int l = 1; l < kLanes; ++l) {
@@ -233,9 +305,40 @@ extern "C" int ferry_h2d_mark_used(ferry_h2d* h, const int64_t* slots, int64_t n
 extern "C" int ferry_h2d_synchronize(ferry_h2d* h) {
   ferry::clear_error();
   for (int l = 0; l < kLanes; ++l) H2D_HIP(hipStreamSynchronize(h->stream[l]));
+  if (h->last_kernel_copy) H2D_HIP(hipEventSynchronize(h->last_kernel_copy->e));
   return 0;
 }
 
 extern "C" int64_t ferry_h2d_copies(const ferry_h2d* h) { return h ? h->copies : 0; }
+
+extern "C" int ferry_h2d_set_engine(ferry_h2d* h, int32_t kind) {
+  ferry::clear_error();
+  if (!h || (kind != FERRY_H2D_DMA && kind != FERRY_H2D_KERNEL)) {
+    ferry::set_error("h2d_set_engine: bad arguments");
+    return 2;
+  }
+  if (kind == FERRY_H2D_KERNEL && !kernel_copy_ok(h)) {
+    ferry::set_error("h2d_set_engine: the copy kernel needs a device-mapped pool and 16-byte "
+                     "aligned rows");
+    return 2;
+  }
+  // no wait: every fetch is ordered after the copies of the other kind already queued (the
+  // DMA lanes fork from stream[0] after the latest kernel-mode copy; kernel-mode copies wait
+  // for stream[0], into which the lanes join)
+  h->kind = kind;
+  return 0;
+}
+
+extern "C" int ferry_h2d_set_kernel_stream(ferry_h2d* h, void* stream) {
+  ferry::clear_error();
+  if (!h) {
+    ferry::set_error("h2d_set_kernel_stream: null engine");
+    return 2;
+  }
+  h->kernel_stream = (hipStream_t)stream;
+  return 0;
+}
+
+extern "C" int32_t ferry_h2d_engine(const ferry_h2d* h) { return h ? h->kind : -1; }
 
 extern "C" void* ferry_h2d_stream(ferry_h2d* h) { return h ? (void*)h->stream[0] : nullptr; }

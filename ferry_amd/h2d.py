@@ -1,8 +1,10 @@
 """H2D expert fetch engine (the reference's ``H2DEngine``, ferry/csrc/expert_ops.cpp:94-142).
 
-Copies rows of a pinned host pool into GPU cache slots with ``hipMemcpyAsync`` on the
-engine's own stream.  A copy into a slot waits, on the GPU, for the last compute that read
-that slot (``mark_used``).  ``wait_host`` blocks the host like the reference;
+Copies rows of a pinned host pool into GPU cache slots on the engine's own stream: by default
+with one launch of a copy kernel per fetch call that reads the pool through its device mapping
+(``KERNEL``), or with one ``hipMemcpyAsync`` per row part on two DMA streams (``DMA``, the
+reference's way).  A copy into a slot waits, on the GPU, for the last compute that read that
+slot (``mark_used``).  ``wait_host`` blocks the host like the reference;
 ``wait_stream`` makes a compute stream wait on the GPU instead, which lets resident experts
 run while missing ones are still in flight.
 """
@@ -16,6 +18,9 @@ from ._lib import check, lib
 
 def _i64(values):
     return np.ascontiguousarray(np.asarray(values, dtype=np.int64).reshape(-1))
+
+
+DMA, KERNEL = 0, 1   # FERRY_H2D_DMA, FERRY_H2D_KERNEL
 
 
 class H2DEngine:
@@ -62,6 +67,32 @@ class H2DEngine:
 
     def synchronize(self):
         check(lib().ferry_h2d_synchronize(self._h), 'H2DEngine.synchronize')
+
+    @property
+    def engine(self):
+        """How rows are copied: ``KERNEL`` or ``DMA``."""
+        return int(lib().ferry_h2d_engine(self._h))
+
+    @engine.setter
+    def engine(self, kind):
+        check(lib().ferry_h2d_set_engine(self._h, int(kind)), 'H2DEngine.engine')
+
+    def set_kernel_stream(self, stream=None):
+        """Run kernel-mode copies on ``stream`` (a torch stream; None: the engine's own).  A
+        handle of 0 is HIP's null stream (torch's default stream), not the engine's."""
+        handle = stream.cuda_stream if stream is not None else lib().ferry_h2d_stream(self._h)
+        check(lib().ferry_h2d_set_kernel_stream(self._h, handle), 'H2DEngine.set_kernel_stream')
+
+    @property
+    def kernel_ok(self):
+        """Whether the copy kernel can serve this pool (device-mapped, 16-byte rows)."""
+        cur = self.engine
+        try:
+            self.engine = KERNEL
+        except RuntimeError:
+            return False
+        self.engine = cur
+        return True
 
     @property
     def copies(self):

@@ -6,10 +6,12 @@ median over repeats) and scripts/build_quota_lut.py:21-47 (domains + the Step-2 
 written as the JSON that ferry/quota.py:80-90 reads).  With one GPU there is one bandwidth
 domain (mask 1) and the quota of m missing experts is [m].
 
-Two rates are measured, both in GiB/s like the reference's file:
-  * ``engine``: the copies go through this package's H2D engine (``ferry_h2d_fetch``: each row
-    split over two DMA streams), which is what ``OffloadRuntime`` achieves; this is the
-    domain's ``gib_per_s``;
+Three rates are measured, all in GiB/s like the reference's file:
+  * ``engine``: one fetch call through this package's H2D engine in its default mode (the copy
+    kernel, one launch for all rows, when the pool is device-mapped), which is how
+    ``OffloadRuntime`` copies a decode step's misses; this is the domain's ``gib_per_s``;
+  * ``dma``: the engine's DMA mode (each row split over two DMA streams), how the runtime copies
+    a prefill call's misses;
   * ``single_stream``: one ``copy_`` per expert on one stream, the reference's pattern.
 
     python -m ferry_amd.h2dprof --output topology/mi355x_qwen3.json [--model-path DIR]
@@ -52,38 +54,44 @@ def _time_single_stream(stream, pool, cache, copies, spin_cycles):
     return start.elapsed_time(end) / 1e3
 
 
-def measure(expert_bytes, copies=64, repeats=5, slots=8, pool_rows=8, device=0,
+def measure(expert_bytes, copies=64, repeats=5, slots=None, pool_rows=8, device=0,
             spin_cycles=SPIN_CYCLES):
-    """Median GiB/s of ``copies`` back-to-back expert copies: dict(engine, single_stream,
+    """Median GiB/s of ``copies`` back-to-back expert copies: dict(engine, dma, single_stream,
     samples)."""
-    from .h2d import H2DEngine
+    from .h2d import DMA, H2DEngine
     from .hostmem import pinned_empty
     torch.cuda.set_device(device)
     elements = expert_bytes // 2
+    slots = copies if slots is None else slots   # distinct slots: one fetch call, one launch
     pool = pinned_empty((pool_rows, elements), torch.bfloat16)
     pool.copy_(torch.randn((pool_rows, elements)).to(torch.bfloat16))
     cache = torch.empty((slots, elements), dtype=torch.bfloat16, device=device)
     engine = H2DEngine(cache, pool)
+    dma = H2DEngine(cache, pool)
+    dma.engine = DMA
     stream = torch.cuda.Stream(device=device)
     idx = list(range(copies))
     slot_seq = [i % slots for i in idx]
     key_seq = [i % pool_rows for i in idx]
     gib = copies * expert_bytes / 2 ** 30
-    # warm up both paths
+    # warm up every path
     _time_engine(engine, slot_seq[:8], key_seq[:8], 0)
+    _time_engine(dma, slot_seq[:8], key_seq[:8], 0)
     _time_single_stream(stream, pool, cache, 8, 0)
-    samples = dict(engine=[], single_stream=[])
+    samples = dict(engine=[], dma=[], single_stream=[])
+    kinds = ['engine', 'dma', 'single_stream']
     for rep in range(repeats):
-        order = ('engine', 'single_stream') if rep % 2 == 0 else ('single_stream', 'engine')
-        for kind in order:
-            if kind == 'engine':
-                t = _time_engine(engine, slot_seq, key_seq, spin_cycles)
-            else:
+        for kind in kinds[rep % 3:] + kinds[:rep % 3]:
+            if kind == 'single_stream':
                 t = _time_single_stream(stream, pool, cache, copies, spin_cycles)
+            else:
+                t = _time_engine(engine if kind == 'engine' else dma, slot_seq, key_seq,
+                                 spin_cycles)
             samples[kind].append(gib / t)
-    engine.synchronize()
-    engine.close()
-    return dict(engine=statistics.median(samples['engine']),
+    for e in (engine, dma):
+        e.synchronize()
+        e.close()
+    return dict(engine=statistics.median(samples['engine']), dma=statistics.median(samples['dma']),
                 single_stream=statistics.median(samples['single_stream']), samples=samples)
 
 
@@ -95,6 +103,7 @@ def topology_document(measured, expert_bytes, experts, model_type=None, device=0
                               per_gpu_gib_per_s=[float(measured['engine'])])],
                 quota_lut=[[m] for m in range(experts + 1)],
                 measured=dict(engine_gib_per_s=measured['engine'],
+                              dma_gib_per_s=measured['dma'],
                               single_stream_gib_per_s=measured['single_stream'],
                               samples=measured['samples']))
 
@@ -121,8 +130,8 @@ def main(argv=None):
     out.parent.mkdir(parents=True, exist_ok=True)
     out.write_text(json.dumps(doc, indent=1) + '\n')
     print(f'H2D {a.expert_bytes} B copies x {a.copies}, median of {a.repeats}: engine '
-          f'{res["engine"]:.2f} GiB/s, single stream {res["single_stream"]:.2f} GiB/s '
-          f'({time.time() - t0:.1f} s); wrote {out}', flush=True)
+          f'{res["engine"]:.2f} GiB/s, DMA {res["dma"]:.2f} GiB/s, single stream '
+          f'{res["single_stream"]:.2f} GiB/s ({time.time() - t0:.1f} s); wrote {out}', flush=True)
     return doc
 
 

@@ -9,11 +9,14 @@ Per MoE layer call (world = 1):
   3. the C++ planner picks the misses (ascending expert) and their slots (routing-aware
      eviction, bit-exact with the reference) and the H2D engine enqueues their copies on its
      own stream;
-  4. experts already resident run first; the compute stream then waits on the GPU for the
-     copies and runs the fetched experts (``overlap=False`` restores the reference's serial
-     host wait).  A prefill-sized call copies its misses in a few groups, heaviest expert
-     first, and computes each group as soon as its copies land, so that only the lightest
-     group's compute is left after the last copy;
+  4. a decode-sized call copies its misses with one copy-kernel launch on the compute stream
+     itself and then runs every active expert in one FFN launch: no cross-queue wait between
+     the copy and its consumer, and no kernel beside the copy kernel (whose host reads slow
+     the HBM-bound kernels that run next to it).  A prefill-sized call copies on the DMA
+     engines instead and overlaps: experts already resident run first, and the misses are
+     copied in a few groups, heaviest expert first, each computed as soon as its copies land,
+     so that only the lightest group's compute is left after the last copy.
+     ``overlap=False`` restores the reference's serial host wait (DMA copies);
   5. the combine kernel sums each token's k expert rows in fp32 (ascending expert ID).
 """
 import time
@@ -86,6 +89,8 @@ class OffloadRuntime:
         if self.h2d is not None:
             self.h2d.close()
         self.h2d = self.ops.H2DEngine(self.cache, self.pool)
+        self._kernel_copy = self.h2d.kernel_ok
+        self._copy_mode = None
         self.event = 0
         self.fetches_per_rank = np.zeros(self.world, np.int64)
         self.decode_fetches_per_rank = np.zeros(self.world, np.int64)
@@ -158,6 +163,8 @@ class OffloadRuntime:
         d2h.synchronize()
         t_ready = time.perf_counter_ns()
         chunked = T * k >= CHUNK_MIN_PAIRS
+        on_stream = self.overlap and not chunked and self._kernel_copy
+        self._set_copy_mode(on_stream, stream)
         # with chunks or timing the copies are queued here; otherwise the planner's native call
         # queues them itself, right after planning
         queue_here = chunked or self.timing
@@ -185,7 +192,7 @@ class OffloadRuntime:
             groups = [np.arange(len(fetches))]
         timing = self.timing and len(fetches) > 0
         if timing:
-            copy_stream = self.h2d.stream
+            copy_stream = stream if on_stream else self.h2d.stream
             ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
             ev[0].record(copy_stream)
         if queue_here and len(fetches):
@@ -211,12 +218,20 @@ class OffloadRuntime:
             self.h2d.wait_host(fetches[:, 2])
             self.serial_wait_ns += time.perf_counter_ns() - started
         mark = self.ops.timing_mark() if timing else 0
-        if len(resident_list):
+        waits = []
+        if on_stream:
+            # the copies are queued on this stream (the wait on their events costs nothing);
+            # resident rows may come from DMA copies of earlier calls
+            active_list = np.flatnonzero(active)
+            self.h2d.wait_stream(slot_of[active_list], stream)
+            if timing:
+                waits.append((ev[0], ev[1]))   # the copy kernel holds this stream
+            self._ffn(common, active_list, slot32, buf, stream, counts_e)
+        elif len(resident_list):
             self.h2d.wait_stream(slot_of[resident_list], stream)
             self._ffn(common, resident_list, slot32, buf, stream, counts_e)
         shared_out = shared(common[1], out=self._shared_out(T)) if shared is not None else None
-        waits = []
-        if len(fetches):
+        if len(fetches) and not on_stream:
             for g in groups:
                 w0 = w1 = None
                 if timing:
@@ -243,6 +258,15 @@ class OffloadRuntime:
             h['fetch_enqueue'] += t_fetch - t_plan
             h['enqueue_after_fetch'] += time.perf_counter_ns() - t_fetch
         return out
+
+    def _set_copy_mode(self, on_stream, stream):
+        """Copy kernel on ``stream`` for on-stream calls, DMA copies otherwise."""
+        from .h2d import DMA, KERNEL
+        mode = (on_stream, stream.cuda_stream if on_stream else None)
+        if mode != self._copy_mode:
+            self.h2d.engine = KERNEL if on_stream else DMA
+            self.h2d.set_kernel_stream(stream if on_stream else None)
+            self._copy_mode = mode
 
     def _shared_out(self, tokens):
         b = self._bufs[tokens]

@@ -225,6 +225,22 @@ int ferry_h2d_synchronize(ferry_h2d* h);
 int64_t ferry_h2d_copies(const ferry_h2d* h);
 /* the engine's copy stream (for event timing by the caller) */
 void* ferry_h2d_stream(ferry_h2d* h);
+/* How the engine copies (no counterpart in the reference, whose engine always issues one
+ * cudaMemcpyAsync per row).  FERRY_H2D_KERNEL: one launch of a copy kernel per fetch call that
+ * reads the pool through its device mapping (the default when the pool has one and rows are
+ * 16-byte multiples).  FERRY_H2D_DMA: one hipMemcpyAsync per row part on two DMA streams.
+ * Both write the same bytes, and every fetch is ordered after the copies of either kind that
+ * the engine queued before it.  ferry_h2d_set_kernel_stream picks the stream that kernel-mode
+ * copies run on (initially the engine's own, ferry_h2d_stream; null is HIP's null stream):
+ * with the caller's compute stream, the
+ * kernels that read the fetched rows follow the copy on one queue, with no cross-queue wait.
+ * The copy kernel slows HBM-bound kernels that run beside it (its host reads hold memory
+ * resources for the link's latency), so callers use it where little compute overlaps the copy.
+ */
+enum { FERRY_H2D_DMA = 0, FERRY_H2D_KERNEL = 1 };
+int ferry_h2d_set_engine(ferry_h2d* h, int32_t kind);
+int32_t ferry_h2d_engine(const ferry_h2d* h);
+int ferry_h2d_set_kernel_stream(ferry_h2d* h, void* stream);
 
 /*
  * Plan one layer call and enqueue its fetch in one host call: the steps of ferry/runtime.py:64-89

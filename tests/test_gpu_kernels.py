@@ -377,17 +377,26 @@ def test_full_layer_matches_fp64(device):
 # H2D engine
 # ---------------------------------------------------------------------------------------------
 
-def test_h2d_fetch_and_counters(device):
+@pytest.mark.parametrize('kind', ['kernel', 'dma'])
+def test_h2d_fetch_and_counters(device, kind):
+    from ferry_amd import h2d
     from ferry_amd.h2d import H2DEngine
     rows, cap, width = 10, 4, 1 << 16
     pool = torch.arange(rows * width, dtype=torch.int32).view(rows, width).to(torch.bfloat16).pin_memory()
     cache = torch.zeros((cap, width), dtype=torch.bfloat16, device=device)
     eng = H2DEngine(cache, pool)
+    assert eng.engine == h2d.KERNEL     # torch's pinned memory is device-mapped
+    eng.engine = h2d.KERNEL if kind == 'kernel' else h2d.DMA
     eng.fetch([2, 0, 3], [7, 1, 9])
     eng.wait_host([2, 0, 3])
     assert eng.copies == 3
     assert torch.equal(cache[2].cpu(), pool[7]) and torch.equal(cache[0].cpu(), pool[1])
     assert torch.equal(cache[3].cpu(), pool[9])
+    # a slot named twice in one call ends with the later row, as with copies in stream order
+    eng.fetch([0, 1, 0, 2, 1], [5, 6, 7, 8, 3])
+    eng.wait_host([0, 1, 2])
+    for slot, key in ((0, 7), (1, 3), (2, 8)):
+        assert torch.equal(cache[slot].cpu(), pool[key]), (kind, slot)
     s = torch.cuda.current_stream()
     eng.fetch([1], [4])
     eng.wait_stream([1], s)
@@ -402,15 +411,18 @@ def test_h2d_fetch_and_counters(device):
     eng.close()
 
 
-def test_h2d_copy_waits_for_last_use(device):
+@pytest.mark.parametrize('kind', ['kernel', 'dma'])
+def test_h2d_copy_waits_for_last_use(device, kind):
     """A fetch into a slot must not overwrite it before the compute that reads it ends."""
     ops = _ops()
+    from ferry_amd import h2d
     from ferry_amd.h2d import H2DEngine
     H, I, T, k, E = 2048, 768, 64, 1, 2
     rows_w = _pool(2, H, I, seed=21)
     pool = rows_w.pin_memory()
     cache = torch.zeros((1, 3 * H * I), dtype=torch.bfloat16, device=device)
     eng = H2DEngine(cache, pool)
+    eng.engine = h2d.KERNEL if kind == 'kernel' else h2d.DMA
     eng.fetch([0], [0])
     s = torch.cuda.current_stream()
     eng.wait_stream([0], s)
@@ -431,3 +443,64 @@ def test_h2d_copy_waits_for_last_use(device):
     torch.testing.assert_close(part.cpu().float(), ref.float(), rtol=2e-2, atol=1e-2)
     assert torch.equal(cache[0].cpu(), rows_w[1])
     eng.close()
+
+
+def test_h2d_kernel_copy_on_caller_stream(device):
+    """Kernel-mode copies queued on the caller's stream -- torch's default stream, whose handle
+    is 0, and a side stream -- are ordered before that stream's next kernels with no wait."""
+    from ferry_amd.h2d import H2DEngine
+    rows, cap, width = 12, 6, 3 * 64 * 128
+    pool = torch.randn((rows, width)).to(torch.bfloat16).pin_memory()
+    cache = torch.zeros((cap, width), dtype=torch.bfloat16, device=device)
+    eng = H2DEngine(cache, pool)
+    default = torch.cuda.current_stream()
+    assert default.cuda_stream == 0
+    side = torch.cuda.Stream()
+    for i, st in enumerate((default, side, default)):
+        eng.set_kernel_stream(st)
+        with torch.cuda.stream(st):
+            eng.fetch([i, i + 3], [2 * i, 2 * i + 5])
+            snap = cache[[i, i + 3]].clone()     # same stream, right after the copy kernel
+        torch.cuda.synchronize()
+        assert torch.equal(snap.cpu(), pool[[2 * i, 2 * i + 5]]), i
+    eng.set_kernel_stream(None)
+    eng.fetch([5], [11])
+    eng.wait_host([5])
+    assert torch.equal(cache[5].cpu(), pool[11])
+    eng.close()
+
+
+def test_h2d_kernel_copy_many_rows_and_ragged_widths(device):
+    """The copy kernel against the DMA path: a fetch of more rows than one launch takes (300, in
+    any slot order), row sizes that are and are not multiples of its 16-byte unit (the latter
+    stay on DMA), and both kinds interleaved on one engine."""
+    from ferry_amd import h2d
+    from ferry_amd.h2d import H2DEngine
+    g = torch.Generator().manual_seed(5)
+    rows, cap = 320, 300
+    for width in (8 * 4099, 7):          # 65,584 B rows (16-byte multiple) and 14 B rows
+        pool = torch.randint(-30000, 30000, (rows, width), generator=g, dtype=torch.int16)
+        pool = pool.view(torch.bfloat16).pin_memory()
+        cache = torch.zeros((cap, width), dtype=torch.bfloat16, device=device)
+        eng = H2DEngine(cache, pool)
+        if width % 8:
+            assert eng.engine == h2d.DMA
+            with pytest.raises(RuntimeError):
+                eng.engine = h2d.KERNEL
+        else:
+            assert eng.engine == h2d.KERNEL
+        slots = torch.randperm(cap, generator=g).numpy()
+        keys = torch.randperm(rows, generator=g)[:cap].numpy()
+        bits = lambda t: t.view(torch.int16)   # noqa: E731  (random bits include NaNs)
+        eng.fetch(slots, keys)
+        eng.wait_host(slots)
+        assert torch.equal(bits(cache.cpu()[slots]), bits(pool[keys]))
+        if width % 8 == 0:
+            eng.engine = h2d.DMA
+            eng.fetch(slots[:50], keys[::-1][:50])
+            eng.engine = h2d.KERNEL
+            eng.fetch(slots[50:60], keys[:10])
+            eng.wait_host(slots[:60])
+            assert torch.equal(bits(cache.cpu()[slots[:50]]), bits(pool[keys[::-1][:50].copy()]))
+            assert torch.equal(bits(cache.cpu()[slots[50:60]]), bits(pool[keys[:10]]))
+        eng.close()

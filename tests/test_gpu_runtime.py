@@ -71,6 +71,55 @@ def test_runtime_small_evicting(device):
     assert rt.h2d.copies == int(rt.fetches_per_rank.sum()) > 20   # evictions happened
 
 
+def test_runtime_mixed_copy_modes(device):
+    """Prefill-sized calls (DMA copies, chunked) and decode-sized calls (copy kernel on the
+    compute stream) interleaved on one runtime: every call against the oracle, the eviction
+    trace bit-exact."""
+    from ferry_amd.model import ModelSpec
+    spec = ModelSpec('qwen3_moe', (0, 1), 32, 4, 256, 128)
+    rt, _ = _run(device, spec, cap=24, calls=12, tokens_of=lambda c: [4096, 16, 5000, 3][c % 4],
+                 seed=8, zipf=0.8)
+    assert rt._kernel_copy and rt.h2d.copies > 24
+
+
+@pytest.mark.parametrize('tokens', [16, 64])
+def test_runtime_on_stream_matches_dma_overlap(device, tokens):
+    """The decode path with the copy kernel on the compute stream (one FFN launch after the
+    copy) and the DMA path (resident experts first, then the fetched ones) give bit-identical
+    outputs and the same fetch trace."""
+    from dataclasses import replace
+
+    from ferry_amd import expert_ops as ops
+    from ferry_amd import workloads
+    from ferry_amd.model import QWEN3_30B_A3B
+    from ferry_amd.quota import Topology
+    from ferry_amd.runtime import OffloadRuntime
+    spec = replace(QWEN3_30B_A3B, moe_layers=(0, 1))
+    pool = workloads.make_pool(spec, spec.layers, seed=3)
+    bias = torch.from_numpy(workloads.zipf_log_bias(spec.experts, 1.1, np.random.default_rng(0)))
+    cap = 80      # above any call's distinct experts (<= 62 at 64 tokens), below two layers'
+    runs = []
+    for kernel_copy in (True, False):
+        rt = OffloadRuntime(spec, pool, [cap], 'ferry', Topology.uniform(1, spec.experts))
+        assert rt._kernel_copy
+        rt._kernel_copy = kernel_copy
+        g = torch.Generator(device=device)
+        g.manual_seed(4)
+        outs = []
+        for call in range(8):
+            x = torch.randn((tokens, spec.hidden), generator=g, device=device).to(torch.bfloat16)
+            z = torch.randn((tokens, spec.experts), generator=g, device=device) + bias.to(device)
+            w, sel = ops.router_topk(z.to(torch.bfloat16), spec.topk)
+            assert len(torch.unique(sel)) <= cap
+            outs.append(rt.execute(call % 2, x, sel, w, None).cpu())
+        runs.append((outs, rt.controller.slots[0].copy(), rt.h2d.copies))
+        rt.close()
+    (a, slots_a, n_a), (b, slots_b, n_b) = runs
+    assert n_a == n_b > cap and np.array_equal(slots_a, slots_b)
+    for i, (u, v) in enumerate(zip(a, b)):
+        assert torch.equal(u, v), i
+
+
 def test_runtime_serial_mode(device):
     from ferry_amd.model import ModelSpec
     spec = ModelSpec('qwen3_moe', (0, 1), 16, 4, 256, 128)
@@ -99,6 +148,7 @@ def test_h2d_profiler_writes_loadable_topology(device, tmp_path):
                 '--copies', '16', '--repeats', '3'])
     m = doc['measured']
     assert 1.0 < m['engine_gib_per_s'] < 200.0 and 1.0 < m['single_stream_gib_per_s'] < 200.0
+    assert 1.0 < m['dma_gib_per_s'] < 200.0
     assert len(m['samples']['engine']) == 3
     topo = Topology(out, 1, 16)
     assert topo.lut[:, 0].tolist() == list(range(17))
