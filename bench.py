@@ -23,6 +23,8 @@ Also on the line:
     cache (1,843 / 499 slots) from cold, so every layer fetches its missing experts over PCIe;
   * decode_loop: the 48-layer Qwen3 decode loop (1024-token prefill, then 64-token steps,
     pooled cache of 1,843, W = 128 eviction), ``--loop-steps`` steps (default 8, bounded);
+  * decode_copy_kernel: the headline stream through OffloadRuntime(copy='kernel'): the misses
+    copied by one kernel launch on the compute stream, then one FFN launch (no overlap);
   * cpu_baseline: the reference's op order in torch on the host cores (all cores of the
     process's affinity), median of >= 5 repeats on the decode stream, plus one config-3 prefill
     layer with the 48-layer extrapolation.
@@ -106,7 +108,7 @@ def decode_stream(w, steps, device):
     return out
 
 
-def run_decode(args, device):
+def run_decode(args, device, copy='dma'):
     from ferry_amd import expert_ops as ops
     from ferry_amd import workloads
     from ferry_amd.quota import Topology
@@ -114,7 +116,8 @@ def run_decode(args, device):
     w = workloads.CONFIGS[2]
     spec = w.spec
     pool = workloads.make_pool(spec, 1, seed=0)
-    rt = OffloadRuntime(spec, pool, [w.cache_slots], 'ferry', Topology.uniform(1, spec.experts))
+    rt = OffloadRuntime(spec, pool, [w.cache_slots], 'ferry', Topology.uniform(1, spec.experts),
+                        copy=copy)
     stream = decode_stream(w, args.warmup + args.steps, device)
 
     def step(lg, x):
@@ -552,6 +555,20 @@ def main():
                     parallelism='single GPU (one expert-parallel share)'),
         roofline=roofline, decode=block)
     print(f'# decode done: {line["value"]:.0f} tokens/s', file=sys.stderr, flush=True)
+    # the same decode stream with the copy kernel on the compute stream (not the reference's
+    # fetch scheme, so not the headline): one launch per fetch, then one FFN launch
+    dk = run_decode(args, device, copy='kernel')
+    rk, bk = decode_block(dk, args)
+    line['decode_copy_kernel'] = dict(
+        tokens_per_s=dk['tokens'] / dk['elapsed'], ms_per_step=dk['elapsed'] / args.steps * 1e3,
+        h2d_gbs=bk['h2d_gbs'], fetch_ms_per_step=bk['fetch_ms_per_step'],
+        fetch_hidden_frac=bk['fetch_hidden_frac'], ffn_kernel=rk['kernel'],
+        ffn_avg_launch_us=rk['avg_launch_us'], ffn_launches=rk['launches'],
+        ffn_gbs=rk['achieved'], ffn_frac=rk['frac'],
+        note='copy=kernel: the misses of a step are copied by one kernel launch on the compute '
+             'stream, then every active expert runs in one FFN launch (no overlap)')
+    print(f'# decode (copy kernel) done: {line["decode_copy_kernel"]["tokens_per_s"]:.0f} tokens/s',
+          file=sys.stderr, flush=True)
     if not args.no_prefill:
         line['prefill'] = run_prefill(args, device, 3)
         line['roofline_prefill'] = prefill_roofline(line['prefill'])

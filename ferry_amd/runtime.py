@@ -9,14 +9,16 @@ Per MoE layer call (world = 1):
   3. the C++ planner picks the misses (ascending expert) and their slots (routing-aware
      eviction, bit-exact with the reference) and the H2D engine enqueues their copies on its
      own stream;
-  4. a decode-sized call copies its misses with one copy-kernel launch on the compute stream
-     itself and then runs every active expert in one FFN launch: no cross-queue wait between
-     the copy and its consumer, and no kernel beside the copy kernel (whose host reads slow
-     the HBM-bound kernels that run next to it).  A prefill-sized call copies on the DMA
-     engines instead and overlaps: experts already resident run first, and the misses are
-     copied in a few groups, heaviest expert first, each computed as soon as its copies land,
-     so that only the lightest group's compute is left after the last copy.
-     ``overlap=False`` restores the reference's serial host wait (DMA copies);
+  4. the misses are copied with ``hipMemcpyAsync`` on the fetch engine's DMA streams while the
+     experts already resident run; the compute stream then waits on the GPU for the copies and
+     runs the fetched experts.  A prefill-sized call copies its misses in a few groups,
+     heaviest expert first, each computed as soon as its copies land, so that only the
+     lightest group's compute is left after the last copy.  ``overlap=False`` restores the
+     reference's serial host wait.  ``copy='kernel'`` (not the reference's scheme) copies a
+     decode-sized call's misses with one copy-kernel launch on the compute stream instead and
+     then runs every active expert in one FFN launch: no idle link between copies and no
+     cross-queue wait, but no overlap either (the copy kernel's host reads slow the HBM-bound
+     kernels that run beside it, so nothing runs beside it);
   5. the combine kernel sums each token's k expert rows in fp32 (ascending expert ID).
 """
 import time
@@ -48,7 +50,7 @@ def expert_ops():
 class OffloadRuntime:
     def __init__(self, spec, pool, capacities, policy, topology, history_window=128,
                  balance_tol_bps=200, salt=1, eviction_score='frequency', overlap=True,
-                 timing=False):
+                 timing=False, copy='dma'):
         if dist.is_available() and dist.is_initialized() and dist.get_world_size() != 1:
             raise NotImplementedError('ferry_amd runs on one GPU (world = 1)')
         if len(capacities) != 1:
@@ -61,6 +63,9 @@ class OffloadRuntime:
         self.window = history_window
         self.overlap = overlap
         self.timing = timing
+        if copy not in ('dma', 'kernel'):
+            raise ValueError("copy must be 'dma' or 'kernel'")
+        self.copy = copy
         self.ops = expert_ops()
         self.device = torch.device('cuda', torch.cuda.current_device())
         self.cache = torch.empty((self.cap, spec.expert_elements), dtype=torch.bfloat16,
@@ -89,7 +94,9 @@ class OffloadRuntime:
         if self.h2d is not None:
             self.h2d.close()
         self.h2d = self.ops.H2DEngine(self.cache, self.pool)
-        self._kernel_copy = self.h2d.kernel_ok
+        self._kernel_copy = self.copy == 'kernel' and self.h2d.kernel_ok
+        if self.copy == 'kernel' and not self._kernel_copy:
+            raise RuntimeError("copy='kernel' needs a device-mapped pool with 16-byte rows")
         self._copy_mode = None
         self.event = 0
         self.fetches_per_rank = np.zeros(self.world, np.int64)

@@ -13,13 +13,13 @@ pytestmark = pytest.mark.gpu
 
 
 def _run(device, spec, cap, calls, tokens_of, seed, zipf, overlap=True, check_every=1,
-         gate_scale=8.0):
+         gate_scale=8.0, copy='dma'):
     from ferry_amd import workloads
     from ferry_amd.quota import Topology
     from ferry_amd.runtime import OffloadRuntime
     pool = workloads.make_pool(spec, spec.layers, seed=seed)
     rt = OffloadRuntime(spec, pool, [cap], 'ferry', Topology.uniform(1, spec.experts),
-                        overlap=overlap)
+                        overlap=overlap, copy=copy)
     planner = PlannerRef(spec.layers, spec.experts, cap)
     hist = GateHistoryRef(spec.layers, spec.experts, 128)
     g = torch.Generator(device=device)
@@ -72,14 +72,22 @@ def test_runtime_small_evicting(device):
 
 
 def test_runtime_mixed_copy_modes(device):
-    """Prefill-sized calls (DMA copies, chunked) and decode-sized calls (copy kernel on the
-    compute stream) interleaved on one runtime: every call against the oracle, the eviction
-    trace bit-exact."""
+    """copy='kernel': prefill-sized calls (DMA copies, chunked) and decode-sized calls (copy
+    kernel on the compute stream) interleaved on one runtime: every call against the oracle,
+    the eviction trace bit-exact."""
     from ferry_amd.model import ModelSpec
     spec = ModelSpec('qwen3_moe', (0, 1), 32, 4, 256, 128)
     rt, _ = _run(device, spec, cap=24, calls=12, tokens_of=lambda c: [4096, 16, 5000, 3][c % 4],
-                 seed=8, zipf=0.8)
+                 seed=8, zipf=0.8, copy='kernel')
     assert rt._kernel_copy and rt.h2d.copies > 24
+
+
+def test_runtime_small_evicting_copy_kernel(device):
+    from ferry_amd.model import ModelSpec
+    spec = ModelSpec('qwen3_moe', (0, 1, 2), 32, 4, 256, 128)
+    rt, _ = _run(device, spec, cap=20, calls=40, tokens_of=lambda c: [3, 16, 40, 1, 130][c % 5],
+                 seed=5, zipf=1.0, copy='kernel')
+    assert rt.h2d.copies == int(rt.fetches_per_rank.sum()) > 20
 
 
 @pytest.mark.parametrize('tokens', [16, 64])
@@ -99,10 +107,10 @@ def test_runtime_on_stream_matches_dma_overlap(device, tokens):
     bias = torch.from_numpy(workloads.zipf_log_bias(spec.experts, 1.1, np.random.default_rng(0)))
     cap = 80      # above any call's distinct experts (<= 62 at 64 tokens), below two layers'
     runs = []
-    for kernel_copy in (True, False):
-        rt = OffloadRuntime(spec, pool, [cap], 'ferry', Topology.uniform(1, spec.experts))
-        assert rt._kernel_copy
-        rt._kernel_copy = kernel_copy
+    for copy in ('kernel', 'dma'):
+        rt = OffloadRuntime(spec, pool, [cap], 'ferry', Topology.uniform(1, spec.experts),
+                            copy=copy)
+        assert rt._kernel_copy == (copy == 'kernel')
         g = torch.Generator(device=device)
         g.manual_seed(4)
         outs = []
