@@ -9,19 +9,21 @@
 // resident can run while missing ones are still in flight.
 //
 // Two ways to copy, chosen per engine (ferry_h2d_set_engine):
-//  * FERRY_H2D_KERNEL (the default when the pool has a device mapping and rows are 16-byte
-//    multiples): one launch of h2d_copy_kernel per fetch call on the first stream reads the
-//    pool over PCIe and writes the slots.  One launch has no idle link time between rows.
-//  * FERRY_H2D_DMA: each row is copied as kLanes equal parts by hipMemcpyAsync on kLanes
-//    streams: one DMA stream does not fill the host link (measured on MI355X: ~47 GB/s with one
-//    stream, ~56.5 GB/s with two), and splitting every row keeps the lanes balanced whatever
-//    the number of misses.  A fetch call forks the lanes from the first stream and joins them
-//    back into it.  Per copy only the hipMemcpyAsync itself is queued: a stream wait or an
-//    event between two copies on a DMA stream costs tens of microseconds of idle link.
+//  * FERRY_H2D_DMA (the default, the reference's scheme): hipMemcpyAsync on kLanes DMA streams.
+//    One DMA stream does not fill the host link (measured on MI355X: ~47 GB/s with one stream,
+//    ~56.5 GB/s with two).  The call's rows, concatenated, are cut into kLanes equal byte
+//    ranges, which keeps the lanes balanced whatever the number of misses.  The lanes are
+//    joined back into the first stream after their copies.  Per copy only the hipMemcpyAsync
+//    itself is queued: a stream wait or an event between two copies on a DMA stream costs tens
+//    of microseconds of idle link.
+//  * FERRY_H2D_KERNEL (possible when the pool has a device mapping and rows are 16-byte
+//    multiples): one launch of h2d_copy_kernel per fetch call, on the kernel stream
+//    (ferry_h2d_set_kernel_stream; initially the first stream), reads the pool over PCIe and
+//    writes the slots.  One launch leaves no idle link time between rows, but its host reads
+//    slow the HBM-bound kernels that run beside it.
 // A slot is ready when the copy-done events of all its lanes have fired (in kernel mode every
-// lane's event is the first stream's).  The first stream (ferry_h2d_stream) brackets every copy
-// of a call.  The engine owns its streams (default priority) and events; it allocates no device
-// memory.
+// lane's event is the launch's).  The engine owns its streams (default priority) and events; it
+// allocates no device memory.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -58,6 +60,7 @@ struct ferry_h2d {
   hipStream_t kernel_stream = nullptr;  // stream of kernel-mode copies (initially stream[0])
   std::shared_ptr<Event> last_kernel_copy;  // done event of the latest kernel-mode fetch
   bool dma_since_kernel = false;      // DMA fetches queued since the latest kernel-mode fetch
+  std::shared_ptr<Event> lane_done[kLanes];  // per lane: end of its copies of the last DMA call
   std::vector<int64_t> batch_of;      // per slot: last kernel-mode launch batch that wrote it
   int64_t batch = 0;
   hipStream_t last_kernel_stream = nullptr;  // stream of the latest kernel-mode fetch
@@ -65,7 +68,7 @@ struct ferry_h2d {
   int64_t part[kLanes + 1] = {};      // byte boundaries of the row parts
   int32_t device = 0;
   hipStream_t stream[kLanes] = {};
-  hipEvent_t join = nullptr;          // fork / join of the lanes around a fetch call
+  hipEvent_t join = nullptr;          // joins the lanes into the first stream
   std::vector<std::shared_ptr<Event>> copy_done[kLanes];  // per lane, per slot
   std::vector<int64_t> copy_seq;      // per slot: sequence number of its last copy, -1 if none
   std::vector<std::shared_ptr<Event>> used;  // per slot: last compute that read it
@@ -112,7 +115,6 @@ extern "C" int ferry_h2d_create(void* cache, int64_t cache_rows, const void* poo
   h->row_bytes = row_bytes;
   h->device = device;
   h->pool_dev = (const char*)attr.devicePointer;
-  if (kernel_copy_ok(h.get())) h->kind = FERRY_H2D_KERNEL;
   for (int l = 0; l <= kLanes; ++l) h->part[l] = row_bytes * l / kLanes / 256 * 256;
   h->part[kLanes] = row_bytes;
   for (int l = 0; l < kLanes; ++l) {
@@ -212,24 +214,58 @@ extern "C" int ferry_h2d_fetch(ferry_h2d* h, const int64_t* slots, const int64_t
   }
   // kernel-mode copies queued on another stream end before these copies start
   if (h->last_kernel_copy && !h->dma_since_kernel)
-    H2D_HIP(hipStreamWaitEvent(h->stream[0], h->last_kernel_copy->e, 0));
+    for (int l = 0; l < kLanes; ++l)
+      H2D_HIP(hipStreamWaitEvent(h->stream[l], h->last_kernel_copy->e, 0));
   h->dma_since_kernel = true;
-  // fork: the other lanes start after what is already queued on lane 0, so that events the
-  // caller records on lane 0 around the call bracket every copy of it
-  for (int l = 1; l < kLanes; ++l) {
-    H2D_HIP(hipEventRecord(h->join, h->stream[0]));
-    H2D_HIP(hipStreamWaitEvent(h->stream[l], h->join, 0));
+  // Each lane starts after the other lanes' copies of earlier calls (a slot's bytes can move to
+  // another lane from one call to the next).  Those have usually finished by now, and then no
+  // wait is queued: a lane waiting on an event that another DMA queue records starts tens of
+  // microseconds late even when nothing is pending.
+  for (int m = 0; m < kLanes; ++m) {
+    if (!h->lane_done[m]) continue;
+    const hipError_t q = hipEventQuery(h->lane_done[m]->e);
+    if (q == hipSuccess) continue;
+    if (q != hipErrorNotReady) {
+      ferry::set_error("hipEventQuery failed: %s", hipGetErrorString(q));
+      return 3;
+    }
+    (void)hipGetLastError();
+    for (int l = 0; l < kLanes; ++l)
+      if (l != m) H2D_HIP(hipStreamWaitEvent(h->stream[l], h->lane_done[m]->e, 0));
   }
   for (int l = 0; l < kLanes; ++l)
     for (hipEvent_t e : pending) H2D_HIP(hipStreamWaitEvent(h->stream[l], e, 0));
-  for (int64_t i = 0; i < n; ++i) {
-    const int64_t slot = slots[i], key = keys[i];
+  // The call's rows, concatenated, are cut into kLanes equal byte ranges, one per lane: a lane
+  // copies about n / kLanes whole rows plus a part of the row its range ends in.  A call that
+  // names a slot twice splits every row instead, whose in-lane order makes the later row win.
+  bool repeated = false;
+  ++h->batch;
+  for (int64_t i = 0; i < n && !repeated; ++i) {
+    repeated = h->batch_of[(size_t)slots[i]] == h->batch;
+    h->batch_of[(size_t)slots[i]] = h->batch;
+  }
+  const int64_t rb = h->row_bytes;
+  if (!repeated) {
+    const int64_t total = n * rb;
     for (int l = 0; l < kLanes; ++l) {
-      const int64_t b0 = h->part[l], nb = h->part[l + 1] - b0;
-      if (nb > 0)
-        H2D_HIP(hipMemcpyAsync(h->cache + slot * h->row_bytes + b0,
-                               h->pool + key * h->row_bytes + b0, (size_t)nb,
-                               hipMemcpyHostToDevice, h->stream[l]));
+      const int64_t lo = l == 0 ? 0 : total * l / kLanes / 256 * 256;
+      const int64_t hi = l + 1 == kLanes ? total : total * (l + 1) / kLanes / 256 * 256;
+      for (int64_t b = lo; b < hi;) {
+        const int64_t i = b / rb, off = b - i * rb;
+        const int64_t nb = (hi - b < rb - off) ? hi - b : rb - off;
+        H2D_HIP(hipMemcpyAsync(h->cache + slots[i] * rb + off, h->pool + keys[i] * rb + off,
+                               (size_t)nb, hipMemcpyHostToDevice, h->stream[l]));
+        b += nb;
+      }
+    }
+  } else {
+    for (int64_t i = 0; i < n; ++i) {
+      for (int l = 0; l < kLanes; ++l) {
+        const int64_t b0 = h->part[l], nb = h->part[l + 1] - b0;
+        if (nb > 0)
+          H2D_HIP(hipMemcpyAsync(h->cache + slots[i] * rb + b0, h->pool + keys[i] * rb + b0,
+                                 (size_t)nb, hipMemcpyHostToDevice, h->stream[l]));
+      }
     }
   }
   for (int l = 0; l < kLanes; ++l) {
@@ -237,6 +273,7 @@ extern "C" int ferry_h2d_fetch(ferry_h2d* h, const int64_t* slots, const int64_t
     H2D_HIP(hipEventCreateWithFlags(&ev->e, hipEventDisableTiming));
     H2D_HIP(hipEventRecord(ev->e, h->stream[l]));
     for (int64_t i = 0; i < n; ++i) h->copy_done[l][(size_t)slots[i]] = ev;
+    h->lane_done[l] = ev;
   }
   for (int64_t i = 0; i < n; ++i) h->copy_seq[(size_t)slots[i]] = h->seq++;
   h->copies += n;

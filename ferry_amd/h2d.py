@@ -1,9 +1,8 @@
 """H2D expert fetch engine (the reference's ``H2DEngine``, ferry/csrc/expert_ops.cpp:94-142).
 
-Copies rows of a pinned host pool into GPU cache slots on the engine's own stream: by default
-with one launch of a copy kernel per fetch call that reads the pool through its device mapping
-(``KERNEL``), or with one ``hipMemcpyAsync`` per row part on two DMA streams (``DMA``, the
-reference's way).  A copy into a slot waits, on the GPU, for the last compute that read that
+Copies rows of a pinned host pool into GPU cache slots: by default with ``hipMemcpyAsync`` on
+the engine's two DMA streams (``DMA``, the reference's way), or with one launch of a copy
+kernel per fetch call that reads the pool through its device mapping (``KERNEL``).  A copy into a slot waits, on the GPU, for the last compute that read that
 slot (``mark_used``).  ``wait_host`` blocks the host like the reference;
 ``wait_stream`` makes a compute stream wait on the GPU instead, which lets resident experts
 run while missing ones are still in flight.

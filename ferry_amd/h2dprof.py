@@ -7,11 +7,11 @@ written as the JSON that ferry/quota.py:80-90 reads).  With one GPU there is one
 domain (mask 1) and the quota of m missing experts is [m].
 
 Three rates are measured, all in GiB/s like the reference's file:
-  * ``engine``: one fetch call through this package's H2D engine in its default mode (the copy
-    kernel, one launch for all rows, when the pool is device-mapped), which is how
-    ``OffloadRuntime`` copies a decode step's misses; this is the domain's ``gib_per_s``;
-  * ``dma``: the engine's DMA mode (each row split over two DMA streams), how the runtime copies
-    a prefill call's misses;
+  * ``engine``: one fetch call through this package's H2D engine in its default mode
+    (``hipMemcpyAsync`` on two DMA streams), which is how ``OffloadRuntime`` copies by default;
+    this is the domain's ``gib_per_s``;
+  * ``kernel``: the engine's copy kernel (one launch for all rows; ``OffloadRuntime(copy=
+    'kernel')`` on decode-sized calls);
   * ``single_stream``: one ``copy_`` per expert on one stream, the reference's pattern.
 
     python -m ferry_amd.h2dprof --output topology/mi355x_qwen3.json [--model-path DIR]
@@ -56,9 +56,9 @@ def _time_single_stream(stream, pool, cache, copies, spin_cycles):
 
 def measure(expert_bytes, copies=64, repeats=5, slots=None, pool_rows=8, device=0,
             spin_cycles=SPIN_CYCLES):
-    """Median GiB/s of ``copies`` back-to-back expert copies: dict(engine, dma, single_stream,
-    samples)."""
-    from .h2d import DMA, H2DEngine
+    """Median GiB/s of ``copies`` back-to-back expert copies: dict(engine, kernel, single_stream,
+    samples); kernel is None when the pool cannot use the copy kernel."""
+    from .h2d import KERNEL, H2DEngine
     from .hostmem import pinned_empty
     torch.cuda.set_device(device)
     elements = expert_bytes // 2
@@ -67,31 +67,39 @@ def measure(expert_bytes, copies=64, repeats=5, slots=None, pool_rows=8, device=
     pool.copy_(torch.randn((pool_rows, elements)).to(torch.bfloat16))
     cache = torch.empty((slots, elements), dtype=torch.bfloat16, device=device)
     engine = H2DEngine(cache, pool)
-    dma = H2DEngine(cache, pool)
-    dma.engine = DMA
+    kern = H2DEngine(cache, pool)
+    if kern.kernel_ok:
+        kern.engine = KERNEL
+    else:
+        kern.close()
+        kern = None
     stream = torch.cuda.Stream(device=device)
     idx = list(range(copies))
     slot_seq = [i % slots for i in idx]
     key_seq = [i % pool_rows for i in idx]
     gib = copies * expert_bytes / 2 ** 30
+    engines = dict(engine=engine, kernel=kern)
+    kinds = ['engine', 'single_stream'] + (['kernel'] if kern is not None else [])
     # warm up every path
-    _time_engine(engine, slot_seq[:8], key_seq[:8], 0)
-    _time_engine(dma, slot_seq[:8], key_seq[:8], 0)
-    _time_single_stream(stream, pool, cache, 8, 0)
-    samples = dict(engine=[], dma=[], single_stream=[])
-    kinds = ['engine', 'dma', 'single_stream']
+    for kind in kinds:
+        if kind == 'single_stream':
+            _time_single_stream(stream, pool, cache, 8, 0)
+        else:
+            _time_engine(engines[kind], slot_seq[:8], key_seq[:8], 0)
+    samples = {kind: [] for kind in kinds}
     for rep in range(repeats):
-        for kind in kinds[rep % 3:] + kinds[:rep % 3]:
+        for kind in kinds[rep % len(kinds):] + kinds[:rep % len(kinds)]:
             if kind == 'single_stream':
                 t = _time_single_stream(stream, pool, cache, copies, spin_cycles)
             else:
-                t = _time_engine(engine if kind == 'engine' else dma, slot_seq, key_seq,
-                                 spin_cycles)
+                t = _time_engine(engines[kind], slot_seq, key_seq, spin_cycles)
             samples[kind].append(gib / t)
-    for e in (engine, dma):
-        e.synchronize()
-        e.close()
-    return dict(engine=statistics.median(samples['engine']), dma=statistics.median(samples['dma']),
+    for e in engines.values():
+        if e is not None:
+            e.synchronize()
+            e.close()
+    return dict(engine=statistics.median(samples['engine']),
+                kernel=statistics.median(samples['kernel']) if kern is not None else None,
                 single_stream=statistics.median(samples['single_stream']), samples=samples)
 
 
@@ -103,7 +111,7 @@ def topology_document(measured, expert_bytes, experts, model_type=None, device=0
                               per_gpu_gib_per_s=[float(measured['engine'])])],
                 quota_lut=[[m] for m in range(experts + 1)],
                 measured=dict(engine_gib_per_s=measured['engine'],
-                              dma_gib_per_s=measured['dma'],
+                              kernel_gib_per_s=measured['kernel'],
                               single_stream_gib_per_s=measured['single_stream'],
                               samples=measured['samples']))
 
@@ -130,7 +138,7 @@ def main(argv=None):
     out.parent.mkdir(parents=True, exist_ok=True)
     out.write_text(json.dumps(doc, indent=1) + '\n')
     print(f'H2D {a.expert_bytes} B copies x {a.copies}, median of {a.repeats}: engine '
-          f'{res["engine"]:.2f} GiB/s, DMA {res["dma"]:.2f} GiB/s, single stream '
+          f'{res["engine"]:.2f} GiB/s, copy kernel {res["kernel"] or 0:.2f} GiB/s, single stream '
           f'{res["single_stream"]:.2f} GiB/s ({time.time() - t0:.1f} s); wrote {out}', flush=True)
     return doc
 

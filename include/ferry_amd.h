@@ -226,9 +226,10 @@ int64_t ferry_h2d_copies(const ferry_h2d* h);
 /* the engine's copy stream (for event timing by the caller) */
 void* ferry_h2d_stream(ferry_h2d* h);
 /* How the engine copies (no counterpart in the reference, whose engine always issues one
- * cudaMemcpyAsync per row).  FERRY_H2D_KERNEL: one launch of a copy kernel per fetch call that
- * reads the pool through its device mapping (the default when the pool has one and rows are
- * 16-byte multiples).  FERRY_H2D_DMA: one hipMemcpyAsync per row part on two DMA streams.
+ * cudaMemcpyAsync per row).  FERRY_H2D_DMA (the default): hipMemcpyAsync on two DMA streams,
+ * each taking half of the call's bytes.  FERRY_H2D_KERNEL: one launch of a copy kernel per
+ * fetch call that reads the pool through its device mapping (possible when the pool has one
+ * and rows are 16-byte multiples).
  * Both write the same bytes, and every fetch is ordered after the copies of either kind that
  * the engine queued before it.  ferry_h2d_set_kernel_stream picks the stream that kernel-mode
  * copies run on (initially the engine's own, ferry_h2d_stream; null is HIP's null stream):

@@ -264,8 +264,8 @@ def test_topology_file_round_trip(tmp_path):
     import json
     from ferry_amd.h2dprof import topology_document
     from ferry_amd.quota import Topology
-    measured = dict(engine=52.5, dma=51.0, single_stream=44.0,
-                    samples=dict(engine=[52.5], dma=[51.0], single_stream=[44.0]))
+    measured = dict(engine=52.5, kernel=55.0, single_stream=44.0,
+                    samples=dict(engine=[52.5], kernel=[55.0], single_stream=[44.0]))
     doc = topology_document(measured, 9437184, 128, 'qwen3_moe')
     path = tmp_path / 'topo.json'
     path.write_text(json.dumps(doc))

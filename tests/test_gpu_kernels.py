@@ -385,7 +385,7 @@ def test_h2d_fetch_and_counters(device, kind):
     pool = torch.arange(rows * width, dtype=torch.int32).view(rows, width).to(torch.bfloat16).pin_memory()
     cache = torch.zeros((cap, width), dtype=torch.bfloat16, device=device)
     eng = H2DEngine(cache, pool)
-    assert eng.engine == h2d.KERNEL     # torch's pinned memory is device-mapped
+    assert eng.engine == h2d.DMA and eng.kernel_ok    # torch's pinned memory is device-mapped
     eng.engine = h2d.KERNEL if kind == 'kernel' else h2d.DMA
     eng.fetch([2, 0, 3], [7, 1, 9])
     eng.wait_host([2, 0, 3])
@@ -448,11 +448,13 @@ def test_h2d_copy_waits_for_last_use(device, kind):
 def test_h2d_kernel_copy_on_caller_stream(device):
     """Kernel-mode copies queued on the caller's stream -- torch's default stream, whose handle
     is 0, and a side stream -- are ordered before that stream's next kernels with no wait."""
+    from ferry_amd import h2d
     from ferry_amd.h2d import H2DEngine
     rows, cap, width = 12, 6, 3 * 64 * 128
     pool = torch.randn((rows, width)).to(torch.bfloat16).pin_memory()
     cache = torch.zeros((cap, width), dtype=torch.bfloat16, device=device)
     eng = H2DEngine(cache, pool)
+    eng.engine = h2d.KERNEL
     default = torch.cuda.current_stream()
     assert default.cuda_stream == 0
     side = torch.cuda.Stream()
@@ -483,12 +485,13 @@ def test_h2d_kernel_copy_many_rows_and_ragged_widths(device):
         pool = pool.view(torch.bfloat16).pin_memory()
         cache = torch.zeros((cap, width), dtype=torch.bfloat16, device=device)
         eng = H2DEngine(cache, pool)
+        assert eng.engine == h2d.DMA
         if width % 8:
-            assert eng.engine == h2d.DMA
+            assert not eng.kernel_ok
             with pytest.raises(RuntimeError):
                 eng.engine = h2d.KERNEL
         else:
-            assert eng.engine == h2d.KERNEL
+            eng.engine = h2d.KERNEL
         slots = torch.randperm(cap, generator=g).numpy()
         keys = torch.randperm(rows, generator=g)[:cap].numpy()
         bits = lambda t: t.view(torch.int16)   # noqa: E731  (random bits include NaNs)

@@ -156,7 +156,7 @@ def test_h2d_profiler_writes_loadable_topology(device, tmp_path):
                 '--copies', '16', '--repeats', '3'])
     m = doc['measured']
     assert 1.0 < m['engine_gib_per_s'] < 200.0 and 1.0 < m['single_stream_gib_per_s'] < 200.0
-    assert 1.0 < m['dma_gib_per_s'] < 200.0
+    assert 1.0 < m['kernel_gib_per_s'] < 200.0
     assert len(m['samples']['engine']) == 3
     topo = Topology(out, 1, 16)
     assert topo.lut[:, 0].tolist() == list(range(17))
