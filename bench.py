@@ -156,6 +156,7 @@ def run_decode(args, device, copy='dma'):
     fetch_ms, exposed_ms, overlap_ms = rt.fetch_timing()   # reads the launch log: before disabling
     ops.timing_enable(False)
     res = dict(workload=w, elapsed=t1 - t0, instrumented_elapsed=t3 - t2,
+               critical=rt.critical_path_timing(),
                sync_timeouts=ops.ffn_sync_timeouts(),
                tokens=w.tokens * args.steps, copies=copies, kernels=ks, fetch_ms=fetch_ms,
                exposed_ms=exposed_ms, overlap_ms=overlap_ms, expert_bytes=spec.expert_bytes,
@@ -206,7 +207,9 @@ def decode_block(dec, args):
                                      for n, v in ks['launch'].items()},
                  kernel_avg_launch_us={n: v['avg_us'] for n, v in ks['launch'].items()},
                  host_us_per_step={n: v / args.steps / 1e3 for n, v in dec['host_ns'].items()},
-                 instrumented_ms_per_step=dec['instrumented_elapsed'] / args.steps * 1e3)
+                 instrumented_ms_per_step=dec['instrumented_elapsed'] / args.steps * 1e3,
+                 critical_path_us={k: (v * 1e3 if k.endswith('_ms') and v is not None else v)
+                                   for k, v in dec['critical'].items()})
     return roofline, block
 
 

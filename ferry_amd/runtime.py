@@ -103,6 +103,7 @@ class OffloadRuntime:
         self.decode_fetches_per_rank = np.zeros(self.world, np.int64)
         self.serial_wait_ns = 0
         self.timings = []
+        self.step_marks = []   # timing=True: (ids ready, copies queued, copies done, compute resumes)
         self.kernel_bytes = dict(up=0, down=0, flops=0, experts=0, launches=0)
         # host time per phase of execute (ns, timing=True): the planning path between the
         # wait for the routing IDs and the fetch enqueue is on the critical path of a step
@@ -158,7 +159,7 @@ class OffloadRuntime:
         if not frequency:
             tail = min(T, self.window)
             tail_host = probs_tail[-tail:].float().to('cpu', non_blocking=True)
-        d2h = torch.cuda.Event()
+        d2h = torch.cuda.Event(enable_timing=self.timing)
         d2h.record(stream)
 
         # 2. layout (overlaps the host planning)
@@ -253,6 +254,7 @@ class OffloadRuntime:
         self.h2d.mark_used(slot_of[np.flatnonzero(active)], stream)
         if timing:
             self.timings.append((ev, waits, (mark, self.ops.timing_mark())))
+            self.step_marks.append((d2h, ev[0], ev[1], waits[-1][1] if waits else None))
         self.event += 1
 
         # 5. combine (+ the shared experts' output)
@@ -313,6 +315,21 @@ class OffloadRuntime:
             exposed += sum(max(0.0, a.elapsed_time(b)) for a, b in waits)
             overlapped += self.ops.timing_overlap(m0, m1, ev[0], ev[1])
         return fetch, exposed, overlapped
+
+    def critical_path_timing(self):
+        """Mean GPU-side gaps (ms) over the calls with copies recorded with timing=True: from the
+        routing IDs being written (the history kernel's end) to the copies being queued (the
+        host reads the IDs and plans in between), and from the last copy's end to the compute
+        stream resuming after its wait for the copies."""
+        torch.cuda.synchronize(self.device)
+        plan, resume = [], []
+        for d2h, q, done, w1 in self.step_marks:
+            plan.append(d2h.elapsed_time(q))
+            if w1 is not None:
+                resume.append(done.elapsed_time(w1))
+        mean = lambda v: sum(v) / len(v) if v else None   # noqa: E731
+        return dict(ids_to_copy_queue_ms=mean(plan), copy_end_to_compute_ms=mean(resume),
+                    calls=len(plan))
 
     def close(self):
         if self.h2d is not None:
