@@ -1387,11 +1387,44 @@ __global__ __launch_bounds__(kTiledThreads, 1) void ffn_tiled(FfnArgs a) {
       pipeline(std::false_type{});
     else
       pipeline(std::true_type{});
+    // 32x32 accumulator layout: column = lane & 31, row(v) = (v / 4) * 8 + (lane / 32) * 4 + v % 4.
+    if constexpr (MODE == 1) {
+      // phase-2 epilogue, straight from the accumulators: for each pair of rows (v, v + 1) a
+      // lane computes both of its column's outputs, swaps one with its neighbour lane (DPP
+      // quad_perm [1,0,3,2]), and stores two adjacent columns of one row as 4 bytes -- the even
+      // lane row v, the odd lane row v + 1.  No LDS staging and no barrier before the stores;
+      // the barrier after them keeps the row table until every wavefront has read it.
+      const bool odd = lane & 1;
+      const int64_t colw = (int64_t)ntile * BN + wn * 64 + (l32 & ~1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int vp = 0; vp < 8; ++vp) {
+          const int v0 = 2 * vp;
+          const int r0 = wm * 128 + i * 32 + (v0 >> 2) * 8 + (lane >> 5) * 4 + (v0 & 3);  // even
+          const float w0 = wt_s[r0], w1 = wt_s[r0 + 1];
+          const int r = odd ? r0 + 1 : r0;
+          const int64_t orow = orow_s[r];
+          const bool ok = m0 + r < n;
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const uint32_t y0 = f32_to_bf16(bf16r(acc[i][j][v0]) * w0);
+            const uint32_t y1 = f32_to_bf16(bf16r(acc[i][j][v0 + 1]) * w1);
+            const uint32_t send = odd ? y0 : y1;
+            const uint32_t recv =
+                (uint32_t)__builtin_amdgcn_update_dpp((int)send, (int)send, 0xB1, 0xf, 0xf, false);
+            const uint32_t packed = odd ? (recv | (y1 << 16)) : (y0 | (recv << 16));
+            if (ok)
+              *reinterpret_cast<uint32_t*>(&a.out[orow * a.H + colw + j * 32]) = packed;
+          }
+        }
+      }
+      wg_barrier();
+      continue;
+    }
     __syncthreads();  // all fragment reads done before the staging area is reused
 
-    // epilogue: bf16 tile staged in LDS (in two halves of 128 rows for phase 2), then
-    // 16-byte row stores.  32x32 accumulator layout: column = lane & 31,
-    // row(v) = (v / 4) * 8 + (lane / 32) * 4 + v % 4.
+    // epilogue: bf16 tile staged in LDS, then 16-byte row stores.
     constexpr int OC = MODE == 0 ? 128 : 256;  // output columns of the tile
     constexpr int OLD = OC + 8;
     constexpr int HALVES = MODE == 0 ? 1 : 2;
