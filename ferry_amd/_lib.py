@@ -40,7 +40,8 @@ SIGNATURES = [
     ('ferry_plan_layer', _i64,
      [_i64, _i64, _c_p, _i64, _i64, _c_p, _c_p, _i64, _c_p, _c_p, _c_p, _i64, _c_p, _c_p]),
     ('ferry_plan_fetch', _i64,
-     [_i64, _i64, _c_p, _i64, _i64, _c_p, _c_p, _i64, _c_p, _c_p, _c_p, _i64, _c_p, _c_p, _c_p]),
+     [_i64, _i64, _c_p, _i64, _i64, _c_p, _c_p, _i64, _c_p, _c_p, _c_p, _i64, _c_p, _c_p, _c_p,
+      _c_p]),
     ('ferry_choose_slot', _i64, [_i64, _c_p, _c_p, _i64, _c_p, _c_p, _i64]),
     ('ferry_layer_slots', None, [_c_p, _i64, _i64, _i64, _c_p]),
     ('ferry_h2d_create', ctypes.c_int, [_c_p, _i64, _c_p, _i64, _i64, _i32, ctypes.POINTER(_c_p)]),

@@ -107,14 +107,17 @@ class Controller:
         """plan() from raw host pointers (uint8 routing IDs [tokens*topk], float32 scores [E],
         e.g. the mapped staging buffer) with the misses' copies queued on the fetch engine in
         the same native call.  Returns fetches[m, 3] (a view of a buffer reused by the next
-        call) and the per-rank fetch counts."""
+        call) and the per-rank fetch counts; ``self.demand`` then holds each expert's
+        (token, expert) pair count of the call (int64 [E], reused by the next call)."""
         experts = self.spec.experts
         if self._fetch_buf is None:
             self._fetch_buf = np.empty((experts, 3), np.int64)
+            self.demand = np.zeros(experts, np.int64)
         m = lib().ferry_plan_fetch(event, layer, ids_ptr, tokens, topk, scores_ptr,
                                    self._slots_ptr, int(self.capacities[0]), self._owner_ptr,
                                    self._last_ptr, self._scores_ptr, experts,
-                                   self._fetch_buf.ctypes.data, None, h2d_handle)
+                                   self._fetch_buf.ctypes.data, None, self.demand.ctypes.data,
+                                   h2d_handle)
         if m == -1:
             raise AssertionError(last_error())
         if m == INVALID_ROUTING:

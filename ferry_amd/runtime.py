@@ -188,8 +188,10 @@ class OffloadRuntime:
                                                       scores)
             queue_here = True
         t_plan = time.perf_counter_ns()
-        ids = stage_host.numpy()[4 * E:].astype(np.int64).reshape(T, k)
-        counts_e = np.bincount(ids.reshape(-1), minlength=E)
+        if frequency:
+            counts_e = self.controller.demand.copy()   # counted by the planner in its ID pass
+        else:
+            counts_e = np.bincount(ids.reshape(-1), minlength=E)
         missing_keys = fetches[:, 1] - layer * E
         # copy order: heaviest expert first, so that the compute left after the last copy is
         # the lightest (the planner's slot choices do not depend on the order of the copies)

@@ -249,7 +249,9 @@ int ferry_h2d_set_kernel_stream(ferry_h2d* h, void* stream);
  * ferry/policy.py:130-194, then H2DEngine.fetch of ferry/h2d.py / expert_ops.cpp:94-142).
  * ids are the routing IDs as uint8 [tokens*topk] and gate_scores the layer's float32 scores,
  * e.g. straight from the mapped staging buffer that ferry_history_update writes; the other
- * arguments are those of ferry_plan_layer, plus the fetch engine (nullable: plan only).
+ * arguments are those of ferry_plan_layer, plus demand_out (nullable: int64 [experts], each
+ * expert's (token, expert) pair count in this call, as the planner counts them anyway) and the
+ * fetch engine (nullable: plan only).
  * Returns the number of misses m (fetches_out rows as in ferry_plan_layer, their copies queued),
  * -1 when the misses exceed the admission capacity, -2 when the fetch fails, -3 when an ID is
  * outside [0, E) (0xFF from ferry_history_update) or repeated within a token; errors set
@@ -258,7 +260,8 @@ int ferry_h2d_set_kernel_stream(ferry_h2d* h, void* stream);
 int64_t ferry_plan_fetch(int64_t event, int64_t layer, const uint8_t* ids, int64_t tokens,
                          int64_t topk, const float* gate_scores, int64_t* slots, int64_t cap,
                          int64_t* owner, int64_t* last, float* scores, int64_t experts,
-                         int64_t* fetches_out, int64_t* destinations_out, ferry_h2d* h2d);
+                         int64_t* fetches_out, int64_t* destinations_out, int64_t* demand_out,
+                         ferry_h2d* h2d);
 
 #ifdef __cplusplus
 }
