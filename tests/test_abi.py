@@ -124,7 +124,8 @@ def test_product_planner_golden_trace():
 
 def test_fused_plan_fetch_matches_oracle_traces():
     """ferry_plan_fetch (uint8 IDs and float32 scores from raw host pointers, plan only when no
-    fetch engine is given) makes the oracle's decisions and state updates."""
+    fetch engine is given) makes the oracle's decisions and state updates, and returns each
+    expert's demand."""
     from ferry_amd.policy import Controller
     from ferry_amd.quota import Topology
     rng = np.random.default_rng(7)
@@ -152,6 +153,7 @@ def test_fused_plan_fetch_matches_oracle_traces():
             if f is None:
                 break
             assert np.array_equal(f, f_ref) and counts.tolist() == [len(f)]
+            assert np.array_equal(ctl.demand, np.bincount(sel.reshape(-1), minlength=E))
             assert np.array_equal(ctl.slots[0], ref.slots)
             assert np.array_equal(ctl.owner, ref.owner) and np.array_equal(ctl.last, ref.last)
 
