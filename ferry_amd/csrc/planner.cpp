@@ -11,6 +11,7 @@
 // sort of the slots (the same choices, see plan_core).  The call's routing IDs are scanned
 // once, which validates them and counts each expert's demand (returned by ferry_plan_fetch).
 #include <algorithm>
+#include <cmath>
 #include <cstdint>
 #include <cstring>
 #include <vector>
@@ -126,10 +127,18 @@ int64_t plan_core(int64_t event, int64_t layer, const T* ids, int64_t tokens, in
       ++empties;
     }
   if (empties < m) {
+    // a key whose score is NaN never compares below the running best, so the scan never
+    // picks its slot: such slots are no candidates
     for (int64_t i = 0; i < cap; ++i) {
       const int64_t key = slots[i];
-      if (key >= 0 && !(key / experts == layer && active[(size_t)(key % experts)]))
+      if (key >= 0 && !(key / experts == layer && active[(size_t)(key % experts)]) &&
+          !std::isnan(scores[key]))
         order.push_back(i);
+    }
+    if ((int64_t)order.size() < m) {
+      ferry::set_error("no evictable cache slot for key %lld",
+                       (long long)(base + misses[order.size()]));
+      return -1;
     }
     auto before = [&](int64_t a, int64_t b) {
       const int64_t ka = slots[a], kb = slots[b];

@@ -158,6 +158,43 @@ def test_fused_plan_fetch_matches_oracle_traces():
             assert np.array_equal(ctl.owner, ref.owner) and np.array_equal(ctl.last, ref.last)
 
 
+def test_planner_nan_scores_match_oracle():
+    """Keys whose layer score is NaN are never evicted (every comparison with NaN is false in
+    the reference's scan); the planner's one-sort slot choice matches the oracle's per-miss
+    scan on traces with NaN scores, including the calls where no slot is left."""
+    from ferry_amd.policy import Controller
+    from ferry_amd.quota import Topology
+    rng = np.random.default_rng(7)
+    errors = 0
+    for trial in range(40):
+        L, E = int(rng.integers(1, 5)), int(rng.integers(2, 40))
+        cap = int(rng.integers(1, 2 * E))
+        ctl = Controller(_Spec(L, E), [cap], 'ferry', Topology.uniform(1, E))
+        ref = PlannerRef(L, E, cap)
+        for ev in range(40):
+            layer = int(rng.integers(0, L))
+            k = int(rng.integers(1, min(E, 6) + 1))
+            T = int(rng.integers(1, 6))
+            sel = np.stack([rng.choice(E, k, replace=False) for _ in range(T)])
+            gs = (rng.integers(0, 4, E) / 4).astype(np.float32)
+            gs[rng.random(E) < 0.3] = np.nan
+            try:
+                f_ref, _ = ref.plan(ev, layer, sel, gs)
+            except AssertionError:
+                f_ref = None
+            ids = np.ascontiguousarray(sel.reshape(-1).astype(np.uint8))
+            try:
+                f, _ = ctl.plan_fetch(ev, layer, ids.ctypes.data, T, k, gs.ctypes.data, None)
+            except AssertionError:
+                f = None
+            assert (f is None) == (f_ref is None), (trial, ev)
+            if f is None:
+                errors += 1
+                break
+            assert np.array_equal(f, f_ref) and np.array_equal(ctl.slots[0], ref.slots)
+    assert errors > 0
+
+
 def test_product_planner_overflow_raises_assertion():
     from ferry_amd.policy import Controller
     from ferry_amd.quota import Topology
