@@ -2,8 +2,8 @@
 //
 // Reference: ferry/csrc/expert_ops.cpp:94-142 (H2DEngine).  The copies of a fetch call wait (on
 // the copy streams, GPU-side) for the last compute that read any of the call's slots (the
-// "used" events of mark_used); events that have already fired when the call is made add no
-// wait.  After the call's copies every lane records one event, which becomes the copy-done
+// "used" events of mark_used) and for earlier copies into those slots that are still in
+// flight; events that have already fired when the call is made add no wait.  After the call's copies every lane records one event, which becomes the copy-done
 // event of each slot of the call.  Besides the reference's host wait (wait_host), wait_stream
 // makes a compute stream wait for the copies on the GPU, so that experts that are already
 // resident can run while missing ones are still in flight.
@@ -28,6 +28,7 @@
 
 #include <cstdint>
 #include <memory>
+#include <utility>
 #include <vector>
 
 #include "../../include/ferry_amd.h"
@@ -58,12 +59,10 @@ struct ferry_h2d {
   const char* pool_dev = nullptr;     // the pool's device mapping (null: DMA copies only)
   int32_t kind = FERRY_H2D_DMA;
   hipStream_t kernel_stream = nullptr;  // stream of kernel-mode copies (initially stream[0])
-  std::shared_ptr<Event> last_kernel_copy;  // done event of the latest kernel-mode fetch
-  bool dma_since_kernel = false;      // DMA fetches queued since the latest kernel-mode fetch
-  std::shared_ptr<Event> lane_done[kLanes];  // per lane: end of its copies of the last DMA call
-  std::vector<int64_t> batch_of;      // per slot: last kernel-mode launch batch that wrote it
+  // per stream that kernel-mode copies have used: the done event of its latest copy launch
+  std::vector<std::pair<hipStream_t, std::shared_ptr<Event>>> kernel_last;
+  std::vector<int64_t> batch_of;      // per slot: last batch of rows that wrote it (one call)
   int64_t batch = 0;
-  hipStream_t last_kernel_stream = nullptr;  // stream of the latest kernel-mode fetch
   int64_t cache_rows = 0, pool_rows = 0, row_bytes = 0;
   int64_t part[kLanes + 1] = {};      // byte boundaries of the row parts
   int32_t device = 0;
@@ -123,7 +122,6 @@ extern "C" int ferry_h2d_create(void* cache, int64_t cache_rows, const void* poo
   }
   H2D_HIP(hipEventCreateWithFlags(&h->join, hipEventDisableTiming));
   h->kernel_stream = h->stream[0];
-  h->last_kernel_stream = h->stream[0];
   h->copy_seq.assign((size_t)cache_rows, -1);
   h->batch_of.assign((size_t)cache_rows, 0);
   h->used.assign((size_t)cache_rows, nullptr);
@@ -136,6 +134,7 @@ extern "C" int ferry_h2d_destroy(ferry_h2d* h) {
   if (!h) return 0;
   for (int l = 0; l < kLanes; ++l)
     if (h->stream[l]) (void)hipStreamSynchronize(h->stream[l]);
+  for (auto& kl : h->kernel_last) (void)hipEventSynchronize(kl.second->e);
   for (int l = 0; l < kLanes; ++l) h->copy_done[l].clear();
   if (h->join) (void)hipEventDestroy(h->join);
   h->used.clear();
@@ -149,8 +148,25 @@ extern "C" int ferry_h2d_fetch(ferry_h2d* h, const int64_t* slots, const int64_t
                                int64_t n) {
   ferry::clear_error();
   if (n <= 0) return 0;
-  // the reads of the slots about to be overwritten that may still be running
-  std::vector<hipEvent_t> pending;
+  // What a copy into a slot must follow: the last compute that read the slot (WAR) and any
+  // earlier copy into it still in flight, on whichever lane or stream (WAW).  Events that have
+  // fired when the call is made add no wait.
+  std::vector<hipEvent_t> pending, checked;
+  auto note = [&](const std::shared_ptr<Event>& ev) -> bool {
+    if (!ev) return true;
+    for (hipEvent_t e : checked)
+      if (e == ev->e) return true;
+    checked.push_back(ev->e);
+    const hipError_t q = hipEventQuery(ev->e);
+    if (q == hipErrorNotReady) {
+      (void)hipGetLastError();  // a pending event is not an error
+      pending.push_back(ev->e);
+    } else if (q != hipSuccess) {
+      ferry::set_error("hipEventQuery failed: %s", hipGetErrorString(q));
+      return false;
+    }
+    return true;
+  };
   for (int64_t i = 0; i < n; ++i) {
     const int64_t slot = slots[i], key = keys[i];
     if (slot < 0 || slot >= h->cache_rows || key < 0 || key >= h->pool_rows) {
@@ -158,33 +174,13 @@ extern "C" int ferry_h2d_fetch(ferry_h2d* h, const int64_t* slots, const int64_t
                        (long long)key);
       return 2;
     }
-    const auto& u = h->used[(size_t)slot];
-    if (!u) continue;
-    bool seen = false;
-    for (hipEvent_t e : pending) seen = seen || e == u->e;
-    if (seen) continue;
-    const hipError_t q = hipEventQuery(u->e);
-    if (q == hipErrorNotReady) {
-      (void)hipGetLastError();  // a pending event is not an error
-      pending.push_back(u->e);
-    } else if (q != hipSuccess) {
-      ferry::set_error("hipEventQuery failed: %s", hipGetErrorString(q));
-      return 3;
-    }
+    if (!note(h->used[(size_t)slot])) return 3;
+    for (int l = 0; l < kLanes; ++l)
+      if (!note(h->copy_done[l][(size_t)slot])) return 3;
   }
   if (h->kind == FERRY_H2D_KERNEL) {
     hipStream_t s = h->kernel_stream;
     for (hipEvent_t e : pending) H2D_HIP(hipStreamWaitEvent(s, e, 0));
-    // copies queued earlier on the DMA lanes, into any slot, end before this launch starts
-    if (s != h->stream[0] && h->dma_since_kernel) {
-      H2D_HIP(hipEventRecord(h->join, h->stream[0]));
-      H2D_HIP(hipStreamWaitEvent(s, h->join, 0));
-    }
-    // and so do kernel-mode copies queued on another stream
-    if (h->last_kernel_copy && s != h->last_kernel_stream)
-      H2D_HIP(hipStreamWaitEvent(s, h->last_kernel_copy->e, 0));
-    h->dma_since_kernel = false;
-    h->last_kernel_stream = s;
     // rows of one launch run concurrently: a slot named twice in the call starts a new
     // launch, so that the later row wins, as with copies in stream order
     int64_t b0 = 0;
@@ -207,32 +203,19 @@ extern "C" int ferry_h2d_fetch(ferry_h2d* h, const int64_t* slots, const int64_t
     H2D_HIP(hipEventRecord(ev->e, s));
     for (int l = 0; l < kLanes; ++l)
       for (int64_t i = 0; i < n; ++i) h->copy_done[l][(size_t)slots[i]] = ev;
-    h->last_kernel_copy = ev;
+    bool known = false;
+    for (auto& kl : h->kernel_last)
+      if (kl.first == s) {
+        kl.second = ev;
+        known = true;
+      }
+    if (!known) h->kernel_last.emplace_back(s, ev);
     for (int64_t i = 0; i < n; ++i) h->copy_seq[(size_t)slots[i]] = h->seq++;
     h->copies += n;
     return 0;
   }
-  // kernel-mode copies queued on another stream end before these copies start
-  if (h->last_kernel_copy && !h->dma_since_kernel)
-    for (int l = 0; l < kLanes; ++l)
-      H2D_HIP(hipStreamWaitEvent(h->stream[l], h->last_kernel_copy->e, 0));
-  h->dma_since_kernel = true;
-  // Each lane starts after the other lanes' copies of earlier calls (a slot's bytes can move to
-  // another lane from one call to the next).  Those have usually finished by now, and then no
-  // wait is queued: a lane waiting on an event that another DMA queue records starts tens of
-  // microseconds late even when nothing is pending.
-  for (int m = 0; m < kLanes; ++m) {
-    if (!h->lane_done[m]) continue;
-    const hipError_t q = hipEventQuery(h->lane_done[m]->e);
-    if (q == hipSuccess) continue;
-    if (q != hipErrorNotReady) {
-      ferry::set_error("hipEventQuery failed: %s", hipGetErrorString(q));
-      return 3;
-    }
-    (void)hipGetLastError();
-    for (int l = 0; l < kLanes; ++l)
-      if (l != m) H2D_HIP(hipStreamWaitEvent(h->stream[l], h->lane_done[m]->e, 0));
-  }
+  // No unconditional cross-lane wait: a lane waiting on an event that another DMA queue
+  // records starts tens of microseconds late even when nothing is pending.
   for (int l = 0; l < kLanes; ++l)
     for (hipEvent_t e : pending) H2D_HIP(hipStreamWaitEvent(h->stream[l], e, 0));
   // The call's rows, concatenated, are cut into kLanes equal byte ranges, one per lane: a lane
@@ -273,7 +256,6 @@ extern "C" int ferry_h2d_fetch(ferry_h2d* h, const int64_t* slots, const int64_t
     H2D_HIP(hipEventCreateWithFlags(&ev->e, hipEventDisableTiming));
     H2D_HIP(hipEventRecord(ev->e, h->stream[l]));
     for (int64_t i = 0; i < n; ++i) h->copy_done[l][(size_t)slots[i]] = ev;
-    h->lane_done[l] = ev;
   }
   for (int64_t i = 0; i < n; ++i) h->copy_seq[(size_t)slots[i]] = h->seq++;
   h->copies += n;
@@ -302,23 +284,32 @@ extern "C" int ferry_h2d_wait_host(ferry_h2d* h, const int64_t* slots, int64_t n
 extern "C" int ferry_h2d_wait_stream(ferry_h2d* h, const int64_t* slots, int64_t n,
                                      void* stream) {
   ferry::clear_error();
-  // copies complete in issue order on each lane: waiting for the most recently issued copy
-  // among the slots, on every lane, covers all of them
-  int64_t best = -1, best_seq = -1;
+  // every still-running copy into the slots, each event once (copies into different slots
+  // are not ordered with each other: DMA lanes, kernel-mode streams)
+  std::vector<hipEvent_t> seen;
   for (int64_t i = 0; i < n; ++i) {
     const int64_t slot = slots[i];
     if (slot < 0 || slot >= h->cache_rows) {
       ferry::set_error("h2d_wait_stream: slot %lld out of range", (long long)slot);
       return 2;
     }
-    if (h->copy_seq[(size_t)slot] > best_seq) {
-      best_seq = h->copy_seq[(size_t)slot];
-      best = slot;
+    if (h->copy_seq[(size_t)slot] < 0) continue;
+    for (int l = 0; l < kLanes; ++l) {
+      const hipEvent_t e = h->copy_done[l][(size_t)slot]->e;
+      bool dup = false;
+      for (hipEvent_t x : seen) dup = dup || x == e;
+      if (dup) continue;
+      seen.push_back(e);
+      const hipError_t q = hipEventQuery(e);
+      if (q == hipSuccess) continue;
+      if (q != hipErrorNotReady) {
+        ferry::set_error("hipEventQuery failed: %s", hipGetErrorString(q));
+        return 3;
+      }
+      (void)hipGetLastError();
+      H2D_HIP(hipStreamWaitEvent((hipStream_t)stream, e, 0));
     }
   }
-  if (best >= 0)
-    for (int l = 0; l < kLanes; ++l)
-      H2D_HIP(hipStreamWaitEvent((hipStream_t)stream, h->copy_done[l][(size_t)best]->e, 0));
   return 0;
 }
 
@@ -342,7 +333,7 @@ extern "C" int ferry_h2d_mark_used(ferry_h2d* h, const int64_t* slots, int64_t n
 extern "C" int ferry_h2d_synchronize(ferry_h2d* h) {
   ferry::clear_error();
   for (int l = 0; l < kLanes; ++l) H2D_HIP(hipStreamSynchronize(h->stream[l]));
-  if (h->last_kernel_copy) H2D_HIP(hipEventSynchronize(h->last_kernel_copy->e));
+  for (auto& kl : h->kernel_last) H2D_HIP(hipEventSynchronize(kl.second->e));
   return 0;
 }
 
@@ -359,9 +350,7 @@ extern "C" int ferry_h2d_set_engine(ferry_h2d* h, int32_t kind) {
                      "aligned rows");
     return 2;
   }
-  // no wait: every fetch is ordered after the copies of the other kind already queued (the
-  // DMA lanes fork from stream[0] after the latest kernel-mode copy; kernel-mode copies wait
-  // for stream[0], into which the lanes join)
+  // no wait: every fetch follows the earlier copies into its slots, of either kind
   h->kind = kind;
   return 0;
 }

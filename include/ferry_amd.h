@@ -230,8 +230,8 @@ void* ferry_h2d_stream(ferry_h2d* h);
  * each taking half of the call's bytes.  FERRY_H2D_KERNEL: one launch of a copy kernel per
  * fetch call that reads the pool through its device mapping (possible when the pool has one
  * and rows are 16-byte multiples).
- * Both write the same bytes, and every fetch is ordered after the copies of either kind that
- * the engine queued before it.  ferry_h2d_set_kernel_stream picks the stream that kernel-mode
+ * Both write the same bytes, and a copy into a slot is ordered after the earlier copies into
+ * that slot, of either kind, that are still in flight.  ferry_h2d_set_kernel_stream picks the stream that kernel-mode
  * copies run on (initially the engine's own, ferry_h2d_stream; null is HIP's null stream):
  * with the caller's compute stream, the
  * kernels that read the fetched rows follow the copy on one queue, with no cross-queue wait.

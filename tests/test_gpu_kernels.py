@@ -472,6 +472,46 @@ def test_h2d_kernel_copy_on_caller_stream(device):
     eng.close()
 
 
+def test_h2d_copy_order_across_modes(device):
+    """A copy into a slot follows the earlier copies into that slot whatever their kind (DMA
+    lanes, copy kernel on the engine's stream or on a caller's stream); wait_stream covers every
+    still-running copy into the listed slots, of either kind."""
+    from ferry_amd import h2d
+    from ferry_amd.h2d import H2DEngine
+    rows, cap, width = 8, 4, 4 << 20          # 8 MiB rows: copies long enough to overlap
+    g = torch.Generator().manual_seed(11)
+    pool = torch.randint(-30000, 30000, (rows, width), generator=g, dtype=torch.int16)
+    pool = pool.view(torch.bfloat16).pin_memory()
+    cache = torch.zeros((cap, width), dtype=torch.bfloat16, device=device)
+    eng = H2DEngine(cache, pool)
+    side = torch.cuda.Stream()
+    bits = lambda t: t.view(torch.int16)   # noqa: E731
+    for rep in range(3):
+        # write after write into slot 0: DMA, then the kernel on a side stream, then DMA
+        eng.engine = h2d.DMA
+        eng.fetch([0, 1], [1, 2])
+        eng.engine = h2d.KERNEL
+        eng.set_kernel_stream(side)
+        eng.fetch([0, 2], [3, 4])
+        eng.engine = h2d.DMA
+        eng.fetch([3], [5])
+        eng.engine = h2d.KERNEL
+        eng.set_kernel_stream(None)
+        eng.fetch([3], [6])
+        # a consumer stream waits for slots filled by both kinds
+        consumer = torch.cuda.Stream()
+        eng.wait_stream([0, 1, 2, 3], consumer)
+        with torch.cuda.stream(consumer):
+            snap = cache.clone()
+        torch.cuda.synchronize()
+        want = pool[[3, 2, 4, 6]]
+        assert torch.equal(bits(snap.cpu()), bits(want)), rep
+        eng.synchronize()
+        cache.zero_()
+        torch.cuda.synchronize()
+    eng.close()
+
+
 def test_h2d_kernel_copy_many_rows_and_ragged_widths(device):
     """The copy kernel against the DMA path: a fetch of more rows than one launch takes (300, in
     any slot order), row sizes that are and are not multiples of its 16-byte unit (the latter
