@@ -3,11 +3,15 @@
 Headline (``value``): the Qwen3-30B-A3B-shaped MoE layer in decode -- 16 tokens per step, 128
 experts top-8 (renormalised softmax), hidden 2048, SwiGLU intermediate 768, bf16, a 38-slot
 expert cache with the other experts in pinned host memory, router logits N(0, 1) + log
-Zipf(1.1) popularity (seed 1).  One step = one layer call: router kernel -> device history +
-routing IDs to the host -> host planner -> H2D fetch of the misses -> layout -> grouped SwiGLU
-(resident experts first) -> combine.  The timed pass runs without instrumentation; a second
-pass over the same stream (from an empty cache again) collects per-launch kernel times, fetch
-events and host phase times.
+Zipf(1.1) popularity (seed 1), expert weights N(0, 0.02) bf16.  One step = one layer call:
+router kernel -> device history + routing IDs to the host -> host planner -> H2D fetch of the
+misses -> layout -> grouped SwiGLU (resident experts first) -> combine.  The fetch copies the
+misses as packed rows (OffloadRuntime(pack=True): per value a sign|mantissa byte and a 4-bit
+exponent code, lossless, 1.33x fewer bytes over the host link) with hipMemcpyAsync on two DMA
+streams, and a kernel unpacks them into the cache slots; the outputs are bit-identical to raw
+fetches.  The timed pass runs without instrumentation; a second pass over the same stream
+(from an empty cache again) collects per-launch kernel times, fetch events and host phase
+times.
 
 Also on the line:
   * roofline: the decode FFN kernel (ffn_skinny_fused: gate/up + SwiGLU + down in one launch),
@@ -21,9 +25,13 @@ Also on the line:
   * prefill_stack / prefill_stack_deepseek: those layers over the whole stack (48 / 26 layers,
     distinct seeded weights and routing per layer) through OffloadRuntime with the pooled 30 %
     cache (1,843 / 499 slots) from cold, so every layer fetches its missing experts over PCIe;
+    packed fetches, with the raw-row run under ``raw``;
   * decode_loop: the 48-layer Qwen3 decode loop (1024-token prefill, then 64-token steps,
     pooled cache of 1,843, W = 128 eviction), ``--loop-steps`` steps (default 8, bounded);
-  * decode_copy_kernel: the headline stream through OffloadRuntime(copy='kernel'): the misses
+    packed fetches, with the raw-row run under ``raw``;
+  * decode_raw: the headline stream with raw rows over the host link (OffloadRuntime(pack=
+    False), the reference's transfer format);
+  * decode_copy_kernel: the headline stream through OffloadRuntime(copy='kernel'): raw misses
     copied by one kernel launch on the compute stream, then one FFN launch (no overlap);
   * cpu_baseline: the reference's op order in torch on the host cores (all cores of the
     process's affinity), median of >= 5 repeats on the decode stream, plus one config-3 prefill
@@ -47,6 +55,7 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 PCIE_PEAK_GBS = 64.0
+PACK_THREADS = 16   # host threads that pack a pool (the box's CPU share)
 
 TILED_TRAFFIC_PROFILE = ROOT / 'profiles' / 'ffn_tiled_prefill_qwen3_t8192_hbm_traffic.md'
 FUSED_TRAFFIC_PROFILE = ROOT / 'profiles' / 'ffn_skinny_fused_decode_qwen3_t16_hbm_traffic.md'
@@ -84,6 +93,54 @@ def parse():
     return p.parse_args()
 
 
+def run_stacks(args, device):
+    """The two prefill stacks and the decode loop, each with packed fetches and with raw rows.
+    Pinned host memory is limited (about a quarter of RAM), so the raw runs use a pinned pool
+    that is freed before the same seeded pool is rebuilt in pageable memory, packed (the
+    packed copy is pinned) and freed again."""
+    import gc
+
+    from ferry_amd import workloads
+    from ferry_amd.h2d import PackedPool
+    out = {}
+    for cfg in (3, 4):
+        w = workloads.CONFIGS[cfg]
+        layers = w.layers if cfg == 4 else 48
+        t0 = time.perf_counter()
+        pool = workloads.make_pool(w.spec, layers, seed=w.seed)
+        pool_s = time.perf_counter() - t0
+        raw = raw_summary(run_prefill_stack(device, cfg, pool))
+        if cfg == 3:
+            loop_raw = raw_summary(run_decode_loop(device, args.loop_steps, pool))
+        del pool
+        gc.collect()
+        src = workloads.make_pool(w.spec, layers, seed=w.seed, pinned=False)
+        t0 = time.perf_counter()
+        packed = PackedPool(src, PACK_THREADS)
+        pack_s = time.perf_counter() - t0
+        del src
+        gc.collect()
+        key = 'prefill_stack' if cfg == 3 else 'prefill_stack_deepseek'
+        out[key] = run_prefill_stack(device, cfg, packed)
+        out[key].update(pool_build_s=pool_s, pack_s=pack_s, pack_ratio=packed.ratio, raw=raw)
+        print(f'# {key} done', file=sys.stderr, flush=True)
+        if cfg == 3:
+            out['decode_loop'] = run_decode_loop(device, args.loop_steps, packed)
+            out['decode_loop']['raw'] = loop_raw
+            print('# decode loop done', file=sys.stderr, flush=True)
+        packed.close()
+        del packed
+        gc.collect()
+    return out
+
+
+def raw_summary(block):
+    """The throughput fields of a stack / loop block run with raw rows over the host link."""
+    keys = ('tokens_per_s', 'decode_tokens_per_s', 'stack_ms', 'decode_ms_per_layer_step',
+            'h2d_gbs', 'fetch_hidden_frac')
+    return {k: block[k] for k in keys if k in block}
+
+
 def launch_stats(ops, name):
     n, ms = ops.timing_summary(name)
     return dict(launches=n, total_ms=ms, avg_us=ms / n * 1e3 if n else None)
@@ -108,7 +165,7 @@ def decode_stream(w, steps, device):
     return out
 
 
-def run_decode(args, device, copy='dma'):
+def run_decode(args, device, copy='dma', pack=False):
     from ferry_amd import expert_ops as ops
     from ferry_amd import workloads
     from ferry_amd.quota import Topology
@@ -117,7 +174,12 @@ def run_decode(args, device, copy='dma'):
     spec = w.spec
     pool = workloads.make_pool(spec, 1, seed=0)
     rt = OffloadRuntime(spec, pool, [w.cache_slots], 'ferry', Topology.uniform(1, spec.experts),
-                        copy=copy)
+                        copy=copy, pack=pack)
+    packing = None
+    if rt.packed is not None:
+        packing = dict(ratio=rt.packed.ratio, packed_rows=rt.packed.packed_rows,
+                       packed_bytes=rt.packed.packed_bytes,
+                       row_bytes=spec.expert_bytes)
     stream = decode_stream(w, args.warmup + args.steps, device)
 
     def step(lg, x):
@@ -156,7 +218,7 @@ def run_decode(args, device, copy='dma'):
     fetch_ms, exposed_ms, overlap_ms = rt.fetch_timing()   # reads the launch log: before disabling
     ops.timing_enable(False)
     res = dict(workload=w, elapsed=t1 - t0, instrumented_elapsed=t3 - t2,
-               critical=rt.critical_path_timing(),
+               critical=rt.critical_path_timing(), packing=packing,
                sync_timeouts=ops.ffn_sync_timeouts(),
                tokens=w.tokens * args.steps, copies=copies, kernels=ks, fetch_ms=fetch_ms,
                exposed_ms=exposed_ms, overlap_ms=overlap_ms, expert_bytes=spec.expert_bytes,
@@ -544,9 +606,18 @@ def main():
         torch.bitwise_not(src, out=dst)       # reads n*4 bytes, writes n*4 bytes
         torch.cuda.synchronize()
         del src, dst
-    dec = run_decode(args, device)
+    dec = run_decode(args, device, pack=True)
     w = dec['workload']
     roofline, block = decode_block(dec, args)
+    pk = dec['packing']
+    block['packing'] = dict(
+        ratio=pk['ratio'], packed_rows=pk['packed_rows'],
+        link_gbs=(dec['copies'] * pk['packed_bytes'] / pk['packed_rows'])
+        / (dec['fetch_ms'] * 1e-3) / 1e9 if dec['fetch_ms'] else None,
+        note='the misses cross the host link as packed rows (per value a sign|mantissa byte and '
+             'a 4-bit exponent code, lossless) into staging buffers and are unpacked into the '
+             'cache slots on the GPU; h2d_gbs counts expert bytes delivered, link_gbs the '
+             'packed bytes copied')
     line = dict(
         metric='MoE-layer tokens/sec (Qwen3-30B-A3B-shaped decode layer, 16 tok/step, 38/128 cached)',
         value=dec['tokens'] / dec['elapsed'], unit='tokens/s', n_gpus=1, steps=args.steps,
@@ -555,6 +626,8 @@ def main():
         config=dict(workload=w.name, tokens_per_step=w.tokens, experts=w.spec.experts,
                     topk=w.spec.topk, hidden=w.spec.hidden, intermediate=w.spec.intermediate,
                     cache_slots=w.cache_slots, router='N(0,1)+log Zipf(1.1), seed 1',
+                    expert_weights='N(0, 0.02) bf16, seeded',
+                    fetch='hipMemcpyAsync of packed rows on two DMA streams, unpacked on the GPU',
                     parallelism='single GPU (one expert-parallel share)'),
         roofline=roofline, decode=block)
     print(f'# decode done: {line["value"]:.0f} tokens/s', file=sys.stderr, flush=True)
@@ -572,27 +645,23 @@ def main():
              'stream, then every active expert runs in one FFN launch (no overlap)')
     print(f'# decode (copy kernel) done: {line["decode_copy_kernel"]["tokens_per_s"]:.0f} tokens/s',
           file=sys.stderr, flush=True)
+    # the same decode stream fetching raw rows, as the reference's engine does
+    dr = run_decode(args, device, pack=False)
+    rr, br = decode_block(dr, args)
+    line['decode_raw'] = dict(
+        tokens_per_s=dr['tokens'] / dr['elapsed'], ms_per_step=dr['elapsed'] / args.steps * 1e3,
+        h2d_gbs=br['h2d_gbs'], fetch_ms_per_step=br['fetch_ms_per_step'],
+        fetch_hidden_frac=br['fetch_hidden_frac'], ffn_frac=rr['frac'],
+        note='OffloadRuntime(pack=False): raw bf16 rows over the host link')
+    print(f'# decode (raw rows) done: {line["decode_raw"]["tokens_per_s"]:.0f} tokens/s',
+          file=sys.stderr, flush=True)
     if not args.no_prefill:
         line['prefill'] = run_prefill(args, device, 3)
         line['roofline_prefill'] = prefill_roofline(line['prefill'])
         line['prefill_deepseek'] = run_prefill(args, device, 4)
         print('# prefill layers done', file=sys.stderr, flush=True)
     if not args.no_stacks:
-        from ferry_amd import workloads
-        t0 = time.perf_counter()
-        pool = workloads.make_pool(workloads.CONFIGS[3].spec, 48, seed=workloads.CONFIGS[3].seed)
-        pool_s = time.perf_counter() - t0
-        line['prefill_stack'] = run_prefill_stack(device, 3, pool)
-        line['prefill_stack']['pool_build_s'] = pool_s
-        print('# qwen3 prefill stack done', file=sys.stderr, flush=True)
-        line['decode_loop'] = run_decode_loop(device, args.loop_steps, pool)
-        print('# decode loop done', file=sys.stderr, flush=True)
-        del pool
-        w4 = workloads.CONFIGS[4]
-        pool = workloads.make_pool(w4.spec, w4.layers, seed=w4.seed)
-        line['prefill_stack_deepseek'] = run_prefill_stack(device, 4, pool)
-        del pool
-        print('# deepseek prefill stack done', file=sys.stderr, flush=True)
+        line.update(run_stacks(args, device))
     if not args.no_cpu_baseline:
         line['cpu_baseline'] = cpu_baseline(dec, args.cpu_seconds, device,
                                             with_prefill=not args.no_prefill)

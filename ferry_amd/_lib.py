@@ -56,6 +56,12 @@ SIGNATURES = [
     ('ferry_h2d_set_engine', ctypes.c_int, [_c_p, _i32]),
     ('ferry_h2d_engine', _i32, [_c_p]),
     ('ferry_h2d_set_kernel_stream', ctypes.c_int, [_c_p, _c_p]),
+    ('ferry_pack_pool', ctypes.c_int, [_c_p, _i64, _i64, _i32, ctypes.POINTER(_c_p)]),
+    ('ferry_packed_pool_stats', ctypes.c_int, [_c_p, _c_p, _c_p]),
+    ('ferry_packed_pool_destroy', ctypes.c_int, [_c_p]),
+    ('ferry_h2d_use_packed', ctypes.c_int, [_c_p, _c_p, _i64]),
+    ('ferry_h2d_create_packed', ctypes.c_int, [_c_p, _i64, _c_p, _i32, _i64, ctypes.POINTER(_c_p)]),
+    ('ferry_pack_row', ctypes.c_int, [_c_p, _i64, _c_p, _i64, _c_p]),
     ('ferry_timing_enable', ctypes.c_int, [_i32]),
     ('ferry_timing_mark', _i64, []),
     ('ferry_timing_range', ctypes.c_int, [_i64, _i64, _c_p]),

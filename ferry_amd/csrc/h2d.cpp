@@ -27,17 +27,25 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <cstring>
 #include <memory>
 #include <utility>
 #include <vector>
 
 #include "../../include/ferry_amd.h"
+#include "pack_format.h"
 
 namespace ferry {
 void set_error(const char* fmt, ...);
 void clear_error();
 hipError_t h2d_copy_launch(const void* pool, void* cache, int64_t row_bytes, const int64_t* keys,
                            const int64_t* slots, int64_t n, hipStream_t stream);
+hipError_t h2d_unpack_launch(const UnpackList& list, int64_t n, hipStream_t stream);
+void pack_plan_rows(const uint16_t* pool, int64_t rows, int64_t n, int threads, uint32_t* base,
+                    int64_t* escapes);
+void pack_write_rows(const uint16_t* pool, int64_t rows, int64_t n, int threads,
+                     const uint32_t* base, const int64_t* escapes, const int64_t* off,
+                     uint8_t* dst);
 }  // namespace ferry
 
 namespace {
@@ -53,6 +61,18 @@ struct Event {
 
 constexpr int kLanes = 2;
 
+// The packed copy of a pool (ferry_pack_pool): pinned host memory holding every row, packed or
+// (when packing would not shrink it) raw, and per row its offset, size and form.  An engine
+// fetches from it alone; the pool it was made from is no longer needed.
+struct ferry_packed_pool {
+  const char* pool = nullptr;         // the pool it was made from (for ferry_h2d_use_packed)
+  int64_t rows = 0, row_bytes = 0;
+  uint8_t* data = nullptr;
+  std::vector<int64_t> off, size;
+  std::vector<uint8_t> raw;           // per row: 1 when stored raw
+  int64_t bytes = 0, packed_rows = 0, packed_bytes = 0, largest = 0;
+};
+
 struct ferry_h2d {
   char* cache = nullptr;
   const char* pool = nullptr;
@@ -63,6 +83,12 @@ struct ferry_h2d {
   std::vector<std::pair<hipStream_t, std::shared_ptr<Event>>> kernel_last;
   std::vector<int64_t> batch_of;      // per slot: last batch of rows that wrote it (one call)
   int64_t batch = 0;
+  // packed pool (ferry_h2d_use_packed): DMA copies move packed rows into device staging
+  // buffers, and an unpack kernel writes the slots
+  const ferry_packed_pool* packed = nullptr;
+  uint8_t* ring = nullptr;            // device staging buffers, ring_rows x entry_bytes
+  int64_t ring_rows = 0, entry_bytes = 0, ring_next = 0;
+  std::vector<std::shared_ptr<Event>> ring_ev;  // per staging buffer: the unpack that read it
   int64_t cache_rows = 0, pool_rows = 0, row_bytes = 0;
   int64_t part[kLanes + 1] = {};      // byte boundaries of the row parts
   int32_t device = 0;
@@ -136,11 +162,108 @@ extern "C" int ferry_h2d_destroy(ferry_h2d* h) {
     if (h->stream[l]) (void)hipStreamSynchronize(h->stream[l]);
   for (auto& kl : h->kernel_last) (void)hipEventSynchronize(kl.second->e);
   for (int l = 0; l < kLanes; ++l) h->copy_done[l].clear();
+  h->ring_ev.clear();
+  if (h->ring) (void)hipFree(h->ring);
   if (h->join) (void)hipEventDestroy(h->join);
   h->used.clear();
   for (int l = 0; l < kLanes; ++l)
     if (h->stream[l]) (void)hipStreamDestroy(h->stream[l]);
   delete h;
+  return 0;
+}
+
+// DMA fetch on a packed pool: the packed rows are copied into device staging buffers and one
+// unpack launch per batch (at most kUnpackRows packed rows, at most one per staging buffer)
+// writes their slots; rows that stayed raw are copied straight into their slots.  The batch's
+// bytes, concatenated, are cut into kLanes equal ranges; the lanes join into the first stream,
+// which runs the unpack, and every slot of the batch is ready at the event after it.
+static int fetch_packed(ferry_h2d* h, const int64_t* slots, const int64_t* keys, int64_t n) {
+  struct Seg {
+    const char* src;
+    char* dst;
+    int64_t bytes;
+  };
+  const int64_t rb = h->row_bytes;
+  const ferry_packed_pool* pp = h->packed;
+  const int64_t per_batch = h->ring_rows < ferry::kUnpackRows ? h->ring_rows : ferry::kUnpackRows;
+  int64_t i0 = 0;
+  while (i0 < n) {
+    std::vector<Seg> segs;
+    ferry::UnpackList ul;
+    ul.n_rows = 0;
+    std::vector<int64_t> entries;
+    int64_t i1 = i0;
+    ++h->batch;   // a slot named twice starts a new batch, so that the later row wins
+    for (; i1 < n; ++i1) {
+      const int64_t key = keys[i1];
+      if (h->batch_of[(size_t)slots[i1]] == h->batch) break;
+      char* slot_ptr = h->cache + slots[i1] * rb;
+      const char* src = (const char*)pp->data + pp->off[(size_t)key];
+      if (pp->raw[(size_t)key]) {
+        h->batch_of[(size_t)slots[i1]] = h->batch;
+        segs.push_back({src, slot_ptr, rb});
+        continue;
+      }
+      if (ul.n_rows == per_batch) break;
+      h->batch_of[(size_t)slots[i1]] = h->batch;
+      const int64_t k = h->ring_next;
+      h->ring_next = (k + 1) % h->ring_rows;
+      char* st = (char*)h->ring + k * h->entry_bytes;
+      segs.push_back({src, st, pp->size[(size_t)key]});
+      ul.src[ul.n_rows] = (const uint8_t*)st;
+      ul.dst[ul.n_rows] = (uint16_t*)slot_ptr;
+      ++ul.n_rows;
+      entries.push_back(k);
+    }
+    // a staging buffer is rewritten only after the unpack that last read it
+    std::vector<hipEvent_t> waited;
+    for (int64_t k : entries) {
+      const auto& ev = h->ring_ev[(size_t)k];
+      if (!ev) continue;
+      bool dup = false;
+      for (hipEvent_t x : waited) dup = dup || x == ev->e;
+      if (dup) continue;
+      waited.push_back(ev->e);
+      const hipError_t q = hipEventQuery(ev->e);
+      if (q == hipSuccess) continue;
+      if (q != hipErrorNotReady) {
+        ferry::set_error("hipEventQuery failed: %s", hipGetErrorString(q));
+        return 3;
+      }
+      (void)hipGetLastError();
+      for (int l = 0; l < kLanes; ++l) H2D_HIP(hipStreamWaitEvent(h->stream[l], ev->e, 0));
+    }
+    int64_t total = 0;
+    for (const Seg& sg : segs) total += sg.bytes;
+    for (int l = 0; l < kLanes; ++l) {
+      const int64_t lo = l == 0 ? 0 : total * l / kLanes / 256 * 256;
+      const int64_t hi = l + 1 == kLanes ? total : total * (l + 1) / kLanes / 256 * 256;
+      int64_t at = 0;
+      for (const Seg& sg : segs) {
+        const int64_t a = lo > at ? lo : at;
+        const int64_t b = hi < at + sg.bytes ? hi : at + sg.bytes;
+        if (a < b)
+          H2D_HIP(hipMemcpyAsync(sg.dst + (a - at), sg.src + (a - at), (size_t)(b - a),
+                                 hipMemcpyHostToDevice, h->stream[l]));
+        at += sg.bytes;
+      }
+    }
+    for (int l = 1; l < kLanes; ++l) {
+      H2D_HIP(hipEventRecord(h->join, h->stream[l]));
+      H2D_HIP(hipStreamWaitEvent(h->stream[0], h->join, 0));
+    }
+    if (ul.n_rows > 0) H2D_HIP(ferry::h2d_unpack_launch(ul, rb / 2, h->stream[0]));
+    auto ev = std::make_shared<Event>();
+    H2D_HIP(hipEventCreateWithFlags(&ev->e, hipEventDisableTiming));
+    H2D_HIP(hipEventRecord(ev->e, h->stream[0]));
+    for (int64_t i = i0; i < i1; ++i) {
+      for (int l = 0; l < kLanes; ++l) h->copy_done[l][(size_t)slots[i]] = ev;
+      h->copy_seq[(size_t)slots[i]] = h->seq++;
+    }
+    for (int64_t k : entries) h->ring_ev[(size_t)k] = ev;
+    h->copies += i1 - i0;
+    i0 = i1;
+  }
   return 0;
 }
 
@@ -228,6 +351,7 @@ extern "C" int ferry_h2d_fetch(ferry_h2d* h, const int64_t* slots, const int64_t
     h->batch_of[(size_t)slots[i]] = h->batch;
   }
   const int64_t rb = h->row_bytes;
+  if (h->packed) return fetch_packed(h, slots, keys, n);
   if (!repeated) {
     const int64_t total = n * rb;
     for (int l = 0; l < kLanes; ++l) {
@@ -367,4 +491,152 @@ extern "C" int ferry_h2d_set_kernel_stream(ferry_h2d* h, void* stream) {
 
 extern "C" int32_t ferry_h2d_engine(const ferry_h2d* h) { return h ? h->kind : -1; }
 
+extern "C" int ferry_pack_pool(const void* pool, int64_t rows, int64_t row_bytes,
+                               int32_t threads, ferry_packed_pool** out) {
+  ferry::clear_error();
+  if (!out || !pool || rows < 0 || row_bytes <= 0 || row_bytes % 32 != 0 ||
+      row_bytes / 2 >= ((int64_t)1 << 32)) {
+    ferry::set_error("pack_pool: needs rows of a multiple of 16 bf16 values (below 2^32)");
+    return 2;
+  }
+  std::unique_ptr<ferry_packed_pool> pp(new ferry_packed_pool());
+  pp->pool = (const char*)pool;
+  pp->rows = rows;
+  pp->row_bytes = row_bytes;
+  const int64_t n = row_bytes / 2;
+  std::vector<uint32_t> base((size_t)rows);
+  std::vector<int64_t> esc((size_t)rows);
+  ferry::pack_plan_rows((const uint16_t*)pool, rows, n, threads, base.data(), esc.data());
+  pp->off.assign((size_t)rows, 0);
+  pp->size.assign((size_t)rows, 0);
+  pp->raw.assign((size_t)rows, 0);
+  std::vector<int64_t> pack_off((size_t)rows, -1);   // rows to pack: their offset
+  for (int64_t i = 0; i < rows; ++i) {
+    int64_t b = ferry::packed_bytes(n, esc[(size_t)i]);
+    if (b >= row_bytes) {   // no gain: the row is stored raw
+      b = row_bytes;
+      pp->raw[(size_t)i] = 1;
+    } else {
+      pack_off[(size_t)i] = pp->bytes;
+      ++pp->packed_rows;
+      pp->packed_bytes += b;
+      pp->largest = b > pp->largest ? b : pp->largest;
+    }
+    pp->off[(size_t)i] = pp->bytes;
+    pp->size[(size_t)i] = b;
+    pp->bytes += b;
+  }
+  if (pp->bytes > 0) {
+    void* mem = nullptr;
+    H2D_HIP(hipHostMalloc(&mem, (size_t)pp->bytes, 0));
+    pp->data = (uint8_t*)mem;
+    ferry::pack_write_rows((const uint16_t*)pool, rows, n, threads, base.data(), esc.data(),
+                           pack_off.data(), pp->data);
+    for (int64_t i = 0; i < rows; ++i)
+      if (pp->raw[(size_t)i])
+        std::memcpy(pp->data + pp->off[(size_t)i], (const char*)pool + i * row_bytes,
+                    (size_t)row_bytes);
+  }
+  *out = pp.release();
+  return 0;
+}
+
+extern "C" int ferry_packed_pool_stats(const ferry_packed_pool* pp, int64_t* packed_bytes,
+                                       int64_t* packed_rows) {
+  ferry::clear_error();
+  if (!pp) {
+    ferry::set_error("packed_pool_stats: null handle");
+    return 2;
+  }
+  if (packed_bytes) *packed_bytes = pp->packed_bytes;
+  if (packed_rows) *packed_rows = pp->packed_rows;
+  return 0;
+}
+
+extern "C" int ferry_packed_pool_destroy(ferry_packed_pool* pp) {
+  ferry::clear_error();
+  if (!pp) return 0;
+  if (pp->data) (void)hipHostFree(pp->data);
+  delete pp;
+  return 0;
+}
+
+static int ferry_h2d_use_packed_any(ferry_h2d* h, const ferry_packed_pool* pp,
+                                    int64_t ring_rows);
+
+extern "C" int ferry_h2d_use_packed(ferry_h2d* h, const ferry_packed_pool* pp,
+                                    int64_t ring_rows) {
+  ferry::clear_error();
+  if (!h || !h->pool ||
+      (pp && (pp->pool != h->pool || pp->rows != h->pool_rows || pp->row_bytes != h->row_bytes ||
+              ring_rows < 1))) {
+    ferry::set_error("h2d_use_packed: the packed pool was made from another pool, or no "
+                     "staging buffer");
+    return 2;
+  }
+  return ferry_h2d_use_packed_any(h, pp, ring_rows);
+}
+
+// attaches pp (null: detaches) to h, which fetches from it from now on
+static int ferry_h2d_use_packed_any(ferry_h2d* h, const ferry_packed_pool* pp,
+                                    int64_t ring_rows) {
+  for (int l = 0; l < kLanes; ++l) H2D_HIP(hipStreamSynchronize(h->stream[l]));
+  h->ring_ev.clear();
+  if (h->ring) {
+    H2D_HIP(hipFree(h->ring));
+    h->ring = nullptr;
+  }
+  h->packed = nullptr;
+  h->ring_rows = h->entry_bytes = h->ring_next = 0;
+  if (!pp) return 0;
+  if (pp->packed_rows > 0) {
+    void* rg = nullptr;
+    H2D_HIP(hipMalloc(&rg, (size_t)(ring_rows * pp->largest)));
+    h->ring = (uint8_t*)rg;
+    h->ring_rows = ring_rows;
+    h->entry_bytes = pp->largest;
+    h->ring_ev.assign((size_t)ring_rows, nullptr);
+  } else {
+    h->ring_rows = 1;   // batches are never cut by the staging ring
+  }
+  h->packed = pp;
+  return 0;
+}
+
+extern "C" int ferry_h2d_create_packed(void* cache, int64_t cache_rows,
+                                       const ferry_packed_pool* pp, int32_t device,
+                                       int64_t ring_rows, ferry_h2d** out) {
+  ferry::clear_error();
+  if (!out || !cache || !pp || cache_rows < 0 || ring_rows < 1) {
+    ferry::set_error("h2d_create_packed: bad arguments");
+    return 2;
+  }
+  H2D_HIP(hipSetDevice(device));
+  std::unique_ptr<ferry_h2d> h(new ferry_h2d());
+  h->cache = (char*)cache;
+  h->pool = nullptr;   // every row comes from the packed pool
+  h->cache_rows = cache_rows;
+  h->pool_rows = pp->rows;
+  h->row_bytes = pp->row_bytes;
+  h->device = device;
+  for (int l = 0; l <= kLanes; ++l) h->part[l] = h->row_bytes * l / kLanes / 256 * 256;
+  h->part[kLanes] = h->row_bytes;
+  for (int l = 0; l < kLanes; ++l) {
+    H2D_HIP(hipStreamCreateWithFlags(&h->stream[l], hipStreamNonBlocking));
+    h->copy_done[l].assign((size_t)cache_rows, nullptr);
+  }
+  H2D_HIP(hipEventCreateWithFlags(&h->join, hipEventDisableTiming));
+  h->kernel_stream = h->stream[0];
+  h->copy_seq.assign((size_t)cache_rows, -1);
+  h->batch_of.assign((size_t)cache_rows, 0);
+  h->used.assign((size_t)cache_rows, nullptr);
+  ferry_h2d* raw = h.release();
+  const int rc = ferry_h2d_use_packed_any(raw, pp, ring_rows);
+  if (rc != 0) {
+    ferry_h2d_destroy(raw);
+    return rc;
+  }
+  *out = raw;
+  return 0;
+}
 extern "C" void* ferry_h2d_stream(ferry_h2d* h) { return h ? (void*)h->stream[0] : nullptr; }

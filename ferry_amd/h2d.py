@@ -37,6 +37,23 @@ class H2DEngine:
                                      ctypes.byref(handle)), 'H2DEngine')
         self._h = handle.value
 
+    @classmethod
+    def from_packed(cls, cache, packed, ring_rows=64):
+        """An engine that fetches every row from ``packed`` (a PackedPool) in DMA mode; no raw
+        pool is needed."""
+        if not (isinstance(cache, torch.Tensor) and cache.device.type == 'cuda' and cache.is_contiguous()):
+            raise RuntimeError('cache must be a contiguous CUDA tensor')
+        if cache.dim() != 2 or cache.shape[1] * cache.element_size() != packed.row_bytes:
+            raise RuntimeError('packed rows must match cache rows')
+        eng = cls.__new__(cls)
+        eng._cache, eng._pool, eng._packed = cache, None, packed
+        handle = ctypes.c_void_p()
+        check(lib().ferry_h2d_create_packed(cache.data_ptr(), cache.shape[0], packed.handle,
+                                            cache.device.index or 0, int(ring_rows),
+                                            ctypes.byref(handle)), 'H2DEngine.from_packed')
+        eng._h = handle.value
+        return eng
+
     @property
     def handle(self):
         """The native engine (ferry_h2d*), for ferry_plan_fetch."""
@@ -82,6 +99,13 @@ class H2DEngine:
         handle = stream.cuda_stream if stream is not None else lib().ferry_h2d_stream(self._h)
         check(lib().ferry_h2d_set_kernel_stream(self._h, handle), 'H2DEngine.set_kernel_stream')
 
+    def use_packed(self, packed, ring_rows=64):
+        """Fetch from ``packed`` (a PackedPool of this engine's pool; None: raw rows again) in
+        DMA mode, through ``ring_rows`` device staging buffers."""
+        check(lib().ferry_h2d_use_packed(self._h, packed.handle if packed is not None else None,
+                                         int(ring_rows)), 'H2DEngine.use_packed')
+        self._packed = packed   # keep it alive while the engine uses it
+
     @property
     def kernel_ok(self):
         """Whether the copy kernel can serve this pool (device-mapped, 16-byte rows)."""
@@ -105,6 +129,47 @@ class H2DEngine:
     def close(self):
         if getattr(self, '_h', None):
             lib().ferry_h2d_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class PackedPool:
+    """A lossless packed copy of a pool for the host link (ferry_pack_pool), in pinned memory:
+    per value a sign|mantissa byte and a 4-bit exponent code, 12 bits instead of 16 for weights
+    that span few binades (rows that would not shrink are kept raw).  The source pool may be
+    pageable and may be freed afterwards; engines fetch from the packed pool alone
+    (``H2DEngine.from_packed``) or attach it to an engine of the same pinned pool
+    (``use_packed``)."""
+
+    def __init__(self, pool, threads=16):
+        if not (isinstance(pool, torch.Tensor) and pool.device.type == 'cpu'
+                and pool.is_contiguous() and pool.dim() == 2 and pool.dtype == torch.bfloat16):
+            raise RuntimeError('pool must be a contiguous bf16 [rows, row] host tensor')
+        self.rows, self.row_bytes = pool.shape[0], pool.shape[1] * 2
+        self.pool_id = pool.data_ptr()
+        handle = ctypes.c_void_p()
+        check(lib().ferry_pack_pool(pool.data_ptr(), pool.shape[0], pool.shape[1] * 2,
+                                    int(threads), ctypes.byref(handle)), 'PackedPool')
+        self._h = handle.value
+        pb, pr = ctypes.c_int64(), ctypes.c_int64()
+        check(lib().ferry_packed_pool_stats(self._h, ctypes.byref(pb), ctypes.byref(pr)),
+              'PackedPool')
+        self.packed_bytes, self.packed_rows = pb.value, pr.value
+        raw = self.packed_rows * self.row_bytes
+        self.ratio = raw / self.packed_bytes if self.packed_bytes else 1.0   # over packed rows
+
+    @property
+    def handle(self):
+        return self._h
+
+    def close(self):
+        if getattr(self, '_h', None):
+            lib().ferry_packed_pool_destroy(self._h)
             self._h = None
 
     def __del__(self):

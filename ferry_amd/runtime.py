@@ -50,7 +50,7 @@ def expert_ops():
 class OffloadRuntime:
     def __init__(self, spec, pool, capacities, policy, topology, history_window=128,
                  balance_tol_bps=200, salt=1, eviction_score='frequency', overlap=True,
-                 timing=False, copy='dma'):
+                 timing=False, copy='dma', pack=False, pack_threads=16):
         if dist.is_available() and dist.is_initialized() and dist.get_world_size() != 1:
             raise NotImplementedError('ferry_amd runs on one GPU (world = 1)')
         if len(capacities) != 1:
@@ -66,6 +66,16 @@ class OffloadRuntime:
         if copy not in ('dma', 'kernel'):
             raise ValueError("copy must be 'dma' or 'kernel'")
         self.copy = copy
+        # a lossless packed copy of the pool for the host link, made once; every engine of this
+        # runtime fetches packed rows in DMA mode and unpacks them on the GPU
+        # (pack: True, or a PackedPool of this pool built by the caller and shared; ``pool``
+        # itself may be a PackedPool, whose engines need no raw pool)
+        from .h2d import PackedPool
+        self.packed = None
+        if isinstance(pool, PackedPool):
+            self.packed = pool
+        elif pack is not None and pack is not False:
+            self.packed = pack if isinstance(pack, PackedPool) else PackedPool(pool, pack_threads)
         self.ops = expert_ops()
         self.device = torch.device('cuda', torch.cuda.current_device())
         self.cache = torch.empty((self.cap, spec.expert_elements), dtype=torch.bfloat16,
@@ -93,7 +103,10 @@ class OffloadRuntime:
                                                 self.device)
         if self.h2d is not None:
             self.h2d.close()
-        self.h2d = self.ops.H2DEngine(self.cache, self.pool)
+        if self.packed is not None:
+            self.h2d = self.ops.H2DEngine.from_packed(self.cache, self.packed)
+        else:
+            self.h2d = self.ops.H2DEngine(self.cache, self.pool)
         self._kernel_copy = self.copy == 'kernel' and self.h2d.kernel_ok
         if self.copy == 'kernel' and not self._kernel_copy:
             raise RuntimeError("copy='kernel' needs a device-mapped pool with 16-byte rows")

@@ -111,11 +111,14 @@ def router_gates(spec, layers, seed, device='cuda', std=0.02):
             .to(torch.bfloat16) for _ in range(layers)]
 
 
-def make_pool(spec, layers, seed=0, device='cuda', chunk=32):
-    """Pinned host pool [layers * E, 3 H I] bf16 of ~N(0, 0.02) rows (model.py:86-106 format)."""
+def make_pool(spec, layers, seed=0, device='cuda', chunk=32, pinned=True):
+    """Host pool [layers * E, 3 H I] bf16 of ~N(0, 0.02) rows (model.py:86-106 format), pinned
+    (what H2DEngine copies from) or pageable (the source of a PackedPool, which holds its own
+    pinned copy: pinned host memory is limited, about a quarter of RAM on MI355X hosts)."""
     from .hostmem import pinned_empty
     n = layers * spec.experts
-    pool = pinned_empty((n, spec.expert_elements), torch.bfloat16)
+    shape = (n, spec.expert_elements)
+    pool = pinned_empty(shape, torch.bfloat16) if pinned else torch.empty(shape, dtype=torch.bfloat16)
     for k0 in range(0, n, chunk):
         keys = range(k0, min(n, k0 + chunk))
         pool[k0:k0 + len(keys)].copy_(expert_rows(keys, spec.expert_elements, seed, device))

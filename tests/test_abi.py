@@ -319,3 +319,56 @@ def test_topology_file_round_trip(tmp_path):
     path.write_text(json.dumps(doc))
     with pytest.raises(ValueError, match='2 GPUs'):
         Topology(path, 1, 128)
+
+
+def _unpack_numpy(buf, n):
+    """Independent decoder of a packed row (header, sign|mantissa plane, 4-bit exponent codes,
+    escape list) back to uint16 bf16 bits."""
+    hdr = np.frombuffer(buf[:64], dtype=np.uint64)
+    magic, base = np.frombuffer(buf[:8], dtype=np.uint32)
+    assert magic == 0x4b504146
+    values, escapes, nbytes = int(hdr[1]), int(hdr[2]), int(hdr[3])
+    assert values == n and nbytes == len(buf)
+    a = np.frombuffer(buf[64:64 + n], dtype=np.uint8).astype(np.uint16)
+    b = np.frombuffer(buf[64 + n:64 + n + n // 2], dtype=np.uint8)
+    codes = np.empty(n, np.uint16)
+    codes[0::2] = b & 0xF
+    codes[1::2] = b >> 4
+    off = 64 + n + n // 2
+    idx = np.frombuffer(buf[off:off + 4 * escapes], dtype=np.uint32)
+    exps = np.frombuffer(buf[off + 4 * escapes:off + 5 * escapes], dtype=np.uint8).astype(np.uint16)
+    assert np.all(np.diff(idx.astype(np.int64)) > 0)
+    e = base + codes
+    assert np.array_equal(np.flatnonzero(codes == 15), idx)
+    e[idx] = exps
+    return ((a & 0x80) << 8) | (e << 7) | (a & 0x7F)
+
+
+def test_pack_row_round_trip():
+    """The lossless row packing of the H2D link: packed rows decode (here with an independent
+    numpy decoder) to the exact bf16 bits -- Gaussian weights, special values (+-0, +-inf, NaN,
+    denormals, huge and tiny values, forcing escapes) -- and a row of random bits, which would
+    not shrink, is left raw."""
+    import torch
+    from ferry_amd._lib import lib
+    g = torch.Generator().manual_seed(3)
+    n = 1 << 16
+    gauss = (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16)
+    special = gauss.clone()
+    vals = torch.tensor([0.0, -0.0, float('inf'), -float('inf'), float('nan'), 1e-40, -3e-39,
+                         1e30, -2e-30, 7.0], dtype=torch.float32).to(torch.bfloat16)
+    pos = torch.randperm(n, generator=g)[:2000]
+    special[pos] = vals[torch.arange(2000) % len(vals)]
+    for row in (gauss, special):
+        u16 = row.view(torch.int16).numpy().view(np.uint16).copy()
+        nb = ctypes.c_int64()
+        assert lib().ferry_pack_row(u16.ctypes.data, n, None, 0, ctypes.byref(nb)) == 0
+        buf = np.zeros(nb.value, np.uint8)
+        assert lib().ferry_pack_row(u16.ctypes.data, n, buf.ctypes.data, nb.value,
+                                    ctypes.byref(nb)) == 0
+        assert nb.value < (0.76 if row is gauss else 1.0) * 2 * n
+        assert np.array_equal(_unpack_numpy(buf.tobytes(), n), u16)
+    rnd = np.random.default_rng(0).integers(0, 1 << 16, n, dtype=np.uint16)
+    nb = ctypes.c_int64()
+    assert lib().ferry_pack_row(rnd.ctypes.data, n, None, 0, ctypes.byref(nb)) == 1
+    assert lib().ferry_pack_row(rnd.ctypes.data, 100, None, 0, ctypes.byref(nb)) == 2

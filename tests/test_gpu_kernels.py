@@ -512,6 +512,70 @@ def test_h2d_copy_order_across_modes(device):
     eng.close()
 
 
+def test_h2d_packed_pool_fetch_byte_exact(device):
+    """Fetches from a packed pool write the pool rows' exact bytes: Gaussian rows, a row with
+    special values (+-0, +-inf, NaN, denormals, huge: escapes), a row of random bits (left raw);
+    calls of 1 to 10 rows through 3 staging buffers (ring reuse inside a call and across calls),
+    a slot named twice, a GPU-side wait, and raw fetches again after detaching."""
+    from ferry_amd.h2d import H2DEngine, PackedPool
+    rows, cap, width = 24, 10, 3 * 256 * 128
+    g = torch.Generator().manual_seed(21)
+    pool = (torch.randn((rows, width), generator=g) * 0.02).to(torch.bfloat16)
+    vals = torch.tensor([0.0, -0.0, float('inf'), -float('inf'), float('nan'), 1e-40, 1e30, -7.0])
+    pos = torch.randperm(width, generator=g)[:500]
+    pool[5, pos] = vals.to(torch.bfloat16)[torch.arange(500) % len(vals)]
+    pool[7] = torch.randint(-32768, 32767, (width,), generator=g, dtype=torch.int16).view(torch.bfloat16)
+    pool = pool.pin_memory()
+    packed = PackedPool(pool, threads=4)
+    assert packed.packed_rows == rows - 1 and packed.ratio > 1.3
+    cache = torch.zeros((cap, width), dtype=torch.bfloat16, device=device)
+    eng = H2DEngine(cache, pool)
+    eng.use_packed(packed, ring_rows=3)
+    bits = lambda t: t.view(torch.int16)   # noqa: E731
+    rng = np.random.default_rng(2)
+    for size in (1, 7, 10, 3, 10, 2):
+        slots = rng.choice(cap, size, replace=False)
+        keys = rng.choice(rows, size, replace=False)
+        if size >= 7:
+            keys[0] = 7          # the raw row
+            keys[1] = 5          # the row with escapes
+        eng.fetch(slots, keys)
+        eng.wait_host(slots)
+        assert torch.equal(bits(cache.cpu()[slots]), bits(pool[keys])), size
+    eng.fetch([4, 2, 4], [10, 11, 12])          # slot 4 twice: the later row wins
+    consumer = torch.cuda.Stream()
+    eng.wait_stream([4, 2], consumer)
+    with torch.cuda.stream(consumer):
+        snap = cache[[4, 2]].clone()
+    torch.cuda.synchronize()
+    assert torch.equal(bits(snap.cpu()), bits(pool[[12, 11]]))
+    eng.use_packed(None)
+    eng.fetch([0, 1], [3, 5])
+    eng.wait_host([0, 1])
+    assert torch.equal(bits(cache.cpu()[[0, 1]]), bits(pool[[3, 5]]))
+    other = pool.clone().pin_memory()
+    with pytest.raises(RuntimeError):
+        H2DEngine(cache, other).use_packed(packed)   # packed from another pool
+    eng.close()
+    packed.close()
+    # a packed pool made from pageable memory stands alone: the source is freed before fetching
+    src = pool.clone()
+    assert not src.is_pinned()
+    alone = PackedPool(src, threads=4)
+    del src
+    eng = H2DEngine.from_packed(cache, alone, ring_rows=2)
+    slots = np.arange(cap)
+    keys = rng.choice(rows, cap, replace=False)
+    keys[3] = 7
+    eng.fetch(slots, keys)
+    eng.wait_host(slots)
+    assert torch.equal(bits(cache.cpu()), bits(pool[keys]))
+    with pytest.raises(RuntimeError):
+        eng.use_packed(None)      # no raw pool to fall back to
+    eng.close()
+    alone.close()
+
+
 def test_h2d_kernel_copy_many_rows_and_ragged_widths(device):
     """The copy kernel against the DMA path: a fetch of more rows than one launch takes (300, in
     any slot order), row sizes that are and are not multiples of its 16-byte unit (the latter

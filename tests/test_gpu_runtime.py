@@ -128,6 +128,52 @@ def test_runtime_on_stream_matches_dma_overlap(device, tokens):
         assert torch.equal(u, v), i
 
 
+@pytest.mark.parametrize('tokens', [16, 2048])
+def test_runtime_packed_pool_matches_raw(device, tokens):
+    """OffloadRuntime(pack=True) -- misses copied as packed rows and unpacked on the GPU -- gives
+    bit-identical outputs and the same fetch trace as raw fetches, on decode-sized and on
+    chunked prefill-sized calls."""
+    from dataclasses import replace
+
+    from ferry_amd import expert_ops as ops
+    from ferry_amd import workloads
+    from ferry_amd.model import QWEN3_30B_A3B
+    from ferry_amd.quota import Topology
+    from ferry_amd.runtime import OffloadRuntime
+    spec = replace(QWEN3_30B_A3B, moe_layers=(0, 1))
+    pool = workloads.make_pool(spec, spec.layers, seed=3)
+    bias = torch.from_numpy(workloads.zipf_log_bias(spec.experts, 1.1, np.random.default_rng(0)))
+    cap = 200 if tokens > 64 else 80
+    from ferry_amd.h2d import PackedPool
+    runs = []
+    for pack in ('packed_pool', True, False):
+        if pack == 'packed_pool':   # the runtime given a PackedPool of a pageable pool
+            src = workloads.make_pool(spec, spec.layers, seed=3, pinned=False)
+            rt = OffloadRuntime(spec, PackedPool(src), [cap], 'ferry',
+                                Topology.uniform(1, spec.experts))
+            del src
+        else:
+            rt = OffloadRuntime(spec, pool, [cap], 'ferry', Topology.uniform(1, spec.experts),
+                                pack=pack)
+        if pack:
+            assert rt.packed.ratio > 1.3
+        g = torch.Generator(device=device)
+        g.manual_seed(4)
+        outs = []
+        for call in range(6):
+            x = torch.randn((tokens, spec.hidden), generator=g, device=device).to(torch.bfloat16)
+            z = torch.randn((tokens, spec.experts), generator=g, device=device) + bias.to(device)
+            w, sel = ops.router_topk(z.to(torch.bfloat16), spec.topk)
+            outs.append(rt.execute(call % 2, x, sel, w, None).cpu())
+        runs.append((outs, rt.controller.slots[0].copy(), rt.h2d.copies))
+        rt.close()
+    base_outs, base_slots, base_n = runs[-1]
+    for outs, slots, n in runs[:-1]:
+        assert n == base_n > 0 and np.array_equal(slots, base_slots)
+        for i, (u, v) in enumerate(zip(outs, base_outs)):
+            assert torch.equal(u, v), i
+
+
 def test_runtime_serial_mode(device):
     from ferry_amd.model import ModelSpec
     spec = ModelSpec('qwen3_moe', (0, 1), 16, 4, 256, 128)
