@@ -41,11 +41,9 @@ void clear_error();
 hipError_t h2d_copy_launch(const void* pool, void* cache, int64_t row_bytes, const int64_t* keys,
                            const int64_t* slots, int64_t n, hipStream_t stream);
 hipError_t h2d_unpack_launch(const UnpackList& list, int64_t n, hipStream_t stream);
-void pack_plan_rows(const uint16_t* pool, int64_t rows, int64_t n, int threads, uint32_t* base,
-                    int64_t* escapes);
+void pack_plan_rows(const uint16_t* pool, int64_t rows, int64_t n, int threads, PackPlan* plan);
 void pack_write_rows(const uint16_t* pool, int64_t rows, int64_t n, int threads,
-                     const uint32_t* base, const int64_t* escapes, const int64_t* off,
-                     uint8_t* dst);
+                     const PackPlan* plan, const int64_t* off, uint8_t* dst);
 }  // namespace ferry
 
 namespace {
@@ -89,6 +87,8 @@ struct ferry_h2d {
   uint8_t* ring = nullptr;            // device staging buffers, ring_rows x entry_bytes
   int64_t ring_rows = 0, entry_bytes = 0, ring_next = 0;
   std::vector<std::shared_ptr<Event>> ring_ev;  // per staging buffer: the unpack that read it
+  hipStream_t unpack = nullptr;       // runs the unpacks; each waits for its rows' copies
+  hipEvent_t lane_done[kLanes] = {};  // a lane's copies of one sub-batch
   int64_t cache_rows = 0, pool_rows = 0, row_bytes = 0;
   int64_t part[kLanes + 1] = {};      // byte boundaries of the row parts
   int32_t device = 0;
@@ -147,6 +147,9 @@ extern "C" int ferry_h2d_create(void* cache, int64_t cache_rows, const void* poo
     h->copy_done[l].assign((size_t)cache_rows, nullptr);
   }
   H2D_HIP(hipEventCreateWithFlags(&h->join, hipEventDisableTiming));
+  H2D_HIP(hipStreamCreateWithFlags(&h->unpack, hipStreamNonBlocking));
+  for (int l = 0; l < kLanes; ++l)
+    H2D_HIP(hipEventCreateWithFlags(&h->lane_done[l], hipEventDisableTiming));
   h->kernel_stream = h->stream[0];
   h->copy_seq.assign((size_t)cache_rows, -1);
   h->batch_of.assign((size_t)cache_rows, 0);
@@ -160,11 +163,15 @@ extern "C" int ferry_h2d_destroy(ferry_h2d* h) {
   if (!h) return 0;
   for (int l = 0; l < kLanes; ++l)
     if (h->stream[l]) (void)hipStreamSynchronize(h->stream[l]);
+  if (h->unpack) (void)hipStreamSynchronize(h->unpack);
   for (auto& kl : h->kernel_last) (void)hipEventSynchronize(kl.second->e);
   for (int l = 0; l < kLanes; ++l) h->copy_done[l].clear();
   h->ring_ev.clear();
   if (h->ring) (void)hipFree(h->ring);
   if (h->join) (void)hipEventDestroy(h->join);
+  for (int l = 0; l < kLanes; ++l)
+    if (h->lane_done[l]) (void)hipEventDestroy(h->lane_done[l]);
+  if (h->unpack) (void)hipStreamDestroy(h->unpack);
   h->used.clear();
   for (int l = 0; l < kLanes; ++l)
     if (h->stream[l]) (void)hipStreamDestroy(h->stream[l]);
@@ -172,11 +179,18 @@ extern "C" int ferry_h2d_destroy(ferry_h2d* h) {
   return 0;
 }
 
-// DMA fetch on a packed pool: the packed rows are copied into device staging buffers and one
-// unpack launch per batch (at most kUnpackRows packed rows, at most one per staging buffer)
-// writes their slots; rows that stayed raw are copied straight into their slots.  The batch's
-// bytes, concatenated, are cut into kLanes equal ranges; the lanes join into the first stream,
-// which runs the unpack, and every slot of the batch is ready at the event after it.
+// Packed bytes after which a sub-batch of a packed fetch closes: its unpack then runs while the
+// lanes copy the next sub-batch (about one expert row of the models served here).
+constexpr int64_t kSubBatchBytes = int64_t(4) << 20;
+
+// DMA fetch on a packed pool.  The call's rows go in sub-batches of about kSubBatchBytes (at
+// most kUnpackRows packed rows, at most one per staging buffer, no slot twice): the sub-batch's
+// packed rows, concatenated, are cut into kLanes equal byte ranges that the lanes copy into
+// staging buffers (rows that stayed raw go straight into their slots); the unpack stream waits
+// for both lanes' copies of the sub-batch and runs one unpack launch that writes the slots, and
+// every slot of the sub-batch is ready at the event after it.  The lanes never wait for the
+// unpack stream (except to reuse a staging buffer that an unpack has yet to read), so each
+// sub-batch's unpack runs while the lanes copy the next.
 static int fetch_packed(ferry_h2d* h, const int64_t* slots, const int64_t* keys, int64_t n) {
   struct Seg {
     const char* src;
@@ -192,9 +206,9 @@ static int fetch_packed(ferry_h2d* h, const int64_t* slots, const int64_t* keys,
     ferry::UnpackList ul;
     ul.n_rows = 0;
     std::vector<int64_t> entries;
-    int64_t i1 = i0;
-    ++h->batch;   // a slot named twice starts a new batch, so that the later row wins
-    for (; i1 < n; ++i1) {
+    int64_t i1 = i0, total = 0;
+    ++h->batch;   // a slot named twice starts a new sub-batch, so that the later row wins
+    for (; i1 < n && (i1 == i0 || total < kSubBatchBytes); ++i1) {
       const int64_t key = keys[i1];
       if (h->batch_of[(size_t)slots[i1]] == h->batch) break;
       char* slot_ptr = h->cache + slots[i1] * rb;
@@ -202,6 +216,7 @@ static int fetch_packed(ferry_h2d* h, const int64_t* slots, const int64_t* keys,
       if (pp->raw[(size_t)key]) {
         h->batch_of[(size_t)slots[i1]] = h->batch;
         segs.push_back({src, slot_ptr, rb});
+        total += rb;
         continue;
       }
       if (ul.n_rows == per_batch) break;
@@ -210,6 +225,7 @@ static int fetch_packed(ferry_h2d* h, const int64_t* slots, const int64_t* keys,
       h->ring_next = (k + 1) % h->ring_rows;
       char* st = (char*)h->ring + k * h->entry_bytes;
       segs.push_back({src, st, pp->size[(size_t)key]});
+      total += pp->size[(size_t)key];
       ul.src[ul.n_rows] = (const uint8_t*)st;
       ul.dst[ul.n_rows] = (uint16_t*)slot_ptr;
       ++ul.n_rows;
@@ -233,8 +249,6 @@ static int fetch_packed(ferry_h2d* h, const int64_t* slots, const int64_t* keys,
       (void)hipGetLastError();
       for (int l = 0; l < kLanes; ++l) H2D_HIP(hipStreamWaitEvent(h->stream[l], ev->e, 0));
     }
-    int64_t total = 0;
-    for (const Seg& sg : segs) total += sg.bytes;
     for (int l = 0; l < kLanes; ++l) {
       const int64_t lo = l == 0 ? 0 : total * l / kLanes / 256 * 256;
       const int64_t hi = l + 1 == kLanes ? total : total * (l + 1) / kLanes / 256 * 256;
@@ -247,15 +261,13 @@ static int fetch_packed(ferry_h2d* h, const int64_t* slots, const int64_t* keys,
                                  hipMemcpyHostToDevice, h->stream[l]));
         at += sg.bytes;
       }
+      H2D_HIP(hipEventRecord(h->lane_done[l], h->stream[l]));
+      H2D_HIP(hipStreamWaitEvent(h->unpack, h->lane_done[l], 0));
     }
-    for (int l = 1; l < kLanes; ++l) {
-      H2D_HIP(hipEventRecord(h->join, h->stream[l]));
-      H2D_HIP(hipStreamWaitEvent(h->stream[0], h->join, 0));
-    }
-    if (ul.n_rows > 0) H2D_HIP(ferry::h2d_unpack_launch(ul, rb / 2, h->stream[0]));
+    if (ul.n_rows > 0) H2D_HIP(ferry::h2d_unpack_launch(ul, rb / 2, h->unpack));
     auto ev = std::make_shared<Event>();
     H2D_HIP(hipEventCreateWithFlags(&ev->e, hipEventDisableTiming));
-    H2D_HIP(hipEventRecord(ev->e, h->stream[0]));
+    H2D_HIP(hipEventRecord(ev->e, h->unpack));
     for (int64_t i = i0; i < i1; ++i) {
       for (int l = 0; l < kLanes; ++l) h->copy_done[l][(size_t)slots[i]] = ev;
       h->copy_seq[(size_t)slots[i]] = h->seq++;
@@ -341,6 +353,8 @@ extern "C" int ferry_h2d_fetch(ferry_h2d* h, const int64_t* slots, const int64_t
   // records starts tens of microseconds late even when nothing is pending.
   for (int l = 0; l < kLanes; ++l)
     for (hipEvent_t e : pending) H2D_HIP(hipStreamWaitEvent(h->stream[l], e, 0));
+  if (h->packed)   // the unpacks write the slots
+    for (hipEvent_t e : pending) H2D_HIP(hipStreamWaitEvent(h->unpack, e, 0));
   // The call's rows, concatenated, are cut into kLanes equal byte ranges, one per lane: a lane
   // copies about n / kLanes whole rows plus a part of the row its range ends in.  A call that
   // names a slot twice splits every row instead, whose in-lane order makes the later row win.
@@ -457,6 +471,7 @@ extern "C" int ferry_h2d_mark_used(ferry_h2d* h, const int64_t* slots, int64_t n
 extern "C" int ferry_h2d_synchronize(ferry_h2d* h) {
   ferry::clear_error();
   for (int l = 0; l < kLanes; ++l) H2D_HIP(hipStreamSynchronize(h->stream[l]));
+  H2D_HIP(hipStreamSynchronize(h->unpack));
   for (auto& kl : h->kernel_last) H2D_HIP(hipEventSynchronize(kl.second->e));
   return 0;
 }
@@ -494,9 +509,9 @@ extern "C" int32_t ferry_h2d_engine(const ferry_h2d* h) { return h ? h->kind : -
 extern "C" int ferry_pack_pool(const void* pool, int64_t rows, int64_t row_bytes,
                                int32_t threads, ferry_packed_pool** out) {
   ferry::clear_error();
-  if (!out || !pool || rows < 0 || row_bytes <= 0 || row_bytes % 32 != 0 ||
+  if (!out || !pool || rows < 0 || row_bytes <= 0 || row_bytes % 64 != 0 ||
       row_bytes / 2 >= ((int64_t)1 << 32)) {
-    ferry::set_error("pack_pool: needs rows of a multiple of 16 bf16 values (below 2^32)");
+    ferry::set_error("pack_pool: needs rows of a multiple of 32 bf16 values (below 2^32)");
     return 2;
   }
   std::unique_ptr<ferry_packed_pool> pp(new ferry_packed_pool());
@@ -504,15 +519,14 @@ extern "C" int ferry_pack_pool(const void* pool, int64_t rows, int64_t row_bytes
   pp->rows = rows;
   pp->row_bytes = row_bytes;
   const int64_t n = row_bytes / 2;
-  std::vector<uint32_t> base((size_t)rows);
-  std::vector<int64_t> esc((size_t)rows);
-  ferry::pack_plan_rows((const uint16_t*)pool, rows, n, threads, base.data(), esc.data());
+  std::vector<ferry::PackPlan> plan((size_t)rows);
+  ferry::pack_plan_rows((const uint16_t*)pool, rows, n, threads, plan.data());
   pp->off.assign((size_t)rows, 0);
   pp->size.assign((size_t)rows, 0);
   pp->raw.assign((size_t)rows, 0);
   std::vector<int64_t> pack_off((size_t)rows, -1);   // rows to pack: their offset
   for (int64_t i = 0; i < rows; ++i) {
-    int64_t b = ferry::packed_bytes(n, esc[(size_t)i]);
+    int64_t b = ferry::packed_bytes(n, plan[(size_t)i].esc1, plan[(size_t)i].esc2);
     if (b >= row_bytes) {   // no gain: the row is stored raw
       b = row_bytes;
       pp->raw[(size_t)i] = 1;
@@ -530,8 +544,8 @@ extern "C" int ferry_pack_pool(const void* pool, int64_t rows, int64_t row_bytes
     void* mem = nullptr;
     H2D_HIP(hipHostMalloc(&mem, (size_t)pp->bytes, 0));
     pp->data = (uint8_t*)mem;
-    ferry::pack_write_rows((const uint16_t*)pool, rows, n, threads, base.data(), esc.data(),
-                           pack_off.data(), pp->data);
+    ferry::pack_write_rows((const uint16_t*)pool, rows, n, threads, plan.data(), pack_off.data(),
+                           pp->data);
     for (int64_t i = 0; i < rows; ++i)
       if (pp->raw[(size_t)i])
         std::memcpy(pp->data + pp->off[(size_t)i], (const char*)pool + i * row_bytes,
@@ -581,6 +595,7 @@ extern "C" int ferry_h2d_use_packed(ferry_h2d* h, const ferry_packed_pool* pp,
 static int ferry_h2d_use_packed_any(ferry_h2d* h, const ferry_packed_pool* pp,
                                     int64_t ring_rows) {
   for (int l = 0; l < kLanes; ++l) H2D_HIP(hipStreamSynchronize(h->stream[l]));
+  H2D_HIP(hipStreamSynchronize(h->unpack));
   h->ring_ev.clear();
   if (h->ring) {
     H2D_HIP(hipFree(h->ring));
@@ -626,6 +641,9 @@ extern "C" int ferry_h2d_create_packed(void* cache, int64_t cache_rows,
     h->copy_done[l].assign((size_t)cache_rows, nullptr);
   }
   H2D_HIP(hipEventCreateWithFlags(&h->join, hipEventDisableTiming));
+  H2D_HIP(hipStreamCreateWithFlags(&h->unpack, hipStreamNonBlocking));
+  for (int l = 0; l < kLanes; ++l)
+    H2D_HIP(hipEventCreateWithFlags(&h->lane_done[l], hipEventDisableTiming));
   h->kernel_stream = h->stream[0];
   h->copy_seq.assign((size_t)cache_rows, -1);
   h->batch_of.assign((size_t)cache_rows, 0);
@@ -639,4 +657,10 @@ extern "C" int ferry_h2d_create_packed(void* cache, int64_t cache_rows,
   *out = raw;
   return 0;
 }
-extern "C" void* ferry_h2d_stream(ferry_h2d* h) { return h ? (void*)h->stream[0] : nullptr; }
+
+// With a packed pool attached, every sub-batch ends on the unpack stream (after both lanes'
+// copies), so its queue ends with the call's last copy; otherwise the lanes join into stream[0].
+extern "C" void* ferry_h2d_stream(ferry_h2d* h) {
+  if (!h) return nullptr;
+  return h->packed ? (void*)h->unpack : (void*)h->stream[0];
+}

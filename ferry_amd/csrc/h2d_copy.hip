@@ -49,64 +49,127 @@ __global__ __launch_bounds__(256) void h2d_copy_kernel(const u32x4* __restrict__
   }
 }
 
-// Unpacks packed rows (pack_format.h) from the staging buffers into cache slots: a thread turns
-// 8 values (8 bytes of plane A, 4 of plane B) into 16 bytes of bf16; an escape code looks its
-// exponent up by binary search in the row's escape list.
-__device__ __forceinline__ uint32_t escape_exponent(const uint32_t* idx, const uint8_t* ex,
-                                                    int64_t count, uint32_t i) {
-  int64_t lo = 0, hi = count;  // idx[lo .. hi) may hold i
-  while (hi - lo > 1) {
+// Unpacks packed rows (pack_format.h) from the staging buffers into cache slots.  A workgroup
+// of 256 threads decodes one block of 8192 values: a thread turns 32 values (32 bytes of the
+// sign | mantissa plane, 4 bytes of each code plane) into 64 bytes of bf16.  The block's slice
+// of the level-2 codes and of the third-level list is staged in LDS; a block-wide prefix sum of
+// the threads' escape counts gives each escape its rank in that slice.
+constexpr int kUnpackThreads = 256;
+constexpr int kL3Lds = 256;   // third-level entries of a block staged in LDS (more: global search)
+
+__device__ __forceinline__ uint32_t level3_global(const uint32_t* idx, const uint8_t* ex, int64_t lo,
+                                                  int64_t hi, uint32_t i) {
+  while (hi - lo > 1) {   // idx[lo] <= i < idx[hi], as the entry for i is in [lo, hi)
     const int64_t mid = (lo + hi) >> 1;
     if (idx[mid] <= i) lo = mid; else hi = mid;
   }
-  return (count > 0 && idx[lo] == i) ? ex[lo] : 0u;
+  return ex[lo];
 }
 
-__global__ __launch_bounds__(256) void unpack_kernel(UnpackList list, int64_t n) {
+__global__ __launch_bounds__(kUnpackThreads) void unpack_kernel(UnpackList list, int64_t n) {
+  __shared__ uint8_t lds_c[kPackBlock / 2 + 16];
+  __shared__ uint16_t lds_li[kL3Lds];
+  __shared__ uint8_t lds_le[kL3Lds];
+  __shared__ uint32_t lds_wave[kUnpackThreads / 64];
   const int r = blockIdx.y;
+  const int64_t blk = blockIdx.x;
+  const int t = threadIdx.x;
   const uint8_t* src = list.src[r];
   const PackHeader* hd = reinterpret_cast<const PackHeader*>(src);
-  const uint32_t base = hd->base;
-  const int64_t esc = (int64_t)hd->escapes;
-  const uint64_t* pa = reinterpret_cast<const uint64_t*>(src + kPackHeaderBytes);
-  const uint32_t* pb = reinterpret_cast<const uint32_t*>(src + kPackHeaderBytes + n);
-  const uint32_t* eidx = reinterpret_cast<const uint32_t*>(src + kPackHeaderBytes + n + n / 2);
-  const uint8_t* eexp = reinterpret_cast<const uint8_t*>(eidx + esc);
-  u32x4* dst = reinterpret_cast<u32x4*>(list.dst[r]);
-  const int64_t groups = n / 8;
-  for (int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x; g < groups;
-       g += (int64_t)gridDim.x * 256) {
-    const uint64_t A = pa[g];
-    const uint32_t B = pb[g];
-    uint32_t w[4];
-#pragma unroll
-    for (int h = 0; h < 4; ++h) {
-      uint32_t pair = 0;
-#pragma unroll
-      for (int q2 = 0; q2 < 2; ++q2) {
-        const int q = 2 * h + q2;
-        const uint32_t a = (uint32_t)(A >> (8 * q)) & 0xFFu;
-        const uint32_t c = (B >> (4 * q)) & 0xFu;
-        uint32_t e = base + c;
-        if (c == (uint32_t)kPackWindow) e = escape_exponent(eidx, eexp, esc, (uint32_t)(8 * g + q));
-        const uint32_t v = ((a & 0x80u) << 8) | (e << 7) | (a & 0x7Fu);
-        pair |= v << (16 * q2);
-      }
-      w[h] = pair;
+  const uint32_t base1 = hd->base1, base2 = hd->base2;
+  const PackOffsets o = pack_offsets(n, (int64_t)hd->esc1, (int64_t)hd->esc2);
+  const uint32_t* pre = reinterpret_cast<const uint32_t*>(src + o.p);
+  const uint32_t e_lo = pre[2 * blk], e_hi = pre[2 * blk + 2];
+  const uint32_t l_lo = pre[2 * blk + 1], l_hi = pre[2 * blk + 3];
+  const uint32_t* lidx = reinterpret_cast<const uint32_t*>(src + o.l_idx);
+  const uint8_t* lexp = src + o.l_exp;
+  // the block's level-2 nibbles [e_lo, e_hi) lie in bytes [e_lo / 2, (e_hi + 1) / 2)
+  const int c_bytes = (int)(((e_hi + 1) >> 1) - (e_lo >> 1));
+  for (int i = t; i < c_bytes; i += kUnpackThreads) lds_c[i] = src[o.c + (e_lo >> 1) + i];
+  const int l_cnt = (int)(l_hi - l_lo);
+  if (l_cnt <= kL3Lds)
+    for (int i = t; i < l_cnt; i += kUnpackThreads) {
+      lds_li[i] = (uint16_t)(lidx[l_lo + i] - (uint32_t)(blk * kPackBlock));
+      lds_le[i] = lexp[l_lo + i];
     }
-    dst[g] = u32x4{w[0], w[1], w[2], w[3]};
+  const int64_t v0 = blk * kPackBlock + 32 * t;
+  const bool active = v0 < n;   // n is a multiple of 32: a thread has 32 values or none
+  u32x4 a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
+  uint32_t p0 = 0, p1 = 0, p2 = 0;
+  if (active) {
+    const u32x4* pa = reinterpret_cast<const u32x4*>(src + o.a + v0);
+    a0 = pa[0];
+    a1 = pa[1];
+    p0 = *reinterpret_cast<const uint32_t*>(src + o.b0 + v0 / 8);
+    p1 = *reinterpret_cast<const uint32_t*>(src + o.b1 + v0 / 8);
+    p2 = *reinterpret_cast<const uint32_t*>(src + o.b2 + v0 / 8);
   }
+  const uint32_t esc = p0 & p1 & p2;   // code 7
+  // block-wide exclusive prefix sum of the escape counts
+  const uint32_t cnt = (uint32_t)__popc(esc);
+  const int lane = t & 63, wave = t >> 6;
+  uint32_t incl = cnt;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t y = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += y;
+  }
+  if (lane == 63) lds_wave[wave] = incl;
+  __syncthreads();   // also publishes the staged nibbles and third-level entries
+  uint32_t rank = incl - cnt;
+  for (int w = 0; w < wave; ++w) rank += lds_wave[w];
+  if (!active) return;
+  const uint32_t a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+  uint32_t w[16];
+#pragma unroll
+  for (int h = 0; h < 16; ++h) {
+    uint32_t pair = 0;
+#pragma unroll
+    for (int q2 = 0; q2 < 2; ++q2) {
+      const int q = 2 * h + q2;
+      const uint32_t b = (a[q >> 2] >> (8 * (q & 3))) & 0xFFu;
+      const uint32_t c = ((p0 >> q) & 1u) | (((p1 >> q) & 1u) << 1) | (((p2 >> q) & 1u) << 2);
+      const uint32_t e = c == (uint32_t)kPackWindow1 ? 0u : base1 + c;   // escapes: filled below
+      pair |= (((b & 0x80u) << 8) | (e << 7) | (b & 0x7Fu)) << (16 * q2);
+    }
+    w[h] = pair;
+  }
+  // escapes, in value order: level-2 code from LDS, or the third-level list
+  const uint32_t nib0 = (e_lo & 1u) + rank;
+  for (uint32_t m = esc, k = 0; m != 0; m &= m - 1, ++k) {
+    const int q = __builtin_ctz(m);
+    const uint32_t nib = nib0 + k;
+    const uint32_t c2 = (lds_c[nib >> 1] >> (4 * (nib & 1u))) & 0xFu;
+    uint32_t e;
+    if (c2 < (uint32_t)kPackWindow2) {
+      e = base2 + c2;
+    } else {
+      const uint32_t li = (uint32_t)(32 * t + q);   // index within the block
+      if (l_cnt <= kL3Lds) {
+        int j = 0;
+        while (j + 1 < l_cnt && lds_li[j] != li) ++j;
+        e = lds_le[j];
+      } else {
+        e = level3_global(lidx, lexp, l_lo, l_hi, (uint32_t)(blk * kPackBlock) + li);
+      }
+    }
+    const uint32_t bits = e << (7 + 16 * (q & 1));
+#pragma unroll
+    for (int h = 0; h < 16; ++h) w[h] |= (h == (q >> 1)) ? bits : 0u;
+  }
+  u32x4* dst = reinterpret_cast<u32x4*>(list.dst[r] + v0);
+#pragma unroll
+  for (int h = 0; h < 4; ++h) dst[h] = u32x4{w[4 * h], w[4 * h + 1], w[4 * h + 2], w[4 * h + 3]};
 }
 
 }  // namespace
 
-// Unpacks list.n_rows packed rows of n values each, on `stream`.
+// Unpacks list.n_rows packed rows of n values each (n a multiple of 32), on `stream`.
 hipError_t h2d_unpack_launch(const UnpackList& list, int64_t n, hipStream_t stream) {
   if (list.n_rows <= 0) return hipSuccess;
-  const int64_t blocks = (n / 8 + 255) / 256;
-  hipLaunchKernelGGL(unpack_kernel, dim3((unsigned)(blocks < 2048 ? blocks : 2048),
-                                         (unsigned)list.n_rows),
-                     dim3(256), 0, stream, list, n);
+  const int64_t blocks = (n + kPackBlock - 1) / kPackBlock;
+  hipLaunchKernelGGL(unpack_kernel, dim3((unsigned)blocks, (unsigned)list.n_rows),
+                     dim3(kUnpackThreads), 0, stream, list, n);
   return hipGetLastError();
 }
 

@@ -1,5 +1,5 @@
 // Host side of the packed expert rows (the format is described in pack_format.h): choosing each
-// row's exponent window and writing its packed form, over a pool of rows on several threads.
+// row's exponent windows and writing its packed form, over a pool of rows on several threads.
 #include <cstdint>
 #include <cstring>
 #include <thread>
@@ -12,58 +12,92 @@ namespace ferry {
 void set_error(const char* fmt, ...);
 void clear_error();
 
-// Window base and escape count of one row of n bf16 values.
-void pack_plan(const uint16_t* v, int64_t n, uint32_t* base, int64_t* escapes) {
-  int64_t hist[256] = {};
-  for (int64_t i = 0; i < n; ++i) ++hist[(v[i] >> 7) & 0xFF];
-  int64_t best = -1, in = 0;
+// Most populated window of `width` exponents in hist: its first exponent and its population.
+static void best_window(const int64_t* hist, int width, uint32_t* base, int64_t* in_window) {
+  int64_t in = 0, best = -1;
   uint32_t b_best = 0;
-  for (int e = 0; e < kPackWindow; ++e) in += hist[e];
-  for (int b = 0; b + kPackWindow <= 256; ++b) {
-    if (b > 0) in += hist[b + kPackWindow - 1] - hist[b - 1];
+  for (int e = 0; e < width; ++e) in += hist[e];
+  for (int b = 0; b + width <= 256; ++b) {
+    if (b > 0) in += hist[b + width - 1] - hist[b - 1];
     if (in > best) {
       best = in;
       b_best = (uint32_t)b;
     }
   }
   *base = b_best;
-  *escapes = n - best;
+  *in_window = best;
 }
 
-// Writes the packed row (packed_bytes(n, escapes) bytes) of a row planned by pack_plan.
-void pack_write(const uint16_t* v, int64_t n, uint32_t base, int64_t escapes, uint8_t* dst) {
+// The two exponent windows of one row of n bf16 values and its escape counts.
+void pack_plan(const uint16_t* v, int64_t n, PackPlan* plan) {
+  int64_t hist[256] = {};
+  for (int64_t i = 0; i < n; ++i) ++hist[(v[i] >> 7) & 0xFF];
+  int64_t in1, in2;
+  best_window(hist, kPackWindow1, &plan->base1, &in1);
+  for (int e = 0; e < kPackWindow1; ++e) hist[plan->base1 + e] = 0;   // the escapes remain
+  best_window(hist, kPackWindow2, &plan->base2, &in2);
+  plan->esc1 = n - in1;
+  plan->esc2 = plan->esc1 - in2;
+}
+
+// Writes the packed row (packed_bytes(n, esc1, esc2) bytes) of a row planned by pack_plan.
+void pack_write(const uint16_t* v, int64_t n, const PackPlan& plan, uint8_t* dst) {
+  const PackOffsets o = pack_offsets(n, plan.esc1, plan.esc2);
+  const int64_t bytes = packed_bytes(n, plan.esc1, plan.esc2);
   PackHeader hd;
   std::memset(&hd, 0, sizeof(hd));
   hd.magic = kPackMagic;
-  hd.base = base;
+  hd.base1 = plan.base1;
+  hd.base2 = plan.base2;
   hd.values = (uint64_t)n;
-  hd.escapes = (uint64_t)escapes;
-  hd.bytes = (uint64_t)packed_bytes(n, escapes);
+  hd.esc1 = (uint64_t)plan.esc1;
+  hd.esc2 = (uint64_t)plan.esc2;
+  hd.bytes = (uint64_t)bytes;
   std::memcpy(dst, &hd, sizeof(hd));
-  uint8_t* pa = dst + kPackHeaderBytes;
-  uint8_t* pb = pa + n;
-  uint32_t* eidx = reinterpret_cast<uint32_t*>(pb + n / 2);
-  uint8_t* eexp = reinterpret_cast<uint8_t*>(eidx + escapes);
-  int64_t k = 0;
-  for (int64_t i = 0; i < n; i += 2) {
-    uint8_t codes = 0;
-    for (int q = 0; q < 2; ++q) {
+  std::memset(dst + o.c, 0, (size_t)(bytes - o.c));   // nibble plane, alignment gap, tail
+  uint8_t* pa = dst + o.a;
+  uint8_t* b0 = dst + o.b0;
+  uint8_t* b1 = dst + o.b1;
+  uint8_t* b2 = dst + o.b2;
+  uint32_t* pre = reinterpret_cast<uint32_t*>(dst + o.p);
+  uint8_t* pc = dst + o.c;
+  uint32_t* lidx = reinterpret_cast<uint32_t*>(dst + o.l_idx);
+  uint8_t* lexp = dst + o.l_exp;
+  int64_t k1 = 0, k2 = 0;   // escapes and third-level entries so far
+  for (int64_t i = 0; i < n; i += 8) {
+    if (i % kPackBlock == 0) {
+      pre[2 * (i / kPackBlock)] = (uint32_t)k1;
+      pre[2 * (i / kPackBlock) + 1] = (uint32_t)k2;
+    }
+    uint32_t p0 = 0, p1 = 0, p2 = 0;
+    for (int q = 0; q < 8; ++q) {
       const uint16_t x = v[i + q];
       const uint32_t e = (x >> 7) & 0xFF;
       pa[i + q] = (uint8_t)(((x >> 8) & 0x80) | (x & 0x7F));
-      uint32_t c = e - base;  // wraps for e < base
-      if (c >= (uint32_t)(kPackWindow)) {
-        c = kPackWindow;
-        eidx[k] = (uint32_t)(i + q);
-        eexp[k] = (uint8_t)e;
-        ++k;
+      uint32_t c = e - plan.base1;   // wraps for e < base1
+      if (c >= (uint32_t)kPackWindow1) {
+        c = kPackWindow1;
+        uint32_t c2 = e - plan.base2;
+        if (c2 >= (uint32_t)kPackWindow2) {
+          c2 = kPackWindow2;
+          lidx[k2] = (uint32_t)(i + q);
+          lexp[k2] = (uint8_t)e;
+          ++k2;
+        }
+        pc[k1 >> 1] |= (uint8_t)(c2 << (4 * (k1 & 1)));
+        ++k1;
       }
-      codes |= (uint8_t)(c << (4 * q));
+      p0 |= (c & 1u) << q;
+      p1 |= ((c >> 1) & 1u) << q;
+      p2 |= ((c >> 2) & 1u) << q;
     }
-    pb[i / 2] = codes;
+    b0[i / 8] = (uint8_t)p0;
+    b1[i / 8] = (uint8_t)p1;
+    b2[i / 8] = (uint8_t)p2;
   }
-  const int64_t end = kPackHeaderBytes + n + n / 2 + 5 * escapes;
-  std::memset(dst + end, 0, (size_t)(hd.bytes - end));
+  const int64_t nb = (n + kPackBlock - 1) / kPackBlock;
+  pre[2 * nb] = (uint32_t)k1;
+  pre[2 * nb + 1] = (uint32_t)k2;
 }
 
 // Run f(i) for i in [0, n) on `threads` threads.
@@ -79,37 +113,34 @@ void parallel_rows(int64_t n, int threads, F f) {
   for (auto& th : pool) th.join();
 }
 
-// Window bases and escape counts of `rows` rows of n values, on `threads` threads.
-void pack_plan_rows(const uint16_t* pool, int64_t rows, int64_t n, int threads, uint32_t* base,
-                    int64_t* escapes) {
-  parallel_rows(rows, threads, [&](int64_t i) { pack_plan(pool + i * n, n, &base[i], &escapes[i]); });
+// Plans of `rows` rows of n values, on `threads` threads.
+void pack_plan_rows(const uint16_t* pool, int64_t rows, int64_t n, int threads, PackPlan* plan) {
+  parallel_rows(rows, threads, [&](int64_t i) { pack_plan(pool + i * n, n, &plan[i]); });
 }
 
 // Packed rows written at dst + off[i] for every row with off[i] >= 0.
 void pack_write_rows(const uint16_t* pool, int64_t rows, int64_t n, int threads,
-                     const uint32_t* base, const int64_t* escapes, const int64_t* off,
-                     uint8_t* dst) {
+                     const PackPlan* plan, const int64_t* off, uint8_t* dst) {
   parallel_rows(rows, threads, [&](int64_t i) {
-    if (off[i] >= 0) pack_write(pool + i * n, n, base[i], escapes[i], dst + off[i]);
+    if (off[i] >= 0) pack_write(pool + i * n, n, plan[i], dst + off[i]);
   });
 }
 
 }  // namespace ferry
 
-// Packs one row of n bf16 values (n a multiple of 16) into dst (capacity cap bytes; null to
+// Packs one row of n bf16 values (n a multiple of 32) into dst (capacity cap bytes; null to
 // query the size).  *bytes_out receives the packed size; returns 0, or 1 when the packed form
 // is not smaller than the row (the row then stays raw and dst is untouched), 2 on bad arguments.
 extern "C" int ferry_pack_row(const void* src, int64_t n, void* dst, int64_t cap,
                               int64_t* bytes_out) {
   ferry::clear_error();
-  if (!src || n <= 0 || n % 16 != 0 || n >= ((int64_t)1 << 32) || !bytes_out) {
-    ferry::set_error("pack_row: n must be a positive multiple of 16 below 2^32");
+  if (!src || n <= 0 || n % 32 != 0 || n >= ((int64_t)1 << 32) || !bytes_out) {
+    ferry::set_error("pack_row: n must be a positive multiple of 32 below 2^32");
     return 2;
   }
-  uint32_t base;
-  int64_t esc;
-  ferry::pack_plan((const uint16_t*)src, n, &base, &esc);
-  const int64_t bytes = ferry::packed_bytes(n, esc);
+  ferry::PackPlan plan;
+  ferry::pack_plan((const uint16_t*)src, n, &plan);
+  const int64_t bytes = ferry::packed_bytes(n, plan.esc1, plan.esc2);
   *bytes_out = bytes;
   if (bytes >= 2 * n) return 1;
   if (!dst) return 0;
@@ -117,6 +148,6 @@ extern "C" int ferry_pack_row(const void* src, int64_t n, void* dst, int64_t cap
     ferry::set_error("pack_row: %lld bytes needed, %lld given", (long long)bytes, (long long)cap);
     return 2;
   }
-  ferry::pack_write((const uint16_t*)src, n, base, esc, (uint8_t*)dst);
+  ferry::pack_write((const uint16_t*)src, n, plan, (uint8_t*)dst);
   return 0;
 }

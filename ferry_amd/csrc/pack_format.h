@@ -2,36 +2,79 @@
 //
 // A bf16 value is sign (1 bit) | exponent (8) | mantissa (7).  Sign and mantissa are close to
 // random in trained (and in Gaussian) weights; the exponent takes few values (the weights of a
-// row span a few binades).  A packed row keeps, per value, one byte sign | mantissa and a 4-bit
-// exponent code: exponent = base + code for code < 15, where [base, base + 14] is the row's
-// most populated window of 15 exponents; code 15 marks an escape, whose exponent is stored in a
-// list sorted by value index.  12 bits per value instead of 16, plus 5 bytes per escape.
+// row span a few binades, most of them in a handful).  A packed row keeps, per value, one byte
+// sign | mantissa and a 3-bit exponent code: exponent = base1 + code for code < 7, where
+// [base1, base1 + 6] is the row's most populated window of 7 exponents.  Code 7 marks an escape;
+// the escapes' exponents follow in value order as 4-bit codes against a second window
+// [base2, base2 + 14] (the most populated among the escapes), and code 15 there sends the
+// exponent to a third level, a list of (value index, exponent) sorted by index.  A prefix table
+// gives, for each block of 8192 values, the escapes and the third-level entries before it, so a
+// block decodes on its own: it counts its escapes' ranks within the block and reads its slice of
+// the level-2 codes and of the third-level list.  About 11.1 bits per value for the
+// Gaussian-like rows of expert weights, instead of 16.
 //
-// Layout (byte offsets from the row start; n = values per row, a multiple of 16):
-//   [0, 64)                      PackHeader
-//   [64, 64 + n)                 plane A: byte i = (sign << 7) | mantissa of value i
-//   [64 + n, 64 + 3n/2)          plane B: nibble i (low nibble first) = exponent code of value i
-//   [64 + 3n/2, + 4 escapes)     escape indices (uint32, ascending)
-//   [.., + escapes)              escape exponents (uint8)
+// Layout (byte offsets from the row start; n = values per row, a multiple of 32):
+//   [0, 64)                       PackHeader
+//   A   n bytes                   byte i = (sign << 7) | mantissa of value i
+//   B0, B1, B2  n / 8 bytes each  bit (i % 8) of byte i / 8: bit 0 / 1 / 2 of the code of value i
+//   P   8 * (nb + 1) bytes        nb = ceil(n / 8192) blocks; uint32 pairs: P[2b] = escapes
+//                                 among values [0, 8192 b), P[2b + 1] = third-level entries
+//                                 among them (b = nb: the totals)
+//   C   ceil(esc1 / 2) bytes      nibble k (low nibble first) = level-2 code of escape k
+//   L   4 * esc2 + esc2 bytes     uint32 value indices (ascending), then uint8 exponents
 // The row's size is rounded up to 256 bytes.
 #pragma once
 #include <cstdint>
 
 namespace ferry {
 
-constexpr uint32_t kPackMagic = 0x4b504146u;  // "FAPK"
+constexpr uint32_t kPackMagic = 0x3250414bu;  // "KAP2"
 constexpr int64_t kPackHeaderBytes = 64;
-constexpr int kPackWindow = 15;
+constexpr int64_t kPackBlock = 8192;     // values per prefix-table entry
+constexpr int kPackWindow1 = 7;          // 3-bit codes 0..6, 7 = escape
+constexpr int kPackWindow2 = 15;         // 4-bit codes 0..14, 15 = third level
 
 struct PackHeader {
   uint32_t magic;
-  uint32_t base;       // first exponent of the window
+  uint32_t base1;      // first exponent of the 3-bit window
+  uint32_t base2;      // first exponent of the level-2 window
+  uint32_t pad0;
   uint64_t values;     // n
-  uint64_t escapes;
+  uint64_t esc1;       // values with code 7
+  uint64_t esc2;       // escapes with level-2 code 15 (third-level list)
   uint64_t bytes;      // packed size (rounded)
-  uint64_t pad[4];
+  uint64_t pad[2];
 };
 static_assert(sizeof(PackHeader) == kPackHeaderBytes, "header size");
+
+struct PackOffsets {
+  int64_t a, b0, b1, b2, p, c, l_idx, l_exp, end;
+};
+
+// Exponent windows and escape counts chosen for one row.
+struct PackPlan {
+  uint32_t base1, base2;
+  int64_t esc1, esc2;
+};
+
+constexpr PackOffsets pack_offsets(int64_t n, int64_t esc1, int64_t esc2) {
+  PackOffsets o{};
+  o.a = kPackHeaderBytes;
+  o.b0 = o.a + n;
+  o.b1 = o.b0 + n / 8;
+  o.b2 = o.b1 + n / 8;
+  o.p = o.b2 + n / 8;
+  o.c = o.p + 8 * ((n + kPackBlock - 1) / kPackBlock + 1);
+  o.l_idx = o.c + (esc1 + 1) / 2;
+  o.l_idx = (o.l_idx + 3) / 4 * 4;   // aligned uint32 indices
+  o.l_exp = o.l_idx + 4 * esc2;
+  o.end = o.l_exp + esc2;
+  return o;
+}
+
+constexpr int64_t packed_bytes(int64_t n, int64_t esc1, int64_t esc2) {
+  return (pack_offsets(n, esc1, esc2).end + 255) / 256 * 256;
+}
 
 constexpr int kUnpackRows = 64;   // rows per unpack launch
 
@@ -41,10 +84,5 @@ struct UnpackList {
   uint16_t* dst[kUnpackRows];       // cache slots
   int32_t n_rows;
 };
-
-inline int64_t packed_bytes(int64_t n, int64_t escapes) {
-  const int64_t b = kPackHeaderBytes + n + n / 2 + 4 * escapes + escapes;
-  return (b + 255) / 256 * 256;
-}
 
 }  // namespace ferry

@@ -223,7 +223,9 @@ int ferry_h2d_mark_used(ferry_h2d* h, const int64_t* slots, int64_t n, void* str
 int ferry_h2d_synchronize(ferry_h2d* h);
 /* expert_ops.cpp:135 */
 int64_t ferry_h2d_copies(const ferry_h2d* h);
-/* the engine's copy stream (for event timing by the caller) */
+/* the engine's copy stream (for event timing by the caller): after a fetch call its queue ends
+ * with the call's copies -- the first DMA lane, which the others join, or, with a packed pool
+ * attached, the stream that runs the unpacks */
 void* ferry_h2d_stream(ferry_h2d* h);
 /* How the engine copies (no counterpart in the reference, whose engine always issues one
  * cudaMemcpyAsync per row).  FERRY_H2D_DMA (the default): hipMemcpyAsync on two DMA streams,
@@ -244,15 +246,17 @@ int32_t ferry_h2d_engine(const ferry_h2d* h);
 int ferry_h2d_set_kernel_stream(ferry_h2d* h, void* stream);
 /* Lossless packing of the pool for the host link (no counterpart in the reference, whose
  * engine copies raw bf16 rows).  ferry_pack_pool copies every pool row into pinned host memory,
- * in a packed form where it shrinks: per value one byte sign | mantissa and a 4-bit exponent
- * code against the row's most populated window of 15 exponents, the other exponents in an
- * escape list (12 bits per value for weights that span few binades); a row that would not
- * shrink is copied raw.  It reads the pool (pinned or pageable host memory, not changed
+ * in a packed form where it shrinks: per value one byte sign | mantissa and a 3-bit exponent
+ * code against the row's most populated window of 7 exponents; the other exponents follow as
+ * 4-bit codes against a second window of 15, and the rest in an (index, exponent) list (about
+ * 11.1 bits per value for weights that span few binades); a row that would not shrink is
+ * copied raw.  Rows hold a multiple of 32 values.  It reads the pool (pinned or pageable host memory, not changed
  * afterwards) on `threads` host threads; the packed pool then stands alone.  An engine made
  * from it (ferry_h2d_create_packed) or given it (ferry_h2d_use_packed, an engine of the same
  * pinned pool; null detaches it) fetches in DMA mode: packed rows go into `ring_rows` device
  * staging buffers it allocates, and an unpack kernel writes the slots -- the slot bytes are
- * exactly the pool row's.  A packed pool outlives the engines that use it. */
+ * exactly the pool row's.  A call is fetched in sub-batches of about 4 MiB, each unpacked on a
+ * stream of its own while the DMA lanes copy the next.  A packed pool outlives the engines that use it. */
 typedef struct ferry_packed_pool ferry_packed_pool;
 int ferry_pack_pool(const void* pool, int64_t rows, int64_t row_bytes, int32_t threads,
                     ferry_packed_pool** out);
@@ -262,7 +266,7 @@ int ferry_packed_pool_destroy(ferry_packed_pool* pp);
 int ferry_h2d_use_packed(ferry_h2d* h, const ferry_packed_pool* pp, int64_t ring_rows);
 int ferry_h2d_create_packed(void* cache, int64_t cache_rows, const ferry_packed_pool* pp,
                             int32_t device, int64_t ring_rows, ferry_h2d** out);
-/* The packing of one row of n bf16 values (n a multiple of 16) into dst (cap bytes; null to
+/* The packing of one row of n bf16 values (n a multiple of 32) into dst (cap bytes; null to
  * query the size): 0, or 1 when the row would not shrink (dst untouched); *bytes_out is the
  * packed size.  For tests and tools; the engine packs its pool itself. */
 int ferry_pack_row(const void* src, int64_t n, void* dst, int64_t cap, int64_t* bytes_out);

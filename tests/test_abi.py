@@ -322,53 +322,97 @@ def test_topology_file_round_trip(tmp_path):
 
 
 def _unpack_numpy(buf, n):
-    """Independent decoder of a packed row (header, sign|mantissa plane, 4-bit exponent codes,
-    escape list) back to uint16 bf16 bits."""
+    """Independent decoder of a packed row back to uint16 bf16 bits: header, sign|mantissa
+    plane, three bit planes of 3-bit exponent codes (7 = escape), the prefix table, the 4-bit
+    level-2 codes of the escapes in value order (15 = third level) and the third-level
+    (index, exponent) list."""
     hdr = np.frombuffer(buf[:64], dtype=np.uint64)
-    magic, base = np.frombuffer(buf[:8], dtype=np.uint32)
-    assert magic == 0x4b504146
-    values, escapes, nbytes = int(hdr[1]), int(hdr[2]), int(hdr[3])
-    assert values == n and nbytes == len(buf)
+    magic, base1, base2 = np.frombuffer(buf[:12], dtype=np.uint32)
+    assert magic == 0x3250414b
+    values, esc1, esc2, nbytes = (int(x) for x in hdr[2:6])
+    assert values == n and nbytes == len(buf) and nbytes % 256 == 0
     a = np.frombuffer(buf[64:64 + n], dtype=np.uint8).astype(np.uint16)
-    b = np.frombuffer(buf[64 + n:64 + n + n // 2], dtype=np.uint8)
-    codes = np.empty(n, np.uint16)
-    codes[0::2] = b & 0xF
-    codes[1::2] = b >> 4
-    off = 64 + n + n // 2
-    idx = np.frombuffer(buf[off:off + 4 * escapes], dtype=np.uint32)
-    exps = np.frombuffer(buf[off + 4 * escapes:off + 5 * escapes], dtype=np.uint8).astype(np.uint16)
+    off = 64 + n
+    bits = [np.unpackbits(np.frombuffer(buf[off + k * (n // 8):off + (k + 1) * (n // 8)],
+                                        dtype=np.uint8), bitorder='little') for k in range(3)]
+    codes = bits[0].astype(np.uint16) | (bits[1].astype(np.uint16) << 1) | (bits[2].astype(np.uint16) << 2)
+    off += 3 * (n // 8)
+    nb = -(-n // 8192)
+    pre = np.frombuffer(buf[off:off + 8 * (nb + 1)], dtype=np.uint32).reshape(nb + 1, 2)
+    off += 8 * (nb + 1)
+    esc = np.flatnonzero(codes == 7)
+    assert len(esc) == esc1
+    # the prefix table counts escapes and third-level entries before each block
+    assert np.array_equal(pre[:, 0], np.searchsorted(esc, np.arange(nb + 1) * 8192))
+    nib = np.frombuffer(buf[off:off + (esc1 + 1) // 2], dtype=np.uint8)
+    c2 = np.empty(2 * len(nib), np.uint16)
+    c2[0::2] = nib & 0xF
+    c2[1::2] = nib >> 4
+    c2 = c2[:esc1]
+    off = (off + (esc1 + 1) // 2 + 3) // 4 * 4
+    idx = np.frombuffer(buf[off:off + 4 * esc2], dtype=np.uint32)
+    exps = np.frombuffer(buf[off + 4 * esc2:off + 5 * esc2], dtype=np.uint8).astype(np.uint16)
     assert np.all(np.diff(idx.astype(np.int64)) > 0)
-    e = base + codes
-    assert np.array_equal(np.flatnonzero(codes == 15), idx)
+    assert np.array_equal(esc[c2 == 15], idx)
+    assert np.array_equal(pre[:, 1], np.searchsorted(idx, np.arange(nb + 1) * 8192))
+    assert not buf[off + 5 * esc2:].strip(b'\0')   # zero tail
+    e = base1 + codes
+    e[esc] = base2 + c2
     e[idx] = exps
     return ((a & 0x80) << 8) | (e << 7) | (a & 0x7F)
 
 
+def _heavy_block(row, block, count, g):
+    """A copy of a bf16 row whose 8192-value block `block` holds `count` values spread over
+    ~160 binades: most of them beyond both exponent windows (third-level entries)."""
+    import torch
+    out = row.clone()
+    k = torch.randint(20, 100, (count,), generator=g).float()
+    sign = torch.where(torch.rand(count, generator=g) < 0.5, -1.0, 1.0)
+    big = torch.rand(count, generator=g) < 0.5
+    vals = sign * torch.exp2(torch.where(big, k, -k)) * 1.25
+    out[8192 * block:8192 * block + count] = vals.to(torch.bfloat16)
+    return out
+
+
 def test_pack_row_round_trip():
     """The lossless row packing of the H2D link: packed rows decode (here with an independent
-    numpy decoder) to the exact bf16 bits -- Gaussian weights, special values (+-0, +-inf, NaN,
-    denormals, huge and tiny values, forcing escapes) -- and a row of random bits, which would
-    not shrink, is left raw."""
+    numpy decoder) to the exact bf16 bits -- Gaussian weights at a length that is a whole number
+    of 8192-value blocks and at a ragged one, special values (+-0, +-inf, NaN, denormals, huge
+    and tiny values: escapes at every level), values spread over 64 binades (hundreds of
+    third-level entries per block) -- and a row of random bits, which would not shrink, is left
+    raw."""
     import torch
     from ferry_amd._lib import lib
     g = torch.Generator().manual_seed(3)
     n = 1 << 16
     gauss = (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16)
+    ragged = (torch.randn(3 * 8192 + 96, generator=g) * 0.5).to(torch.bfloat16)
     special = gauss.clone()
     vals = torch.tensor([0.0, -0.0, float('inf'), -float('inf'), float('nan'), 1e-40, -3e-39,
                          1e30, -2e-30, 7.0], dtype=torch.float32).to(torch.bfloat16)
     pos = torch.randperm(n, generator=g)[:2000]
     special[pos] = vals[torch.arange(2000) % len(vals)]
-    for row in (gauss, special):
+    wide = (torch.randn(n, generator=g) * torch.exp2(torch.randint(-32, 32, (n,), generator=g)
+                                                     .float())).to(torch.bfloat16)
+    heavy = _heavy_block(gauss, 2, 600, g)
+    for row, bound in ((gauss, 0.70), (ragged, 0.72), (special, 0.9), (heavy, 0.75), (wide, 1.0)):
+        m = row.numel()
         u16 = row.view(torch.int16).numpy().view(np.uint16).copy()
         nb = ctypes.c_int64()
-        assert lib().ferry_pack_row(u16.ctypes.data, n, None, 0, ctypes.byref(nb)) == 0
+        st = lib().ferry_pack_row(u16.ctypes.data, m, None, 0, ctypes.byref(nb))
+        if row is wide and st == 1:
+            continue
+        assert st == 0
         buf = np.zeros(nb.value, np.uint8)
-        assert lib().ferry_pack_row(u16.ctypes.data, n, buf.ctypes.data, nb.value,
+        assert lib().ferry_pack_row(u16.ctypes.data, m, buf.ctypes.data, nb.value,
                                     ctypes.byref(nb)) == 0
-        assert nb.value < (0.76 if row is gauss else 1.0) * 2 * n
-        assert np.array_equal(_unpack_numpy(buf.tobytes(), n), u16)
+        assert nb.value < bound * 2 * m
+        if row is heavy:   # more third-level entries in one block than a workgroup stages
+            assert int(np.frombuffer(buf[32:40].tobytes(), np.uint64)[0]) > 300
+        assert np.array_equal(_unpack_numpy(buf.tobytes(), m), u16)
     rnd = np.random.default_rng(0).integers(0, 1 << 16, n, dtype=np.uint16)
     nb = ctypes.c_int64()
     assert lib().ferry_pack_row(rnd.ctypes.data, n, None, 0, ctypes.byref(nb)) == 1
     assert lib().ferry_pack_row(rnd.ctypes.data, 100, None, 0, ctypes.byref(nb)) == 2
+    assert lib().ferry_pack_row(rnd.ctypes.data, 48, None, 0, ctypes.byref(nb)) == 2

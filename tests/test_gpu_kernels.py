@@ -512,9 +512,22 @@ def test_h2d_copy_order_across_modes(device):
     eng.close()
 
 
+def _spread_block(row, block, count, g):
+    """Row with `count` values of block `block` (8192 values) spread over ~160 binades, so that
+    the packed block holds hundreds of third-level entries."""
+    out = row.clone()
+    k = torch.randint(20, 100, (count,), generator=g).float()
+    sign = torch.where(torch.rand(count, generator=g) < 0.5, -1.0, 1.0)
+    big = torch.rand(count, generator=g) < 0.5
+    out[8192 * block:8192 * block + count] = (sign * torch.exp2(torch.where(big, k, -k))
+                                              * 1.25).to(torch.bfloat16)
+    return out
+
+
 def test_h2d_packed_pool_fetch_byte_exact(device):
     """Fetches from a packed pool write the pool rows' exact bytes: Gaussian rows, a row with
-    special values (+-0, +-inf, NaN, denormals, huge: escapes), a row of random bits (left raw);
+    special values (+-0, +-inf, NaN, denormals, huge: escapes), a row with hundreds of
+    third-level entries in one block, a row of random bits (left raw);
     calls of 1 to 10 rows through 3 staging buffers (ring reuse inside a call and across calls),
     a slot named twice, a GPU-side wait, and raw fetches again after detaching."""
     from ferry_amd.h2d import H2DEngine, PackedPool
@@ -525,6 +538,7 @@ def test_h2d_packed_pool_fetch_byte_exact(device):
     pos = torch.randperm(width, generator=g)[:500]
     pool[5, pos] = vals.to(torch.bfloat16)[torch.arange(500) % len(vals)]
     pool[7] = torch.randint(-32768, 32767, (width,), generator=g, dtype=torch.int16).view(torch.bfloat16)
+    pool[9] = _spread_block(pool[9], 4, 700, g)
     pool = pool.pin_memory()
     packed = PackedPool(pool, threads=4)
     assert packed.packed_rows == rows - 1 and packed.ratio > 1.3
@@ -539,6 +553,7 @@ def test_h2d_packed_pool_fetch_byte_exact(device):
         if size >= 7:
             keys[0] = 7          # the raw row
             keys[1] = 5          # the row with escapes
+            keys[2] = 9          # the row with many third-level entries
         eng.fetch(slots, keys)
         eng.wait_host(slots)
         assert torch.equal(bits(cache.cpu()[slots]), bits(pool[keys])), size
@@ -574,6 +589,27 @@ def test_h2d_packed_pool_fetch_byte_exact(device):
         eng.use_packed(None)      # no raw pool to fall back to
     eng.close()
     alone.close()
+
+
+@pytest.mark.parametrize('width', [2 * 8192 + 96, 32, 8192])
+def test_h2d_packed_pool_ragged_widths(device, width):
+    """Packed rows whose length is not a whole number of 8192-value blocks (a partial last
+    workgroup), a single 32-value row and one exact block unpack to the pool rows' bytes."""
+    from ferry_amd.h2d import H2DEngine, PackedPool
+    rows, cap = 8, 8
+    g = torch.Generator().manual_seed(width)
+    pool = (torch.randn((rows, width), generator=g) * 0.02).to(torch.bfloat16)
+    if width > 8192:
+        pool[3] = _spread_block(pool[3], 1, 400, g)
+    packed = PackedPool(pool, threads=2)
+    cache = torch.zeros((cap, width), dtype=torch.bfloat16, device=device)
+    eng = H2DEngine.from_packed(cache, packed, ring_rows=4)
+    keys = np.arange(rows)[::-1].copy()
+    eng.fetch(np.arange(cap), keys)
+    eng.wait_host(np.arange(cap))
+    assert torch.equal(cache.cpu().view(torch.int16), pool[keys].view(torch.int16))
+    eng.close()
+    packed.close()
 
 
 def test_h2d_kernel_copy_many_rows_and_ragged_widths(device):
