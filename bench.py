@@ -6,10 +6,10 @@ expert cache with the other experts in pinned host memory, router logits N(0, 1)
 Zipf(1.1) popularity (seed 1), expert weights N(0, 0.02) bf16.  One step = one layer call:
 router kernel -> device history + routing IDs to the host -> host planner -> H2D fetch of the
 misses -> layout -> grouped SwiGLU (resident experts first) -> combine.  The fetch copies the
-misses as packed rows (OffloadRuntime(pack=True): per value a sign|mantissa byte and a 4-bit
-exponent code, lossless, 1.33x fewer bytes over the host link) with hipMemcpyAsync on two DMA
-streams, and a kernel unpacks them into the cache slots; the outputs are bit-identical to raw
-fetches.  The timed pass runs without instrumentation; a second pass over the same stream
+misses as packed rows (OffloadRuntime(pack=True): per value a sign|mantissa byte and a 3-bit
+exponent code, the rarer exponents in two escape levels, lossless, 1.44x fewer bytes over the
+host link) with hipMemcpyAsync on two DMA streams, and a kernel unpacks them into the cache
+slots; the outputs are bit-identical to raw fetches.  The timed pass runs without instrumentation; a second pass over the same stream
 (from an empty cache again) collects per-launch kernel times, fetch events and host phase
 times.
 
@@ -615,9 +615,9 @@ def main():
         link_gbs=(dec['copies'] * pk['packed_bytes'] / pk['packed_rows'])
         / (dec['fetch_ms'] * 1e-3) / 1e9 if dec['fetch_ms'] else None,
         note='the misses cross the host link as packed rows (per value a sign|mantissa byte and '
-             'a 4-bit exponent code, lossless) into staging buffers and are unpacked into the '
-             'cache slots on the GPU; h2d_gbs counts expert bytes delivered, link_gbs the '
-             'packed bytes copied')
+             'a 3-bit exponent code, escapes in two more levels, lossless) into staging buffers '
+             'and are unpacked into the cache slots on the GPU; h2d_gbs counts expert bytes '
+             'delivered, link_gbs the packed bytes copied')
     line = dict(
         metric='MoE-layer tokens/sec (Qwen3-30B-A3B-shaped decode layer, 16 tok/step, 38/128 cached)',
         value=dec['tokens'] / dec['elapsed'], unit='tokens/s', n_gpus=1, steps=args.steps,

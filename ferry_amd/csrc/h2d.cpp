@@ -179,12 +179,25 @@ extern "C" int ferry_h2d_destroy(ferry_h2d* h) {
   return 0;
 }
 
-// Packed bytes after which a sub-batch of a packed fetch closes: its unpack then runs while the
-// lanes copy the next sub-batch (about one expert row of the models served here).
+// Sub-batches of a packed fetch, counted from the call's end: the last holds about
+// kSubBatchBytes, the one before it about twice that, and so on.  Only the last sub-batch's
+// unpack follows the call's last copy (the others run while the lanes copy the rest), and a
+// call of B bytes costs about log2(B / kSubBatchBytes) sets of launches and waits.
 constexpr int64_t kSubBatchBytes = int64_t(4) << 20;
 
-// DMA fetch on a packed pool.  The call's rows go in sub-batches of about kSubBatchBytes (at
-// most kUnpackRows packed rows, at most one per staging buffer, no slot twice): the sub-batch's
+// floor(log2(remaining / kSubBatchBytes + 1)): a sub-batch closes where this drops
+static int sub_batch_level(int64_t remaining) {
+  int64_t q = remaining / kSubBatchBytes + 1;
+  int level = 0;
+  while (q > 1) {
+    q >>= 1;
+    ++level;
+  }
+  return level;
+}
+
+// DMA fetch on a packed pool.  The call's rows go in sub-batches (above; also at most
+// kUnpackRows packed rows, at most one per staging buffer, no slot twice): the sub-batch's
 // packed rows, concatenated, are cut into kLanes equal byte ranges that the lanes copy into
 // staging buffers (rows that stayed raw go straight into their slots); the unpack stream waits
 // for both lanes' copies of the sub-batch and runs one unpack launch that writes the slots, and
@@ -200,6 +213,8 @@ static int fetch_packed(ferry_h2d* h, const int64_t* slots, const int64_t* keys,
   const int64_t rb = h->row_bytes;
   const ferry_packed_pool* pp = h->packed;
   const int64_t per_batch = h->ring_rows < ferry::kUnpackRows ? h->ring_rows : ferry::kUnpackRows;
+  int64_t remaining = 0;   // bytes of the call not yet in a sub-batch
+  for (int64_t i = 0; i < n; ++i) remaining += pp->size[(size_t)keys[i]];
   int64_t i0 = 0;
   while (i0 < n) {
     std::vector<Seg> segs;
@@ -207,8 +222,9 @@ static int fetch_packed(ferry_h2d* h, const int64_t* slots, const int64_t* keys,
     ul.n_rows = 0;
     std::vector<int64_t> entries;
     int64_t i1 = i0, total = 0;
+    const int level = sub_batch_level(remaining);
     ++h->batch;   // a slot named twice starts a new sub-batch, so that the later row wins
-    for (; i1 < n && (i1 == i0 || total < kSubBatchBytes); ++i1) {
+    for (; i1 < n && (i1 == i0 || sub_batch_level(remaining - total) == level); ++i1) {
       const int64_t key = keys[i1];
       if (h->batch_of[(size_t)slots[i1]] == h->batch) break;
       char* slot_ptr = h->cache + slots[i1] * rb;
@@ -274,6 +290,7 @@ static int fetch_packed(ferry_h2d* h, const int64_t* slots, const int64_t* keys,
     }
     for (int64_t k : entries) h->ring_ev[(size_t)k] = ev;
     h->copies += i1 - i0;
+    remaining -= total;
     i0 = i1;
   }
   return 0;

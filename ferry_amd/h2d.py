@@ -140,8 +140,10 @@ class H2DEngine:
 
 class PackedPool:
     """A lossless packed copy of a pool for the host link (ferry_pack_pool), in pinned memory:
-    per value a sign|mantissa byte and a 4-bit exponent code, 12 bits instead of 16 for weights
-    that span few binades (rows that would not shrink are kept raw).  The source pool may be
+    per value a sign|mantissa byte and a 3-bit exponent code against the row's 7 most populated
+    exponents, the rest as 4-bit codes against a second window of 15 or in an (index, exponent)
+    list -- about 11.1 bits instead of 16 for weights that span few binades (rows that would
+    not shrink are kept raw; rows hold a multiple of 32 values).  The source pool may be
     pageable and may be freed afterwards; engines fetch from the packed pool alone
     (``H2DEngine.from_packed``) or attach it to an engine of the same pinned pool
     (``use_packed``)."""
