@@ -591,6 +591,43 @@ def test_h2d_packed_pool_fetch_byte_exact(device):
     alone.close()
 
 
+def test_h2d_packed_sub_batches_and_ring_reuse(device):
+    """Calls large enough to go in several sub-batches (about 4, 8, 16 MiB from the call's end),
+    each unpacked on the engine's unpack stream while the DMA lanes copy the next: 12 rows of
+    ~2.8 MiB packed through a ring of 3 staging buffers (every staging buffer is reused inside
+    a call, after the unpack that read it), a call naming a slot twice, calls back to back
+    without a host wait, a raw row among packed ones, and a GPU-side wait on the caller's
+    stream -- every slot holds the pool row's exact bytes."""
+    from ferry_amd.h2d import H2DEngine, PackedPool
+    rows, cap, width = 16, 14, (1 << 21) + 8192
+    g = torch.Generator().manual_seed(5)
+    pool = (torch.randn((rows, width), generator=g) * 0.02).to(torch.bfloat16)
+    pool[6] = torch.randint(-32768, 32767, (width,), generator=g, dtype=torch.int16).view(torch.bfloat16)
+    pool[11] = _spread_block(pool[11], 7, 500, g)
+    packed = PackedPool(pool, threads=8)
+    assert packed.packed_rows == rows - 1
+    cache = torch.zeros((cap, width), dtype=torch.bfloat16, device=device)
+    eng = H2DEngine.from_packed(cache, packed, ring_rows=3)
+    bits = lambda t: t.view(torch.int16)   # noqa: E731
+    keys = np.array([0, 6, 1, 2, 11, 3, 4, 5, 7, 8, 9, 10])
+    eng.fetch(np.arange(12), keys)
+    eng.fetch([12, 13, 12], [13, 14, 15])      # back to back; slot 12 twice: row 15 wins
+    eng.wait_host(np.arange(cap))
+    want = pool[np.concatenate([keys, [15, 14]])]
+    assert torch.equal(bits(cache.cpu()), bits(want))
+    # overwrite every slot in one call (reverse order) and read it on another stream
+    keys2 = np.arange(cap)[::-1].copy()
+    eng.fetch(np.arange(cap), keys2)
+    consumer = torch.cuda.Stream()
+    eng.wait_stream(np.arange(cap), consumer)
+    with torch.cuda.stream(consumer):
+        snap = cache.clone()
+    torch.cuda.synchronize()
+    assert torch.equal(bits(snap.cpu()), bits(pool[keys2]))
+    eng.close()
+    packed.close()
+
+
 @pytest.mark.parametrize('width', [2 * 8192 + 96, 32, 8192])
 def test_h2d_packed_pool_ragged_widths(device, width):
     """Packed rows whose length is not a whole number of 8192-value blocks (a partial last
