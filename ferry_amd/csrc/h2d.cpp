@@ -40,7 +40,8 @@ void set_error(const char* fmt, ...);
 void clear_error();
 hipError_t h2d_copy_launch(const void* pool, void* cache, int64_t row_bytes, const int64_t* keys,
                            const int64_t* slots, int64_t n, hipStream_t stream);
-hipError_t h2d_unpack_launch(const UnpackList& list, int64_t n, hipStream_t stream);
+hipError_t h2d_unpack_launch(const UnpackList& list, int64_t n, hipStream_t stream,
+                             int64_t max_groups);
 void pack_plan_rows(const uint16_t* pool, int64_t rows, int64_t n, int threads, PackPlan* plan);
 void pack_write_rows(const uint16_t* pool, int64_t rows, int64_t n, int threads,
                      const PackPlan* plan, const int64_t* off, uint8_t* dst);
@@ -48,16 +49,56 @@ void pack_write_rows(const uint16_t* pool, int64_t rows, int64_t n, int threads,
 
 namespace {
 
+// The engine's events order work of one device (copies after the reads of a slot, reads after
+// its copies): none needs a system-scope fence, and leaving it out shortens every wait on them.
+constexpr unsigned kEventFlags = hipEventDisableTiming | hipEventDisableSystemFence;
+
 struct Event {
   hipEvent_t e = nullptr;
+  hipStream_t stream = nullptr;   // the stream it was recorded on
+  int64_t order = 0;              // record order among the engine's events
   ~Event() {
     if (e) (void)hipEventDestroy(e);
   }
 };
 
+// Of the events in `evs` (nulls allowed), those worth a wait: per stream only the newest, as a
+// stream's events fire in record order; events that have fired already are dropped.  Returns
+// false (error set) when a query fails.
+bool pending_events(const std::vector<const std::shared_ptr<Event>*>& evs,
+                    std::vector<hipEvent_t>* out) {
+  std::vector<const Event*> newest;
+  for (const std::shared_ptr<Event>* p : evs) {
+    const Event* ev = p->get();
+    if (!ev) continue;
+    bool merged = false;
+    for (const Event*& n : newest)
+      if (n == ev || n->stream == ev->stream) {
+        if (ev->order > n->order) n = ev;
+        merged = true;
+        break;
+      }
+    if (!merged) newest.push_back(ev);
+  }
+  for (const Event* ev : newest) {
+    const hipError_t q = hipEventQuery(ev->e);
+    if (q == hipErrorNotReady) {
+      (void)hipGetLastError();  // a pending event is not an error
+      out->push_back(ev->e);
+    } else if (q != hipSuccess) {
+      ferry::set_error("hipEventQuery failed: %s", hipGetErrorString(q));
+      return false;
+    }
+  }
+  return true;
+}
+
 }  // namespace
 
 constexpr int kLanes = 2;
+// workgroups of a kernel-mode unpack launch (reads over the link): a few hundred workgroups
+// keep far more reads in flight than the link's latency needs
+constexpr int64_t kLinkUnpackGroups = 256;
 
 // The packed copy of a pool (ferry_pack_pool): pinned host memory holding every row, packed or
 // (when packing would not shrink it) raw, and per row its offset, size and form.  An engine
@@ -66,6 +107,7 @@ struct ferry_packed_pool {
   const char* pool = nullptr;         // the pool it was made from (for ferry_h2d_use_packed)
   int64_t rows = 0, row_bytes = 0;
   uint8_t* data = nullptr;
+  const uint8_t* data_dev = nullptr;  // device mapping of data (null: DMA fetches only)
   std::vector<int64_t> off, size;
   std::vector<uint8_t> raw;           // per row: 1 when stored raw
   int64_t bytes = 0, packed_rows = 0, packed_bytes = 0, largest = 0;
@@ -97,12 +139,32 @@ struct ferry_h2d {
   std::vector<std::shared_ptr<Event>> copy_done[kLanes];  // per lane, per slot
   std::vector<int64_t> copy_seq;      // per slot: sequence number of its last copy, -1 if none
   std::vector<std::shared_ptr<Event>> used;  // per slot: last compute that read it
+  std::shared_ptr<Event> marker;      // the latest event of ferry_h2d_mark_used_record
   int64_t seq = 0;
+  int64_t order = 0;                  // events recorded so far
   int64_t copies = 0;
 };
 
-// the copy kernel addresses 16-byte units through 32-bit row indices
+// a new engine event recorded on stream s
+static hipError_t record_event(ferry_h2d* h, hipStream_t s, std::shared_ptr<Event>* out,
+                               unsigned flags = kEventFlags) {
+  auto ev = std::make_shared<Event>();
+  hipError_t r = hipEventCreateWithFlags(&ev->e, flags);
+  if (r == hipSuccess) r = hipEventRecord(ev->e, s);
+  if (r != hipSuccess) return r;
+  ev->stream = s;
+  ev->order = ++h->order;
+  *out = std::move(ev);
+  return hipSuccess;
+}
+
+// the copy kernel addresses 16-byte units through 32-bit row indices; with a packed pool the
+// unpack kernel reads the pool's device mapping instead (rows of a multiple of 32 values, each
+// stored at a 256-byte multiple)
 static bool kernel_copy_ok(const ferry_h2d* h) {
+  if (h->packed)
+    return h->packed->data_dev && (uintptr_t)h->packed->data_dev % 256 == 0 &&
+           (uintptr_t)h->cache % 16 == 0;
   return h->pool_dev && h->row_bytes % 16 == 0 && (uintptr_t)h->pool_dev % 16 == 0 &&
          (uintptr_t)h->cache % 16 == 0 && h->pool_rows < (int64_t(1) << 31) &&
          h->cache_rows < (int64_t(1) << 31);
@@ -146,10 +208,10 @@ extern "C" int ferry_h2d_create(void* cache, int64_t cache_rows, const void* poo
     H2D_HIP(hipStreamCreateWithFlags(&h->stream[l], hipStreamNonBlocking));
     h->copy_done[l].assign((size_t)cache_rows, nullptr);
   }
-  H2D_HIP(hipEventCreateWithFlags(&h->join, hipEventDisableTiming));
+  H2D_HIP(hipEventCreateWithFlags(&h->join, kEventFlags));
   H2D_HIP(hipStreamCreateWithFlags(&h->unpack, hipStreamNonBlocking));
   for (int l = 0; l < kLanes; ++l)
-    H2D_HIP(hipEventCreateWithFlags(&h->lane_done[l], hipEventDisableTiming));
+    H2D_HIP(hipEventCreateWithFlags(&h->lane_done[l], kEventFlags));
   h->kernel_stream = h->stream[0];
   h->copy_seq.assign((size_t)cache_rows, -1);
   h->batch_of.assign((size_t)cache_rows, 0);
@@ -244,6 +306,7 @@ static int fetch_packed(ferry_h2d* h, const int64_t* slots, const int64_t* keys,
       total += pp->size[(size_t)key];
       ul.src[ul.n_rows] = (const uint8_t*)st;
       ul.dst[ul.n_rows] = (uint16_t*)slot_ptr;
+      ul.raw[ul.n_rows] = 0;
       ++ul.n_rows;
       entries.push_back(k);
     }
@@ -280,10 +343,9 @@ static int fetch_packed(ferry_h2d* h, const int64_t* slots, const int64_t* keys,
       H2D_HIP(hipEventRecord(h->lane_done[l], h->stream[l]));
       H2D_HIP(hipStreamWaitEvent(h->unpack, h->lane_done[l], 0));
     }
-    if (ul.n_rows > 0) H2D_HIP(ferry::h2d_unpack_launch(ul, rb / 2, h->unpack));
-    auto ev = std::make_shared<Event>();
-    H2D_HIP(hipEventCreateWithFlags(&ev->e, hipEventDisableTiming));
-    H2D_HIP(hipEventRecord(ev->e, h->unpack));
+    if (ul.n_rows > 0) H2D_HIP(ferry::h2d_unpack_launch(ul, rb / 2, h->unpack, 0));
+    std::shared_ptr<Event> ev;
+    H2D_HIP(record_event(h, h->unpack, &ev));
     for (int64_t i = i0; i < i1; ++i) {
       for (int l = 0; l < kLanes; ++l) h->copy_done[l][(size_t)slots[i]] = ev;
       h->copy_seq[(size_t)slots[i]] = h->seq++;
@@ -303,22 +365,8 @@ extern "C" int ferry_h2d_fetch(ferry_h2d* h, const int64_t* slots, const int64_t
   // What a copy into a slot must follow: the last compute that read the slot (WAR) and any
   // earlier copy into it still in flight, on whichever lane or stream (WAW).  Events that have
   // fired when the call is made add no wait.
-  std::vector<hipEvent_t> pending, checked;
-  auto note = [&](const std::shared_ptr<Event>& ev) -> bool {
-    if (!ev) return true;
-    for (hipEvent_t e : checked)
-      if (e == ev->e) return true;
-    checked.push_back(ev->e);
-    const hipError_t q = hipEventQuery(ev->e);
-    if (q == hipErrorNotReady) {
-      (void)hipGetLastError();  // a pending event is not an error
-      pending.push_back(ev->e);
-    } else if (q != hipSuccess) {
-      ferry::set_error("hipEventQuery failed: %s", hipGetErrorString(q));
-      return false;
-    }
-    return true;
-  };
+  std::vector<hipEvent_t> pending;
+  std::vector<const std::shared_ptr<Event>*> evs;
   for (int64_t i = 0; i < n; ++i) {
     const int64_t slot = slots[i], key = keys[i];
     if (slot < 0 || slot >= h->cache_rows || key < 0 || key >= h->pool_rows) {
@@ -326,33 +374,56 @@ extern "C" int ferry_h2d_fetch(ferry_h2d* h, const int64_t* slots, const int64_t
                        (long long)key);
       return 2;
     }
-    if (!note(h->used[(size_t)slot])) return 3;
-    for (int l = 0; l < kLanes; ++l)
-      if (!note(h->copy_done[l][(size_t)slot])) return 3;
+    evs.push_back(&h->used[(size_t)slot]);
+    for (int l = 0; l < kLanes; ++l) evs.push_back(&h->copy_done[l][(size_t)slot]);
   }
+  if (!pending_events(evs, &pending)) return 3;
   if (h->kind == FERRY_H2D_KERNEL) {
     hipStream_t s = h->kernel_stream;
     for (hipEvent_t e : pending) H2D_HIP(hipStreamWaitEvent(s, e, 0));
     // rows of one launch run concurrently: a slot named twice in the call starts a new
     // launch, so that the later row wins, as with copies in stream order
-    int64_t b0 = 0;
-    ++h->batch;
-    for (int64_t i = 0; i <= n; ++i) {
-      if (i < n && h->batch_of[(size_t)slots[i]] != h->batch) {
+    if (h->packed) {
+      // unpack launches that read the packed rows over the link and write the slots
+      const ferry_packed_pool* pp = h->packed;
+      ferry::UnpackList ul;
+      ul.n_rows = 0;
+      ++h->batch;
+      for (int64_t i = 0; i <= n; ++i) {
+        const bool flush = i == n || h->batch_of[(size_t)slots[i]] == h->batch ||
+                           ul.n_rows == ferry::kUnpackRows;
+        if (flush && ul.n_rows > 0) {
+          H2D_HIP(ferry::h2d_unpack_launch(ul, h->row_bytes / 2, s, kLinkUnpackGroups));
+          ul.n_rows = 0;
+          ++h->batch;
+        }
+        if (i == n) break;
+        const int64_t key = keys[i];
         h->batch_of[(size_t)slots[i]] = h->batch;
-        continue;
+        ul.src[ul.n_rows] = pp->data_dev + pp->off[(size_t)key];
+        ul.dst[ul.n_rows] = (uint16_t*)(h->cache + slots[i] * h->row_bytes);
+        ul.raw[ul.n_rows] = pp->raw[(size_t)key];
+        ++ul.n_rows;
       }
-      H2D_HIP(ferry::h2d_copy_launch(h->pool_dev, h->cache, h->row_bytes, keys + b0, slots + b0,
-                                     i - b0, s));
-      if (i < n) {
-        ++h->batch;
-        h->batch_of[(size_t)slots[i]] = h->batch;
+    } else {
+      int64_t b0 = 0;
+      ++h->batch;
+      for (int64_t i = 0; i <= n; ++i) {
+        if (i < n && h->batch_of[(size_t)slots[i]] != h->batch) {
+          h->batch_of[(size_t)slots[i]] = h->batch;
+          continue;
+        }
+        H2D_HIP(ferry::h2d_copy_launch(h->pool_dev, h->cache, h->row_bytes, keys + b0,
+                                       slots + b0, i - b0, s));
+        if (i < n) {
+          ++h->batch;
+          h->batch_of[(size_t)slots[i]] = h->batch;
+        }
+        b0 = i;
       }
-      b0 = i;
     }
-    auto ev = std::make_shared<Event>();
-    H2D_HIP(hipEventCreateWithFlags(&ev->e, hipEventDisableTiming));
-    H2D_HIP(hipEventRecord(ev->e, s));
+    std::shared_ptr<Event> ev;
+    H2D_HIP(record_event(h, s, &ev));
     for (int l = 0; l < kLanes; ++l)
       for (int64_t i = 0; i < n; ++i) h->copy_done[l][(size_t)slots[i]] = ev;
     bool known = false;
@@ -407,9 +478,8 @@ extern "C" int ferry_h2d_fetch(ferry_h2d* h, const int64_t* slots, const int64_t
     }
   }
   for (int l = 0; l < kLanes; ++l) {
-    auto ev = std::make_shared<Event>();
-    H2D_HIP(hipEventCreateWithFlags(&ev->e, hipEventDisableTiming));
-    H2D_HIP(hipEventRecord(ev->e, h->stream[l]));
+    std::shared_ptr<Event> ev;
+    H2D_HIP(record_event(h, h->stream[l], &ev));
     for (int64_t i = 0; i < n; ++i) h->copy_done[l][(size_t)slots[i]] = ev;
   }
   for (int64_t i = 0; i < n; ++i) h->copy_seq[(size_t)slots[i]] = h->seq++;
@@ -439,9 +509,9 @@ extern "C" int ferry_h2d_wait_host(ferry_h2d* h, const int64_t* slots, int64_t n
 extern "C" int ferry_h2d_wait_stream(ferry_h2d* h, const int64_t* slots, int64_t n,
                                      void* stream) {
   ferry::clear_error();
-  // every still-running copy into the slots, each event once (copies into different slots
-  // are not ordered with each other: DMA lanes, kernel-mode streams)
-  std::vector<hipEvent_t> seen;
+  // every still-running copy into the slots: per copy stream its newest such copy (copies into
+  // different slots are not ordered with each other: DMA lanes, kernel-mode streams)
+  std::vector<const std::shared_ptr<Event>*> evs;
   for (int64_t i = 0; i < n; ++i) {
     const int64_t slot = slots[i];
     if (slot < 0 || slot >= h->cache_rows) {
@@ -449,31 +519,19 @@ extern "C" int ferry_h2d_wait_stream(ferry_h2d* h, const int64_t* slots, int64_t
       return 2;
     }
     if (h->copy_seq[(size_t)slot] < 0) continue;
-    for (int l = 0; l < kLanes; ++l) {
-      const hipEvent_t e = h->copy_done[l][(size_t)slot]->e;
-      bool dup = false;
-      for (hipEvent_t x : seen) dup = dup || x == e;
-      if (dup) continue;
-      seen.push_back(e);
-      const hipError_t q = hipEventQuery(e);
-      if (q == hipSuccess) continue;
-      if (q != hipErrorNotReady) {
-        ferry::set_error("hipEventQuery failed: %s", hipGetErrorString(q));
-        return 3;
-      }
-      (void)hipGetLastError();
-      H2D_HIP(hipStreamWaitEvent((hipStream_t)stream, e, 0));
-    }
+    for (int l = 0; l < kLanes; ++l) evs.push_back(&h->copy_done[l][(size_t)slot]);
   }
+  std::vector<hipEvent_t> pending;
+  if (!pending_events(evs, &pending)) return 3;
+  for (hipEvent_t e : pending) H2D_HIP(hipStreamWaitEvent((hipStream_t)stream, e, 0));
   return 0;
 }
 
 extern "C" int ferry_h2d_mark_used(ferry_h2d* h, const int64_t* slots, int64_t n, void* stream) {
   ferry::clear_error();
   if (n == 0) return 0;
-  auto ev = std::make_shared<Event>();
-  H2D_HIP(hipEventCreateWithFlags(&ev->e, hipEventDisableTiming));
-  H2D_HIP(hipEventRecord(ev->e, (hipStream_t)stream));
+  std::shared_ptr<Event> ev;
+  H2D_HIP(record_event(h, (hipStream_t)stream, &ev));
   for (int64_t i = 0; i < n; ++i) {
     const int64_t slot = slots[i];
     if (slot < 0 || slot >= h->cache_rows) {
@@ -482,6 +540,38 @@ extern "C" int ferry_h2d_mark_used(ferry_h2d* h, const int64_t* slots, int64_t n
     }
     h->used[(size_t)slot] = ev;
   }
+  return 0;
+}
+
+extern "C" int ferry_h2d_mark_used_record(ferry_h2d* h, const int64_t* slots, int64_t n,
+                                          void* stream, void** event_out) {
+  ferry::clear_error();
+  if (!h || !event_out || n < 0) {
+    ferry::set_error("h2d_mark_used_record: bad arguments");
+    return 2;
+  }
+  for (int64_t i = 0; i < n; ++i)
+    if (slots[i] < 0 || slots[i] >= h->cache_rows) {
+      ferry::set_error("h2d_mark_used_record: slot %lld out of range", (long long)slots[i]);
+      return 2;
+    }
+  // a system-scope release, so that the host may read what the stream's kernels wrote to host
+  // memory once the event has fired
+  std::shared_ptr<Event> ev;
+  H2D_HIP(record_event(h, (hipStream_t)stream, &ev, hipEventDisableTiming));
+  for (int64_t i = 0; i < n; ++i) h->used[(size_t)slots[i]] = ev;
+  h->marker = ev;
+  *event_out = (void*)ev->e;
+  return 0;
+}
+
+extern "C" int ferry_h2d_event_synchronize(ferry_h2d* h, void* event) {
+  ferry::clear_error();
+  if (!h || !event) {
+    ferry::set_error("h2d_event_synchronize: bad arguments");
+    return 2;
+  }
+  H2D_HIP(hipEventSynchronize((hipEvent_t)event));
   return 0;
 }
 
@@ -561,6 +651,11 @@ extern "C" int ferry_pack_pool(const void* pool, int64_t rows, int64_t row_bytes
     void* mem = nullptr;
     H2D_HIP(hipHostMalloc(&mem, (size_t)pp->bytes, 0));
     pp->data = (uint8_t*)mem;
+    void* dev = nullptr;
+    if (hipHostGetDevicePointer(&dev, mem, 0) == hipSuccess)
+      pp->data_dev = (const uint8_t*)dev;
+    else
+      (void)hipGetLastError();   // no device mapping: DMA fetches only
     ferry::pack_write_rows((const uint16_t*)pool, rows, n, threads, plan.data(), pack_off.data(),
                            pp->data);
     for (int64_t i = 0; i < rows; ++i)
@@ -620,7 +715,10 @@ static int ferry_h2d_use_packed_any(ferry_h2d* h, const ferry_packed_pool* pp,
   }
   h->packed = nullptr;
   h->ring_rows = h->entry_bytes = h->ring_next = 0;
-  if (!pp) return 0;
+  if (!pp) {
+    if (h->kind == FERRY_H2D_KERNEL && !kernel_copy_ok(h)) h->kind = FERRY_H2D_DMA;
+    return 0;
+  }
   if (pp->packed_rows > 0) {
     void* rg = nullptr;
     H2D_HIP(hipMalloc(&rg, (size_t)(ring_rows * pp->largest)));
@@ -632,6 +730,7 @@ static int ferry_h2d_use_packed_any(ferry_h2d* h, const ferry_packed_pool* pp,
     h->ring_rows = 1;   // batches are never cut by the staging ring
   }
   h->packed = pp;
+  if (h->kind == FERRY_H2D_KERNEL && !kernel_copy_ok(h)) h->kind = FERRY_H2D_DMA;
   return 0;
 }
 
@@ -657,10 +756,10 @@ extern "C" int ferry_h2d_create_packed(void* cache, int64_t cache_rows,
     H2D_HIP(hipStreamCreateWithFlags(&h->stream[l], hipStreamNonBlocking));
     h->copy_done[l].assign((size_t)cache_rows, nullptr);
   }
-  H2D_HIP(hipEventCreateWithFlags(&h->join, hipEventDisableTiming));
+  H2D_HIP(hipEventCreateWithFlags(&h->join, kEventFlags));
   H2D_HIP(hipStreamCreateWithFlags(&h->unpack, hipStreamNonBlocking));
   for (int l = 0; l < kLanes; ++l)
-    H2D_HIP(hipEventCreateWithFlags(&h->lane_done[l], hipEventDisableTiming));
+    H2D_HIP(hipEventCreateWithFlags(&h->lane_done[l], kEventFlags));
   h->kernel_stream = h->stream[0];
   h->copy_seq.assign((size_t)cache_rows, -1);
   h->batch_of.assign((size_t)cache_rows, 0);

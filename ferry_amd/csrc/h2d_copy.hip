@@ -66,15 +66,35 @@ __device__ __forceinline__ uint32_t level3_global(const uint32_t* idx, const uin
   return ex[lo];
 }
 
-__global__ __launch_bounds__(kUnpackThreads) void unpack_kernel(UnpackList list, int64_t n) {
-  __shared__ uint8_t lds_c[kPackBlock / 2 + 16];
-  __shared__ uint16_t lds_li[kL3Lds];
-  __shared__ uint8_t lds_le[kL3Lds];
-  __shared__ uint32_t lds_wave[kUnpackThreads / 64];
-  const int r = blockIdx.y;
-  const int64_t blk = blockIdx.x;
+struct UnpackLds {
+  uint8_t c[kPackBlock / 2 + 16];
+  uint16_t li[kL3Lds];
+  uint8_t le[kL3Lds];
+  uint32_t wave[kUnpackThreads / 64];
+};
+
+// block blk of row r of the list
+__device__ __forceinline__ void unpack_block(const UnpackList& list, int64_t n, int r, int64_t blk,
+                                             UnpackLds& lds) {
+  uint8_t* lds_c = lds.c;
+  uint16_t* lds_li = lds.li;
+  uint8_t* lds_le = lds.le;
+  uint32_t* lds_wave = lds.wave;
   const int t = threadIdx.x;
   const uint8_t* src = list.src[r];
+  if (list.raw[r]) {   // a row kept raw: the workgroup copies its block's 16 KiB as they are
+    const int64_t v = blk * kPackBlock + 32 * t;
+    if (v < n) {
+      const u32x4* s = reinterpret_cast<const u32x4*>(src + 2 * v);
+      u32x4* d = reinterpret_cast<u32x4*>(list.dst[r] + v);
+      const u32x4 x0 = s[0], x1 = s[1], x2 = s[2], x3 = s[3];
+      d[0] = x0;
+      d[1] = x1;
+      d[2] = x2;
+      d[3] = x3;
+    }
+    return;
+  }
   const PackHeader* hd = reinterpret_cast<const PackHeader*>(src);
   const uint32_t base1 = hd->base1, base2 = hd->base2;
   const PackOffsets o = pack_offsets(n, (int64_t)hd->esc1, (int64_t)hd->esc2);
@@ -162,14 +182,32 @@ __global__ __launch_bounds__(kUnpackThreads) void unpack_kernel(UnpackList list,
   for (int h = 0; h < 4; ++h) dst[h] = u32x4{w[4 * h], w[4 * h + 1], w[4 * h + 2], w[4 * h + 3]};
 }
 
+// Workgroup g takes blocks g, g + G, g + 2G, ... (G = gridDim.x) of the list's rows in row
+// order.  With one workgroup per block (staging buffers in HBM) every block is dispatched at
+// once; a packed pool read over the link is served by a few hundred workgroups that loop,
+// which leaves the CUs' other slots to kernels running beside the fetch.
+__global__ __launch_bounds__(kUnpackThreads) void unpack_kernel(UnpackList list, int64_t n) {
+  __shared__ UnpackLds lds;
+  const int64_t blocks = (n + kPackBlock - 1) / kPackBlock;
+  const int64_t items = blocks * list.n_rows;
+  for (int64_t it = blockIdx.x; it < items; it += gridDim.x) {
+    const int r = (int)(it / blocks);
+    unpack_block(list, n, r, it - r * blocks, lds);
+    __syncthreads();   // the next block rewrites the LDS slices
+  }
+}
+
 }  // namespace
 
-// Unpacks list.n_rows packed rows of n values each (n a multiple of 32), on `stream`.
-hipError_t h2d_unpack_launch(const UnpackList& list, int64_t n, hipStream_t stream) {
+// Unpacks list.n_rows packed rows of n values each (n a multiple of 32), on `stream`, with at
+// most max_groups workgroups (0: one per block).
+hipError_t h2d_unpack_launch(const UnpackList& list, int64_t n, hipStream_t stream,
+                             int64_t max_groups) {
   if (list.n_rows <= 0) return hipSuccess;
-  const int64_t blocks = (n + kPackBlock - 1) / kPackBlock;
-  hipLaunchKernelGGL(unpack_kernel, dim3((unsigned)blocks, (unsigned)list.n_rows),
-                     dim3(kUnpackThreads), 0, stream, list, n);
+  const int64_t items = (n + kPackBlock - 1) / kPackBlock * list.n_rows;
+  const int64_t groups = max_groups > 0 && max_groups < items ? max_groups : items;
+  hipLaunchKernelGGL(unpack_kernel, dim3((unsigned)groups), dim3(kUnpackThreads), 0, stream, list,
+                     n);
   return hipGetLastError();
 }
 

@@ -80,8 +80,10 @@ constexpr int kUnpackRows = 64;   // rows per unpack launch
 
 // kernel argument of one unpack launch
 struct UnpackList {
-  const uint8_t* src[kUnpackRows];  // packed rows (device staging buffers)
+  const uint8_t* src[kUnpackRows];  // packed rows: device staging buffers, or the packed pool
+                                    // itself through its device mapping (read over the link)
   uint16_t* dst[kUnpackRows];       // cache slots
+  uint8_t raw[kUnpackRows];         // 1: src holds the row's bf16 values as they are
   int32_t n_rows;
 };
 

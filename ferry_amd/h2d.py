@@ -81,6 +81,21 @@ class H2DEngine:
         check(lib().ferry_h2d_mark_used(self._h, s.ctypes.data, len(s), st.cuda_stream),
               'H2DEngine.mark_used')
 
+    def mark_used_record(self, slots, stream=None):
+        """mark_used and a host-waitable event in one record on ``stream``: returns the
+        event's handle (owned by the engine, valid until the next call of this method), for
+        ``event_synchronize``."""
+        s = _i64(slots)
+        st = stream if stream is not None else torch.cuda.current_stream(self._cache.device)
+        ev = ctypes.c_void_p()
+        check(lib().ferry_h2d_mark_used_record(self._h, s.ctypes.data, len(s), st.cuda_stream,
+                                               ctypes.byref(ev)), 'H2DEngine.mark_used_record')
+        return ev.value
+
+    def event_synchronize(self, event):
+        """Block the host until an event of ``mark_used_record`` has fired."""
+        check(lib().ferry_h2d_event_synchronize(self._h, event), 'H2DEngine.event_synchronize')
+
     def synchronize(self):
         check(lib().ferry_h2d_synchronize(self._h), 'H2DEngine.synchronize')
 

@@ -93,6 +93,7 @@ class OffloadRuntime:
 
     def reset(self):
         """Empty expert cache and routing history (start of every measured run)."""
+        self._flush_used()
         if self.h2d is not None:
             self.h2d.synchronize()
         torch.cuda.synchronize(self.device)
@@ -172,19 +173,37 @@ class OffloadRuntime:
         if not frequency:
             tail = min(T, self.window)
             tail_host = probs_tail[-tail:].float().to('cpu', non_blocking=True)
-        d2h = torch.cuda.Event(enable_timing=self.timing)
-        d2h.record(stream)
+        if self.timing:
+            d2h = torch.cuda.Event(enable_timing=True)
+            d2h.record(stream)
+            self._flush_used()
+            wait_ids = d2h.synchronize
+        else:
+            # one event both releases the IDs to the host and marks the slots that the previous
+            # call read on this stream (no event of their own between that call's kernels)
+            pend = self._pending_used
+            if pend is not None and pend[1] != stream.cuda_stream:
+                self._flush_used()
+                pend = None
+            self._pending_used = None
+            ids_event = self.h2d.mark_used_record(pend[0] if pend is not None else [], stream)
+            wait_ids = lambda: self.h2d.event_synchronize(ids_event)   # noqa: E731
 
         # 2. layout (overlaps the host planning)
         buf['layout'] = self.ops.layout(selected, weights, E, out=buf['layout'])
         lay = buf['layout']
+        chunked = T * k >= CHUNK_MIN_PAIRS
+        on_stream = self.overlap and not chunked and self._kernel_copy
+        if on_stream:
+            # the resident experts will run on the side stream, forked here (before the copy
+            # kernel that the planner queues on this stream)
+            fork = torch.cuda.Event()
+            fork.record(stream)
 
         # 3. plan + fetch
         t_sync = time.perf_counter_ns()
-        d2h.synchronize()
+        wait_ids()
         t_ready = time.perf_counter_ns()
-        chunked = T * k >= CHUNK_MIN_PAIRS
-        on_stream = self.overlap and not chunked and self._kernel_copy
         self._set_copy_mode(on_stream, stream)
         # with chunks or timing the copies are queued here; otherwise the planner's native call
         # queues them itself, right after planning
@@ -242,18 +261,35 @@ class OffloadRuntime:
             self.serial_wait_ns += time.perf_counter_ns() - started
         mark = self.ops.timing_mark() if timing else 0
         waits = []
+        shared_out = None
         if on_stream:
-            # the copies are queued on this stream (the wait on their events costs nothing);
-            # resident rows may come from DMA copies of earlier calls
-            active_list = np.flatnonzero(active)
-            self.h2d.wait_stream(slot_of[active_list], stream)
+            # the copy kernel holds this stream; the resident experts (and the shared experts)
+            # run beside it on the side stream, which joins back before the combine (its work is
+            # long done by then, so the join costs no wait); the fetched experts follow the copy
+            # kernel in this stream's order
+            side = self._side()
+            side.wait_event(fork)
+            if len(resident_list):
+                self.h2d.wait_stream(slot_of[resident_list], side)
+                with torch.cuda.stream(side):
+                    self._ffn(common, resident_list, slot32, buf, side, counts_e)
+            if shared is not None:
+                with torch.cuda.stream(side):
+                    shared_out = shared(common[1], out=self._shared_out(T))
+            join = torch.cuda.Event()
+            join.record(side)
             if timing:
                 waits.append((ev[0], ev[1]))   # the copy kernel holds this stream
-            self._ffn(common, active_list, slot32, buf, stream, counts_e)
+            if len(fetches):
+                fetched = np.sort(missing_keys)
+                self.h2d.wait_stream(slot_of[fetched], stream)
+                self._ffn(common, fetched, slot32, buf, stream, counts_e)
+            stream.wait_event(join)
         elif len(resident_list):
             self.h2d.wait_stream(slot_of[resident_list], stream)
             self._ffn(common, resident_list, slot32, buf, stream, counts_e)
-        shared_out = shared(common[1], out=self._shared_out(T)) if shared is not None else None
+        if shared is not None and not on_stream:
+            shared_out = shared(common[1], out=self._shared_out(T))
         if len(fetches) and not on_stream:
             for g in groups:
                 w0 = w1 = None
@@ -266,7 +302,10 @@ class OffloadRuntime:
                     w1.record(stream)
                     waits.append((w0, w1))
                 self._ffn(common, np.sort(missing_keys[g]), slot32, buf, stream, counts_e)
-        self.h2d.mark_used(slot_of[np.flatnonzero(active)], stream)
+        if self.timing:
+            self.h2d.mark_used(slot_of[np.flatnonzero(active)], stream)
+        else:   # marked by the next call's ID event on this stream (or by _flush_used)
+            self._pending_used = (slot_of[np.flatnonzero(active)], stream.cuda_stream, stream)
         if timing:
             self.timings.append((ev, waits, (mark, self.ops.timing_mark())))
             self.step_marks.append((d2h, ev[0], ev[1], waits[-1][1] if waits else None))
@@ -283,6 +322,13 @@ class OffloadRuntime:
             h['enqueue_after_fetch'] += time.perf_counter_ns() - t_fetch
         return out
 
+    def _flush_used(self):
+        """Mark the slots of the last call as read, with an event of their own."""
+        pend = getattr(self, '_pending_used', None)
+        if pend is not None and self.h2d is not None:
+            self.h2d.mark_used(pend[0], pend[2])
+        self._pending_used = None
+
     def _set_copy_mode(self, on_stream, stream):
         """Copy kernel on ``stream`` for on-stream calls, DMA copies otherwise."""
         from .h2d import DMA, KERNEL
@@ -291,6 +337,12 @@ class OffloadRuntime:
             self.h2d.engine = KERNEL if on_stream else DMA
             self.h2d.set_kernel_stream(stream if on_stream else None)
             self._copy_mode = mode
+
+    def _side(self):
+        """The side stream of copy-kernel calls (default priority), made on first use."""
+        if getattr(self, '_side_stream', None) is None:
+            self._side_stream = torch.cuda.Stream(self.device)
+        return self._side_stream
 
     def _shared_out(self, tokens):
         b = self._bufs[tokens]
@@ -347,5 +399,6 @@ class OffloadRuntime:
                     calls=len(plan))
 
     def close(self):
+        self._flush_used()
         if self.h2d is not None:
             self.h2d.synchronize()

@@ -219,6 +219,16 @@ int ferry_h2d_wait_host(ferry_h2d* h, const int64_t* slots, int64_t n);
 int ferry_h2d_wait_stream(ferry_h2d* h, const int64_t* slots, int64_t n, void* stream);
 /* expert_ops.cpp:124-128 */
 int ferry_h2d_mark_used(ferry_h2d* h, const int64_t* slots, int64_t n, void* stream);
+/* mark_used and an event in one record (no counterpart in the reference, which records one
+ * event per mark_used): the slots count as read by the work enqueued on `stream` so far, and
+ * *event_out is that one event, recorded with a system-scope release so that the host can wait
+ * on it (ferry_h2d_event_synchronize) before reading what the stream's kernels wrote to host
+ * memory.  A caller that reads the routing IDs back this way marks the slots of its previous
+ * call without a second event on its stream.  n may be 0.  The engine owns the event; it stays
+ * valid until the next ferry_h2d_mark_used_record call on the engine. */
+int ferry_h2d_mark_used_record(ferry_h2d* h, const int64_t* slots, int64_t n, void* stream,
+                               void** event_out);
+int ferry_h2d_event_synchronize(ferry_h2d* h, void* event);
 /* expert_ops.cpp:130-133 */
 int ferry_h2d_synchronize(ferry_h2d* h);
 /* expert_ops.cpp:135 */

@@ -524,13 +524,17 @@ def _spread_block(row, block, count, g):
     return out
 
 
-def test_h2d_packed_pool_fetch_byte_exact(device):
+@pytest.mark.parametrize('kind', ['dma', 'kernel'])
+def test_h2d_packed_pool_fetch_byte_exact(device, kind):
     """Fetches from a packed pool write the pool rows' exact bytes: Gaussian rows, a row with
     special values (+-0, +-inf, NaN, denormals, huge: escapes), a row with hundreds of
     third-level entries in one block, a row of random bits (left raw);
     calls of 1 to 10 rows through 3 staging buffers (ring reuse inside a call and across calls),
-    a slot named twice, a GPU-side wait, and raw fetches again after detaching."""
+    a slot named twice, a GPU-side wait, and raw fetches again after detaching.  kind 'kernel':
+    the unpack kernel reads the packed rows over the link itself (no staging, no DMA)."""
+    from ferry_amd import h2d
     from ferry_amd.h2d import H2DEngine, PackedPool
+    mode = h2d.KERNEL if kind == 'kernel' else h2d.DMA
     rows, cap, width = 24, 10, 3 * 256 * 128
     g = torch.Generator().manual_seed(21)
     pool = (torch.randn((rows, width), generator=g) * 0.02).to(torch.bfloat16)
@@ -545,6 +549,7 @@ def test_h2d_packed_pool_fetch_byte_exact(device):
     cache = torch.zeros((cap, width), dtype=torch.bfloat16, device=device)
     eng = H2DEngine(cache, pool)
     eng.use_packed(packed, ring_rows=3)
+    eng.engine = mode
     bits = lambda t: t.view(torch.int16)   # noqa: E731
     rng = np.random.default_rng(2)
     for size in (1, 7, 10, 3, 10, 2):
@@ -565,6 +570,7 @@ def test_h2d_packed_pool_fetch_byte_exact(device):
     torch.cuda.synchronize()
     assert torch.equal(bits(snap.cpu()), bits(pool[[12, 11]]))
     eng.use_packed(None)
+    assert eng.engine == mode          # the raw pool serves either kind
     eng.fetch([0, 1], [3, 5])
     eng.wait_host([0, 1])
     assert torch.equal(bits(cache.cpu()[[0, 1]]), bits(pool[[3, 5]]))
@@ -579,6 +585,7 @@ def test_h2d_packed_pool_fetch_byte_exact(device):
     alone = PackedPool(src, threads=4)
     del src
     eng = H2DEngine.from_packed(cache, alone, ring_rows=2)
+    eng.engine = mode
     slots = np.arange(cap)
     keys = rng.choice(rows, cap, replace=False)
     keys[3] = 7
@@ -628,10 +635,12 @@ def test_h2d_packed_sub_batches_and_ring_reuse(device):
     packed.close()
 
 
+@pytest.mark.parametrize('kind', ['dma', 'kernel'])
 @pytest.mark.parametrize('width', [2 * 8192 + 96, 32, 8192])
-def test_h2d_packed_pool_ragged_widths(device, width):
+def test_h2d_packed_pool_ragged_widths(device, width, kind):
     """Packed rows whose length is not a whole number of 8192-value blocks (a partial last
     workgroup), a single 32-value row and one exact block unpack to the pool rows' bytes."""
+    from ferry_amd import h2d
     from ferry_amd.h2d import H2DEngine, PackedPool
     rows, cap = 8, 8
     g = torch.Generator().manual_seed(width)
@@ -641,6 +650,8 @@ def test_h2d_packed_pool_ragged_widths(device, width):
     packed = PackedPool(pool, threads=2)
     cache = torch.zeros((cap, width), dtype=torch.bfloat16, device=device)
     eng = H2DEngine.from_packed(cache, packed, ring_rows=4)
+    if kind == 'kernel':
+        eng.engine = h2d.KERNEL
     keys = np.arange(rows)[::-1].copy()
     eng.fetch(np.arange(cap), keys)
     eng.wait_host(np.arange(cap))
@@ -684,3 +695,44 @@ def test_h2d_kernel_copy_many_rows_and_ragged_widths(device):
             assert torch.equal(bits(cache.cpu()[slots[:50]]), bits(pool[keys[::-1][:50].copy()]))
             assert torch.equal(bits(cache.cpu()[slots[50:60]]), bits(pool[keys[:10]]))
         eng.close()
+
+
+def test_h2d_packed_kernel_mode_many_rows(device):
+    """Kernel-mode packed fetches of more rows than one unpack launch holds (150 rows: three
+    launches), raw rows among them, a slot named twice (a new launch, the later row wins), then
+    DMA-mode packed fetches into the same slots and kernel-mode ones again, ordered by the
+    engine: every slot holds the pool row's exact bytes."""
+    from ferry_amd import h2d
+    from ferry_amd.h2d import H2DEngine, PackedPool
+    rows, cap, width = 180, 160, 4 * 8192 + 64
+    g = torch.Generator().manual_seed(17)
+    pool = (torch.randn((rows, width), generator=g) * 0.02).to(torch.bfloat16)
+    for r in (3, 77, 140):
+        pool[r] = torch.randint(-32768, 32767, (width,), generator=g,
+                                dtype=torch.int16).view(torch.bfloat16)
+    pool[5] = _spread_block(pool[5], 2, 600, g)
+    packed = PackedPool(pool, threads=8)
+    assert packed.packed_rows == rows - 3
+    cache = torch.zeros((cap, width), dtype=torch.bfloat16, device=device)
+    eng = H2DEngine.from_packed(cache, packed, ring_rows=5)
+    eng.engine = h2d.KERNEL
+    bits = lambda t: t.view(torch.int16)   # noqa: E731
+    slots = torch.randperm(cap, generator=g).numpy()[:150]
+    keys = torch.randperm(rows, generator=g).numpy()[:150]
+    keys[:4] = [3, 77, 140, 5]
+    eng.fetch(slots, keys)
+    eng.wait_host(slots)
+    assert torch.equal(bits(cache.cpu()[slots]), bits(pool[keys]))
+    a, b = int(slots[40]), int(slots[41])
+    eng.fetch([a, b, a], [100, 101, 102])      # slot a twice: row 102 wins
+    eng.engine = h2d.DMA
+    eng.fetch(slots[:20], keys[::-1][:20].copy())
+    eng.engine = h2d.KERNEL
+    eng.fetch(slots[20:30], keys[:10])
+    eng.wait_host(np.concatenate([[a, b], slots[:30]]))
+    got = cache.cpu()
+    assert torch.equal(bits(got[[a, b]]), bits(pool[[102, 101]]))
+    assert torch.equal(bits(got[slots[:20]]), bits(pool[keys[::-1][:20].copy()]))
+    assert torch.equal(bits(got[slots[20:30]]), bits(pool[keys[:10]]))
+    eng.close()
+    packed.close()
