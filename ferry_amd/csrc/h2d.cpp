@@ -140,10 +140,29 @@ struct ferry_h2d {
   std::vector<int64_t> copy_seq;      // per slot: sequence number of its last copy, -1 if none
   std::vector<std::shared_ptr<Event>> used;  // per slot: last compute that read it
   std::shared_ptr<Event> marker;      // the latest event of ferry_h2d_mark_used_record
+  // the last sub-batch of a packed call, unpacked later (ferry_h2d_set_defer_last): on the
+  // stream of the first ferry_h2d_wait_stream that names one of its slots, else on the unpack
+  // stream before anything else the engine does
+  bool defer_last = false;
+  struct {
+    bool active = false;
+    ferry::UnpackList ul;
+    std::shared_ptr<Event> lane[kLanes];   // the lanes' copies of the sub-batch
+    std::vector<int64_t> slots, entries;   // its slots and staging buffers
+  } deferred;
   int64_t seq = 0;
   int64_t order = 0;                  // events recorded so far
   int64_t copies = 0;
 };
+
+#define H2D_HIP(expr)                                                                     \
+  do {                                                                                    \
+    hipError_t _e = (expr);                                                               \
+    if (_e != hipSuccess) {                                                               \
+      ferry::set_error("%s failed: %s", #expr, hipGetErrorString(_e));                   \
+      return 3;                                                                           \
+    }                                                                                     \
+  } while (0)
 
 // a new engine event recorded on stream s
 static hipError_t record_event(ferry_h2d* h, hipStream_t s, std::shared_ptr<Event>* out,
@@ -158,6 +177,27 @@ static hipError_t record_event(ferry_h2d* h, hipStream_t s, std::shared_ptr<Even
   return hipSuccess;
 }
 
+// Runs the deferred unpack (if any) on stream s, after the copies it reads; its slots and
+// staging buffers are then ready at one event on s.
+static int resolve_deferred(ferry_h2d* h, hipStream_t s) {
+  auto& d = h->deferred;
+  if (!d.active) return 0;
+  d.active = false;
+  std::vector<const std::shared_ptr<Event>*> evs;
+  for (int l = 0; l < kLanes; ++l) evs.push_back(&d.lane[l]);
+  std::vector<hipEvent_t> pending;
+  if (!pending_events(evs, &pending)) return 3;
+  for (hipEvent_t e : pending) H2D_HIP(hipStreamWaitEvent(s, e, 0));
+  if (d.ul.n_rows > 0) H2D_HIP(ferry::h2d_unpack_launch(d.ul, h->row_bytes / 2, s, 0));
+  std::shared_ptr<Event> ev;
+  H2D_HIP(record_event(h, s, &ev));
+  for (int64_t slot : d.slots)
+    for (int l = 0; l < kLanes; ++l) h->copy_done[l][(size_t)slot] = ev;
+  for (int64_t k : d.entries) h->ring_ev[(size_t)k] = ev;
+  for (int l = 0; l < kLanes; ++l) d.lane[l].reset();
+  return 0;
+}
+
 // the copy kernel addresses 16-byte units through 32-bit row indices; with a packed pool the
 // unpack kernel reads the pool's device mapping instead (rows of a multiple of 32 values, each
 // stored at a 256-byte multiple)
@@ -169,15 +209,6 @@ static bool kernel_copy_ok(const ferry_h2d* h) {
          (uintptr_t)h->cache % 16 == 0 && h->pool_rows < (int64_t(1) << 31) &&
          h->cache_rows < (int64_t(1) << 31);
 }
-
-#define H2D_HIP(expr)                                                                     \
-  do {                                                                                    \
-    hipError_t _e = (expr);                                                               \
-    if (_e != hipSuccess) {                                                               \
-      ferry::set_error("%s failed: %s", #expr, hipGetErrorString(_e));                   \
-      return 3;                                                                           \
-    }                                                                                     \
-  } while (0)
 
 extern "C" int ferry_h2d_create(void* cache, int64_t cache_rows, const void* pool,
                                 int64_t pool_rows, int64_t row_bytes, int32_t device,
@@ -223,6 +254,7 @@ extern "C" int ferry_h2d_create(void* cache, int64_t cache_rows, const void* poo
 extern "C" int ferry_h2d_destroy(ferry_h2d* h) {
   ferry::clear_error();
   if (!h) return 0;
+  (void)resolve_deferred(h, h->unpack);
   for (int l = 0; l < kLanes; ++l)
     if (h->stream[l]) (void)hipStreamSynchronize(h->stream[l]);
   if (h->unpack) (void)hipStreamSynchronize(h->unpack);
@@ -328,6 +360,9 @@ static int fetch_packed(ferry_h2d* h, const int64_t* slots, const int64_t* keys,
       (void)hipGetLastError();
       for (int l = 0; l < kLanes; ++l) H2D_HIP(hipStreamWaitEvent(h->stream[l], ev->e, 0));
     }
+    // each lane's byte range as copies; issued round-robin over the lanes, so that every lane
+    // starts as early as the host can queue it
+    std::vector<Seg> lane_segs[kLanes];
     for (int l = 0; l < kLanes; ++l) {
       const int64_t lo = l == 0 ? 0 : total * l / kLanes / 256 * 256;
       const int64_t hi = l + 1 == kLanes ? total : total * (l + 1) / kLanes / 256 * 256;
@@ -335,11 +370,39 @@ static int fetch_packed(ferry_h2d* h, const int64_t* slots, const int64_t* keys,
       for (const Seg& sg : segs) {
         const int64_t a = lo > at ? lo : at;
         const int64_t b = hi < at + sg.bytes ? hi : at + sg.bytes;
-        if (a < b)
-          H2D_HIP(hipMemcpyAsync(sg.dst + (a - at), sg.src + (a - at), (size_t)(b - a),
-                                 hipMemcpyHostToDevice, h->stream[l]));
+        if (a < b) lane_segs[l].push_back({sg.src + (a - at), sg.dst + (a - at), b - a});
         at += sg.bytes;
       }
+    }
+    for (size_t j = 0;; ++j) {
+      bool any = false;
+      for (int l = 0; l < kLanes; ++l)
+        if (j < lane_segs[l].size()) {
+          const Seg& sg = lane_segs[l][j];
+          H2D_HIP(hipMemcpyAsync(sg.dst, sg.src, (size_t)sg.bytes, hipMemcpyHostToDevice,
+                                 h->stream[l]));
+          any = true;
+        }
+      if (!any) break;
+    }
+    if (h->defer_last && i1 == n) {
+      // the call's last sub-batch: its unpack waits for a stream that reads its slots
+      auto& d = h->deferred;
+      d.active = true;
+      d.ul = ul;
+      for (int l = 0; l < kLanes; ++l) H2D_HIP(record_event(h, h->stream[l], &d.lane[l]));
+      d.slots.assign(slots + i0, slots + i1);
+      d.entries = entries;
+      for (int64_t i = i0; i < i1; ++i) {
+        for (int l = 0; l < kLanes; ++l) h->copy_done[l][(size_t)slots[i]] = d.lane[l];
+        h->copy_seq[(size_t)slots[i]] = h->seq++;
+      }
+      h->copies += i1 - i0;
+      remaining -= total;
+      i0 = i1;
+      continue;
+    }
+    for (int l = 0; l < kLanes; ++l) {
       H2D_HIP(hipEventRecord(h->lane_done[l], h->stream[l]));
       H2D_HIP(hipStreamWaitEvent(h->unpack, h->lane_done[l], 0));
     }
@@ -362,6 +425,7 @@ extern "C" int ferry_h2d_fetch(ferry_h2d* h, const int64_t* slots, const int64_t
                                int64_t n) {
   ferry::clear_error();
   if (n <= 0) return 0;
+  if (resolve_deferred(h, h->unpack) != 0) return 3;
   // What a copy into a slot must follow: the last compute that read the slot (WAR) and any
   // earlier copy into it still in flight, on whichever lane or stream (WAW).  Events that have
   // fired when the call is made add no wait.
@@ -493,6 +557,7 @@ extern "C" int ferry_h2d_fetch(ferry_h2d* h, const int64_t* slots, const int64_t
 
 extern "C" int ferry_h2d_wait_host(ferry_h2d* h, const int64_t* slots, int64_t n) {
   ferry::clear_error();
+  if (resolve_deferred(h, h->unpack) != 0) return 3;
   for (int64_t i = 0; i < n; ++i) {
     const int64_t slot = slots[i];
     if (slot < 0 || slot >= h->cache_rows) {
@@ -511,19 +576,28 @@ extern "C" int ferry_h2d_wait_stream(ferry_h2d* h, const int64_t* slots, int64_t
   ferry::clear_error();
   // every still-running copy into the slots: per copy stream its newest such copy (copies into
   // different slots are not ordered with each other: DMA lanes, kernel-mode streams)
+  // A deferred unpack of one of the slots runs on the waiting stream, after the waits for the
+  // other slots' copies (those have fired or will fire first: the deferred sub-batch is the
+  // last one copied), so that nothing stands between that unpack and the stream's next kernel.
   std::vector<const std::shared_ptr<Event>*> evs;
+  bool resolve = false;
   for (int64_t i = 0; i < n; ++i) {
     const int64_t slot = slots[i];
     if (slot < 0 || slot >= h->cache_rows) {
       ferry::set_error("h2d_wait_stream: slot %lld out of range", (long long)slot);
       return 2;
     }
-    if (h->copy_seq[(size_t)slot] < 0) continue;
+    bool deferred = false;
+    if (h->deferred.active)
+      for (int64_t ds : h->deferred.slots) deferred = deferred || ds == slot;
+    resolve = resolve || deferred;
+    if (deferred || h->copy_seq[(size_t)slot] < 0) continue;
     for (int l = 0; l < kLanes; ++l) evs.push_back(&h->copy_done[l][(size_t)slot]);
   }
   std::vector<hipEvent_t> pending;
   if (!pending_events(evs, &pending)) return 3;
   for (hipEvent_t e : pending) H2D_HIP(hipStreamWaitEvent((hipStream_t)stream, e, 0));
+  if (resolve && resolve_deferred(h, (hipStream_t)stream) != 0) return 3;
   return 0;
 }
 
@@ -577,6 +651,7 @@ extern "C" int ferry_h2d_event_synchronize(ferry_h2d* h, void* event) {
 
 extern "C" int ferry_h2d_synchronize(ferry_h2d* h) {
   ferry::clear_error();
+  if (resolve_deferred(h, h->unpack) != 0) return 3;
   for (int l = 0; l < kLanes; ++l) H2D_HIP(hipStreamSynchronize(h->stream[l]));
   H2D_HIP(hipStreamSynchronize(h->unpack));
   for (auto& kl : h->kernel_last) H2D_HIP(hipEventSynchronize(kl.second->e));
@@ -597,7 +672,19 @@ extern "C" int ferry_h2d_set_engine(ferry_h2d* h, int32_t kind) {
     return 2;
   }
   // no wait: every fetch follows the earlier copies into its slots, of either kind
+  if (resolve_deferred(h, h->unpack) != 0) return 3;
   h->kind = kind;
+  return 0;
+}
+
+extern "C" int ferry_h2d_set_defer_last(ferry_h2d* h, int32_t on) {
+  ferry::clear_error();
+  if (!h) {
+    ferry::set_error("h2d_set_defer_last: null engine");
+    return 2;
+  }
+  if (!on && resolve_deferred(h, h->unpack) != 0) return 3;
+  h->defer_last = on != 0;
   return 0;
 }
 
@@ -706,6 +793,7 @@ extern "C" int ferry_h2d_use_packed(ferry_h2d* h, const ferry_packed_pool* pp,
 // attaches pp (null: detaches) to h, which fetches from it from now on
 static int ferry_h2d_use_packed_any(ferry_h2d* h, const ferry_packed_pool* pp,
                                     int64_t ring_rows) {
+  if (resolve_deferred(h, h->unpack) != 0) return 3;
   for (int l = 0; l < kLanes; ++l) H2D_HIP(hipStreamSynchronize(h->stream[l]));
   H2D_HIP(hipStreamSynchronize(h->unpack));
   h->ring_ev.clear();

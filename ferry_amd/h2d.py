@@ -108,6 +108,17 @@ class H2DEngine:
     def engine(self, kind):
         check(lib().ferry_h2d_set_engine(self._h, int(kind)), 'H2DEngine.engine')
 
+    @property
+    def defer_last(self):
+        """Whether the last sub-batch of a packed fetch is unpacked on the stream that waits
+        for it (``wait_stream``) instead of the engine's unpack stream."""
+        return bool(getattr(self, '_defer_last', False))
+
+    @defer_last.setter
+    def defer_last(self, on):
+        check(lib().ferry_h2d_set_defer_last(self._h, int(bool(on))), 'H2DEngine.defer_last')
+        self._defer_last = bool(on)
+
     def set_kernel_stream(self, stream=None):
         """Run kernel-mode copies on ``stream`` (a torch stream; None: the engine's own).  A
         handle of 0 is HIP's null stream (torch's default stream), not the engine's."""

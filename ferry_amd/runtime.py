@@ -109,6 +109,7 @@ class OffloadRuntime:
         else:
             self.h2d = self.ops.H2DEngine(self.cache, self.pool)
         self._kernel_copy = self.copy == 'kernel' and self.h2d.kernel_ok
+        self._defer_last = False
         if self.copy == 'kernel' and not self._kernel_copy:
             raise RuntimeError("copy='kernel' needs a device-mapped pool with 16-byte rows")
         self._copy_mode = None
@@ -194,6 +195,13 @@ class OffloadRuntime:
         lay = buf['layout']
         chunked = T * k >= CHUNK_MIN_PAIRS
         on_stream = self.overlap and not chunked and self._kernel_copy
+        # packed decode calls: the last sub-batch's unpack runs on this stream right after the
+        # copies (one cross-queue wait before the fetched experts, not two)
+        defer = (self.packed is not None and self.overlap and not chunked and not on_stream
+                 and not self.timing)
+        if defer != self._defer_last:
+            self.h2d.defer_last = defer
+            self._defer_last = defer
         if on_stream:
             # the resident experts will run on the side stream, forked here (before the copy
             # kernel that the planner queues on this stream)

@@ -252,6 +252,13 @@ void* ferry_h2d_stream(ferry_h2d* h);
  */
 enum { FERRY_H2D_DMA = 0, FERRY_H2D_KERNEL = 1 };
 int ferry_h2d_set_engine(ferry_h2d* h, int32_t kind);
+/* Deferred last unpack (no counterpart in the reference; packed pools in DMA mode): with `on`,
+ * the unpack of a fetch call's last sub-batch is not queued on the engine's unpack stream but
+ * by the first ferry_h2d_wait_stream that names one of its slots, on the waiting stream, right
+ * after its wait for the copies -- the reader then follows the last copies with one cross-queue
+ * wait instead of two.  Any other engine call (fetch, wait_host, synchronize, ...) first queues
+ * a pending deferred unpack on the unpack stream.  Off by default. */
+int ferry_h2d_set_defer_last(ferry_h2d* h, int32_t on);
 int32_t ferry_h2d_engine(const ferry_h2d* h);
 int ferry_h2d_set_kernel_stream(ferry_h2d* h, void* stream);
 /* Lossless packing of the pool for the host link (no counterpart in the reference, whose

@@ -598,7 +598,8 @@ def test_h2d_packed_pool_fetch_byte_exact(device, kind):
     alone.close()
 
 
-def test_h2d_packed_sub_batches_and_ring_reuse(device):
+@pytest.mark.parametrize('defer', [False, True])
+def test_h2d_packed_sub_batches_and_ring_reuse(device, defer):
     """Calls large enough to go in several sub-batches (about 4, 8, 16 MiB from the call's end),
     each unpacked on the engine's unpack stream while the DMA lanes copy the next: 12 rows of
     ~2.8 MiB packed through a ring of 3 staging buffers (every staging buffer is reused inside
@@ -615,6 +616,7 @@ def test_h2d_packed_sub_batches_and_ring_reuse(device):
     assert packed.packed_rows == rows - 1
     cache = torch.zeros((cap, width), dtype=torch.bfloat16, device=device)
     eng = H2DEngine.from_packed(cache, packed, ring_rows=3)
+    eng.defer_last = defer   # the last sub-batch's unpack runs where its slots are waited for
     bits = lambda t: t.view(torch.int16)   # noqa: E731
     keys = np.array([0, 6, 1, 2, 11, 3, 4, 5, 7, 8, 9, 10])
     eng.fetch(np.arange(12), keys)
@@ -734,5 +736,49 @@ def test_h2d_packed_kernel_mode_many_rows(device):
     assert torch.equal(bits(got[[a, b]]), bits(pool[[102, 101]]))
     assert torch.equal(bits(got[slots[:20]]), bits(pool[keys[::-1][:20].copy()]))
     assert torch.equal(bits(got[slots[20:30]]), bits(pool[keys[:10]]))
+    eng.close()
+    packed.close()
+
+
+def test_h2d_packed_deferred_last_unpack(device):
+    """With defer_last, the last sub-batch of a packed call is unpacked by the first wait_stream
+    that names one of its slots (on that stream); a wait_stream on other slots leaves it pending;
+    the next fetch, wait_host or synchronize queues a pending one on the unpack stream; turning
+    the option off queues it too.  Every slot holds the pool row's exact bytes."""
+    from ferry_amd.h2d import H2DEngine, PackedPool
+    rows, cap, width = 12, 10, (1 << 20) + 4096
+    g = torch.Generator().manual_seed(9)
+    pool = (torch.randn((rows, width), generator=g) * 0.02).to(torch.bfloat16)
+    pool[4] = torch.randint(-32768, 32767, (width,), generator=g,
+                            dtype=torch.int16).view(torch.bfloat16)
+    packed = PackedPool(pool, threads=8)
+    cache = torch.zeros((cap, width), dtype=torch.bfloat16, device=device)
+    eng = H2DEngine.from_packed(cache, packed, ring_rows=4)
+    eng.defer_last = True
+    bits = lambda t: t.view(torch.int16)   # noqa: E731
+    consumer = torch.cuda.Stream()
+    # 1: the consumer waits for the fetched slots (resolves on the consumer stream)
+    eng.fetch([0, 1, 2, 3, 4, 5], [0, 1, 2, 3, 4, 5])
+    eng.wait_stream([0, 1, 2, 3, 4, 5], consumer)
+    with torch.cuda.stream(consumer):
+        snap = cache[:6].clone()
+    torch.cuda.synchronize()
+    assert torch.equal(bits(snap.cpu()), bits(pool[:6]))
+    # 2: a wait on other slots leaves the pending unpack; the next fetch queues it
+    eng.fetch([6, 7], [6, 7])
+    eng.wait_stream([0], consumer)
+    eng.fetch([8], [8])
+    eng.wait_host([6, 7, 8])
+    assert torch.equal(bits(cache.cpu()[6:9]), bits(pool[6:9]))
+    # 3: synchronize queues it; the raw row (4) among deferred ones
+    eng.fetch([9, 0], [4, 11])
+    eng.synchronize()
+    assert torch.equal(bits(cache.cpu()[[9, 0]]), bits(pool[[4, 11]]))
+    # 4: turning the option off queues it; later calls unpack on the engine's stream
+    eng.fetch([1, 2], [10, 9])
+    eng.defer_last = False
+    eng.fetch([3], [7])
+    eng.wait_host([1, 2, 3])
+    assert torch.equal(bits(cache.cpu()[[1, 2, 3]]), bits(pool[[10, 9, 7]]))
     eng.close()
     packed.close()
