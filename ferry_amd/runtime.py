@@ -202,11 +202,6 @@ class OffloadRuntime:
         if defer != self._defer_last:
             self.h2d.defer_last = defer
             self._defer_last = defer
-        if on_stream:
-            # the resident experts will run on the side stream, forked here (before the copy
-            # kernel that the planner queues on this stream)
-            fork = torch.cuda.Event()
-            fork.record(stream)
 
         # 3. plan + fetch
         t_sync = time.perf_counter_ns()
@@ -269,35 +264,18 @@ class OffloadRuntime:
             self.serial_wait_ns += time.perf_counter_ns() - started
         mark = self.ops.timing_mark() if timing else 0
         waits = []
-        shared_out = None
         if on_stream:
-            # the copy kernel holds this stream; the resident experts (and the shared experts)
-            # run beside it on the side stream, which joins back before the combine (its work is
-            # long done by then, so the join costs no wait); the fetched experts follow the copy
-            # kernel in this stream's order
-            side = self._side()
-            side.wait_event(fork)
-            if len(resident_list):
-                self.h2d.wait_stream(slot_of[resident_list], side)
-                with torch.cuda.stream(side):
-                    self._ffn(common, resident_list, slot32, buf, side, counts_e)
-            if shared is not None:
-                with torch.cuda.stream(side):
-                    shared_out = shared(common[1], out=self._shared_out(T))
-            join = torch.cuda.Event()
-            join.record(side)
+            # the copies are queued on this stream (the wait on their events costs nothing);
+            # resident rows may come from DMA copies of earlier calls
+            active_list = np.flatnonzero(active)
+            self.h2d.wait_stream(slot_of[active_list], stream)
             if timing:
                 waits.append((ev[0], ev[1]))   # the copy kernel holds this stream
-            if len(fetches):
-                fetched = np.sort(missing_keys)
-                self.h2d.wait_stream(slot_of[fetched], stream)
-                self._ffn(common, fetched, slot32, buf, stream, counts_e)
-            stream.wait_event(join)
+            self._ffn(common, active_list, slot32, buf, stream, counts_e)
         elif len(resident_list):
             self.h2d.wait_stream(slot_of[resident_list], stream)
             self._ffn(common, resident_list, slot32, buf, stream, counts_e)
-        if shared is not None and not on_stream:
-            shared_out = shared(common[1], out=self._shared_out(T))
+        shared_out = shared(common[1], out=self._shared_out(T)) if shared is not None else None
         if len(fetches) and not on_stream:
             for g in groups:
                 w0 = w1 = None
@@ -345,12 +323,6 @@ class OffloadRuntime:
             self.h2d.engine = KERNEL if on_stream else DMA
             self.h2d.set_kernel_stream(stream if on_stream else None)
             self._copy_mode = mode
-
-    def _side(self):
-        """The side stream of copy-kernel calls (default priority), made on first use."""
-        if getattr(self, '_side_stream', None) is None:
-            self._side_stream = torch.cuda.Stream(self.device)
-        return self._side_stream
 
     def _shared_out(self, tokens):
         b = self._bufs[tokens]
