@@ -43,6 +43,7 @@ hipError_t h2d_copy_launch(const void* pool, void* cache, int64_t row_bytes, con
 hipError_t h2d_unpack_launch(const UnpackList& list, int64_t n, hipStream_t stream,
                              int64_t max_groups);
 void pack_plan_rows(const uint16_t* pool, int64_t rows, int64_t n, int threads, PackPlan* plan);
+int64_t plan_bytes(int64_t n, const PackPlan& plan);
 void pack_write_rows(const uint16_t* pool, int64_t rows, int64_t n, int threads,
                      const PackPlan* plan, const int64_t* off, uint8_t* dst);
 }  // namespace ferry
@@ -720,7 +721,7 @@ extern "C" int ferry_pack_pool(const void* pool, int64_t rows, int64_t row_bytes
   pp->raw.assign((size_t)rows, 0);
   std::vector<int64_t> pack_off((size_t)rows, -1);   // rows to pack: their offset
   for (int64_t i = 0; i < rows; ++i) {
-    int64_t b = ferry::packed_bytes(n, plan[(size_t)i].esc1, plan[(size_t)i].esc2);
+    int64_t b = ferry::plan_bytes(n, plan[(size_t)i]);
     if (b >= row_bytes) {   // no gain: the row is stored raw
       b = row_bytes;
       pp->raw[(size_t)i] = 1;

@@ -49,16 +49,17 @@ __global__ __launch_bounds__(256) void h2d_copy_kernel(const u32x4* __restrict__
   }
 }
 
-// Unpacks packed rows (pack_format.h) from the staging buffers into cache slots.  A workgroup
-// of 256 threads decodes one block of 8192 values: a thread turns 32 values (32 bytes of the
-// sign | mantissa plane, 4 bytes of each code plane) into 64 bytes of bf16.  The block's slice
-// of the level-2 codes and of the third-level list is staged in LDS; a block-wide prefix sum of
-// the threads' escape counts gives each escape its rank in that slice.
+// Unpacks packed rows (pack_format.h) into cache slots.  A workgroup of 256 threads decodes one
+// block of 8192 values: a thread turns 32 values (32 bytes of the sign | mantissa plane, 4 bytes
+// of each code plane) into 64 bytes of bf16.  The block's slices of the level-2 and level-3 code
+// streams and of the list are staged in LDS; a block-wide prefix sum of the threads' level-1
+// escapes gives each its position in the level-2 slice, and a second one, of the level-2 escapes
+// the threads then find there, their positions in the level-3 slice.
 constexpr int kUnpackThreads = 256;
-constexpr int kL3Lds = 256;   // third-level entries of a block staged in LDS (more: global search)
+constexpr int kListLds = 256;   // list entries of a block staged in LDS (more: global search)
 
-__device__ __forceinline__ uint32_t level3_global(const uint32_t* idx, const uint8_t* ex, int64_t lo,
-                                                  int64_t hi, uint32_t i) {
+__device__ __forceinline__ uint32_t list_global(const uint32_t* idx, const uint8_t* ex, int64_t lo,
+                                                int64_t hi, uint32_t i) {
   while (hi - lo > 1) {   // idx[lo] <= i < idx[hi], as the entry for i is in [lo, hi)
     const int64_t mid = (lo + hi) >> 1;
     if (idx[mid] <= i) lo = mid; else hi = mid;
@@ -67,19 +68,37 @@ __device__ __forceinline__ uint32_t level3_global(const uint32_t* idx, const uin
 }
 
 struct UnpackLds {
-  uint8_t c[kPackBlock / 2 + 16];
-  uint16_t li[kL3Lds];
-  uint8_t le[kL3Lds];
-  uint32_t wave[kUnpackThreads / 64];
+  uint32_t c2[kPackBlock / 16 + 4];   // level-2 code words of the block (16 codes a word)
+  uint32_t c3[kPackBlock / 8 + 4];    // level-3 code words (8 codes a word)
+  uint16_t li[kListLds];
+  uint8_t le[kListLds];
+  uint32_t wave[2][kUnpackThreads / 64];
 };
+
+// exclusive block-wide prefix sum of cnt over the workgroup's threads (all of them call it);
+// its barrier also publishes the LDS writes made before it
+__device__ __forceinline__ uint32_t block_rank(uint32_t cnt, uint32_t* wave_total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t incl = cnt;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t y = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += y;
+  }
+  if (lane == 63) wave_total[wave] = incl;
+  __syncthreads();
+  uint32_t rank = incl - cnt;
+  for (int w = 0; w < wave; ++w) rank += wave_total[w];
+  return rank;
+}
+
+__device__ __forceinline__ uint32_t pick3(uint32_t c, uint32_t x0, uint32_t x1, uint32_t x2) {
+  return c == 0 ? x0 : (c == 1 ? x1 : x2);
+}
 
 // block blk of row r of the list
 __device__ __forceinline__ void unpack_block(const UnpackList& list, int64_t n, int r, int64_t blk,
                                              UnpackLds& lds) {
-  uint8_t* lds_c = lds.c;
-  uint16_t* lds_li = lds.li;
-  uint8_t* lds_le = lds.le;
-  uint32_t* lds_wave = lds.wave;
   const int t = threadIdx.x;
   const uint8_t* src = list.src[r];
   if (list.raw[r]) {   // a row kept raw: the workgroup copies its block's 16 KiB as they are
@@ -96,48 +115,54 @@ __device__ __forceinline__ void unpack_block(const UnpackList& list, int64_t n, 
     return;
   }
   const PackHeader* hd = reinterpret_cast<const PackHeader*>(src);
-  const uint32_t base1 = hd->base1, base2 = hd->base2;
-  const PackOffsets o = pack_offsets(n, (int64_t)hd->esc1, (int64_t)hd->esc2);
-  const uint32_t* pre = reinterpret_cast<const uint32_t*>(src + o.p);
-  const uint32_t e_lo = pre[2 * blk], e_hi = pre[2 * blk + 2];
-  const uint32_t l_lo = pre[2 * blk + 1], l_hi = pre[2 * blk + 3];
+  const uint32_t t10 = hd->t1[0], t11 = hd->t1[1], t12 = hd->t1[2];
+  const uint32_t t20 = hd->t2[0], t21 = hd->t2[1], t22 = hd->t2[2];
+  const uint32_t base3 = hd->base3;
+  const PackOffsets o =
+      pack_offsets(n, (int64_t)hd->esc1, (int64_t)hd->esc2, (int64_t)hd->esc3);
+  const uint32_t* pre = reinterpret_cast<const uint32_t*>(src + o.p) + 3 * blk;
+  const uint32_t e1_lo = pre[0], e2_lo = pre[1], e3_lo = pre[2];
+  const uint32_t e1_hi = pre[3], e2_hi = pre[4], e3_hi = pre[5];
+  // the block's code words and list entries
+  const uint32_t* c2g = reinterpret_cast<const uint32_t*>(src + o.c2);
+  const uint32_t* c3g = reinterpret_cast<const uint32_t*>(src + o.c3);
+  const int w2 = (int)(((e1_hi + 15) >> 4) - (e1_lo >> 4));
+  for (int i = t; i < w2; i += kUnpackThreads) lds.c2[i] = c2g[(e1_lo >> 4) + i];
+  const int w3 = (int)(((e2_hi + 7) >> 3) - (e2_lo >> 3));
+  for (int i = t; i < w3; i += kUnpackThreads) lds.c3[i] = c3g[(e2_lo >> 3) + i];
   const uint32_t* lidx = reinterpret_cast<const uint32_t*>(src + o.l_idx);
   const uint8_t* lexp = src + o.l_exp;
-  // the block's level-2 nibbles [e_lo, e_hi) lie in bytes [e_lo / 2, (e_hi + 1) / 2)
-  const int c_bytes = (int)(((e_hi + 1) >> 1) - (e_lo >> 1));
-  for (int i = t; i < c_bytes; i += kUnpackThreads) lds_c[i] = src[o.c + (e_lo >> 1) + i];
-  const int l_cnt = (int)(l_hi - l_lo);
-  if (l_cnt <= kL3Lds)
+  const int l_cnt = (int)(e3_hi - e3_lo);
+  if (l_cnt <= kListLds)
     for (int i = t; i < l_cnt; i += kUnpackThreads) {
-      lds_li[i] = (uint16_t)(lidx[l_lo + i] - (uint32_t)(blk * kPackBlock));
-      lds_le[i] = lexp[l_lo + i];
+      lds.li[i] = (uint16_t)(lidx[e3_lo + i] - (uint32_t)(blk * kPackBlock));
+      lds.le[i] = lexp[e3_lo + i];
     }
   const int64_t v0 = blk * kPackBlock + 32 * t;
   const bool active = v0 < n;   // n is a multiple of 32: a thread has 32 values or none
   u32x4 a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
-  uint32_t p0 = 0, p1 = 0, p2 = 0;
+  uint32_t p0 = 0, p1 = 0;
   if (active) {
     const u32x4* pa = reinterpret_cast<const u32x4*>(src + o.a + v0);
     a0 = pa[0];
     a1 = pa[1];
     p0 = *reinterpret_cast<const uint32_t*>(src + o.b0 + v0 / 8);
     p1 = *reinterpret_cast<const uint32_t*>(src + o.b1 + v0 / 8);
-    p2 = *reinterpret_cast<const uint32_t*>(src + o.b2 + v0 / 8);
   }
-  const uint32_t esc = p0 & p1 & p2;   // code 7
-  // block-wide exclusive prefix sum of the escape counts
-  const uint32_t cnt = (uint32_t)__popc(esc);
-  const int lane = t & 63, wave = t >> 6;
-  uint32_t incl = cnt;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const uint32_t y = __shfl_up(incl, d, 64);
-    if (lane >= d) incl += y;
+  const uint32_t m1 = p0 & p1;   // level-1 code 3
+  const uint32_t cnt1 = (uint32_t)__popc(m1);
+  const uint32_t rank1 = block_rank(cnt1, lds.wave[0]);   // also publishes the staged slices
+  // the level-2 codes of this thread's escapes: 2-bit codes (e1_lo % 16) + rank1 ... of the slice
+  uint64_t codes2 = 0;
+  if (cnt1) {
+    const uint32_t bit0 = 2 * ((e1_lo & 15) + rank1);
+    const uint32_t w = bit0 >> 5, sh = bit0 & 31;
+    codes2 = ((uint64_t)lds.c2[w] | ((uint64_t)lds.c2[w + 1] << 32)) >> sh;
+    if (sh) codes2 |= (uint64_t)lds.c2[w + 2] << (64 - sh);
+    if (cnt1 < 32) codes2 &= (1ull << (2 * cnt1)) - 1;
   }
-  if (lane == 63) lds_wave[wave] = incl;
-  __syncthreads();   // also publishes the staged nibbles and third-level entries
-  uint32_t rank = incl - cnt;
-  for (int w = 0; w < wave; ++w) rank += lds_wave[w];
+  const uint32_t cnt2 = (uint32_t)__popcll(codes2 & (codes2 >> 1) & 0x5555555555555555ull);
+  const uint32_t rank2 = block_rank(cnt2, lds.wave[1]);
   if (!active) return;
   const uint32_t a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
   uint32_t w[16];
@@ -148,29 +173,34 @@ __device__ __forceinline__ void unpack_block(const UnpackList& list, int64_t n, 
     for (int q2 = 0; q2 < 2; ++q2) {
       const int q = 2 * h + q2;
       const uint32_t b = (a[q >> 2] >> (8 * (q & 3))) & 0xFFu;
-      const uint32_t c = ((p0 >> q) & 1u) | (((p1 >> q) & 1u) << 1) | (((p2 >> q) & 1u) << 2);
-      const uint32_t e = c == (uint32_t)kPackWindow1 ? 0u : base1 + c;   // escapes: filled below
+      const uint32_t c = ((p0 >> q) & 1u) | (((p1 >> q) & 1u) << 1);
+      const uint32_t e = c == (uint32_t)kPackTable ? 0u : pick3(c, t10, t11, t12);   // escapes: below
       pair |= (((b & 0x80u) << 8) | (e << 7) | (b & 0x7Fu)) << (16 * q2);
     }
     w[h] = pair;
   }
-  // escapes, in value order: level-2 code from LDS, or the third-level list
-  const uint32_t nib0 = (e_lo & 1u) + rank;
-  for (uint32_t m = esc, k = 0; m != 0; m &= m - 1, ++k) {
+  // escapes, in value order: level-2 table, else the level-3 window, else the list
+  uint32_t pos3 = (e2_lo & 7) + rank2;   // this thread's next level-3 code in the slice
+  for (uint32_t m = m1, k = 0; m != 0; m &= m - 1, ++k) {
     const int q = __builtin_ctz(m);
-    const uint32_t nib = nib0 + k;
-    const uint32_t c2 = (lds_c[nib >> 1] >> (4 * (nib & 1u))) & 0xFu;
+    const uint32_t c2 = (uint32_t)(codes2 >> (2 * k)) & 3u;
     uint32_t e;
-    if (c2 < (uint32_t)kPackWindow2) {
-      e = base2 + c2;
+    if (c2 < (uint32_t)kPackTable) {
+      e = pick3(c2, t20, t21, t22);
     } else {
-      const uint32_t li = (uint32_t)(32 * t + q);   // index within the block
-      if (l_cnt <= kL3Lds) {
-        int j = 0;
-        while (j + 1 < l_cnt && lds_li[j] != li) ++j;
-        e = lds_le[j];
+      const uint32_t c3 = (lds.c3[pos3 >> 3] >> (4 * (pos3 & 7))) & 0xFu;
+      ++pos3;
+      if (c3 < (uint32_t)kPackWindow3) {
+        e = base3 + c3;
       } else {
-        e = level3_global(lidx, lexp, l_lo, l_hi, (uint32_t)(blk * kPackBlock) + li);
+        const uint32_t li = (uint32_t)(32 * t + q);   // index within the block
+        if (l_cnt <= kListLds) {
+          int j = 0;
+          while (j + 1 < l_cnt && lds.li[j] != li) ++j;
+          e = lds.le[j];
+        } else {
+          e = list_global(lidx, lexp, e3_lo, e3_hi, (uint32_t)(blk * kPackBlock) + li);
+        }
       }
     }
     const uint32_t bits = e << (7 + 16 * (q & 1));

@@ -28,76 +28,112 @@ static void best_window(const int64_t* hist, int width, uint32_t* base, int64_t*
   *in_window = best;
 }
 
-// The two exponent windows of one row of n bf16 values and its escape counts.
+// The kPackTable most populated exponents of hist (ties: the smaller exponent first), their
+// population, and hist with them taken out.
+static int64_t take_table(int64_t* hist, uint8_t* table) {
+  int64_t in = 0;
+  for (int j = 0; j < kPackTable; ++j) {
+    int best = 0;
+    for (int e = 1; e < 256; ++e)
+      if (hist[e] > hist[best]) best = e;
+    table[j] = (uint8_t)best;
+    in += hist[best];
+    hist[best] = -1;   // taken (a later pick never matches it again)
+  }
+  for (int j = 0; j < kPackTable; ++j) hist[table[j]] = 0;
+  return in;
+}
+
+// The exponent tables of one row of n bf16 values and its escape counts.
 void pack_plan(const uint16_t* v, int64_t n, PackPlan* plan) {
   int64_t hist[256] = {};
   for (int64_t i = 0; i < n; ++i) ++hist[(v[i] >> 7) & 0xFF];
-  int64_t in1, in2;
-  best_window(hist, kPackWindow1, &plan->base1, &in1);
-  for (int e = 0; e < kPackWindow1; ++e) hist[plan->base1 + e] = 0;   // the escapes remain
-  best_window(hist, kPackWindow2, &plan->base2, &in2);
+  const int64_t in1 = take_table(hist, plan->t1);
+  const int64_t in2 = take_table(hist, plan->t2);
+  uint32_t base3;
+  int64_t in3;
+  best_window(hist, kPackWindow3, &base3, &in3);
+  plan->base3 = (uint8_t)base3;
   plan->esc1 = n - in1;
   plan->esc2 = plan->esc1 - in2;
+  plan->esc3 = plan->esc2 - in3;
 }
 
-// Writes the packed row (packed_bytes(n, esc1, esc2) bytes) of a row planned by pack_plan.
+int64_t plan_bytes(int64_t n, const PackPlan& plan) {
+  return packed_bytes(n, plan.esc1, plan.esc2, plan.esc3);
+}
+
+// index of e in a table of kPackTable exponents (the first match), or kPackTable
+static inline uint32_t table_code(const uint8_t* t, uint32_t e) {
+  for (int j = 0; j < kPackTable; ++j)
+    if (t[j] == e) return (uint32_t)j;
+  return kPackTable;
+}
+
+// Writes the packed row (plan_bytes(n, plan) bytes) of a row planned by pack_plan.
 void pack_write(const uint16_t* v, int64_t n, const PackPlan& plan, uint8_t* dst) {
-  const PackOffsets o = pack_offsets(n, plan.esc1, plan.esc2);
-  const int64_t bytes = packed_bytes(n, plan.esc1, plan.esc2);
+  const PackOffsets o = pack_offsets(n, plan.esc1, plan.esc2, plan.esc3);
+  const int64_t bytes = plan_bytes(n, plan);
   PackHeader hd;
   std::memset(&hd, 0, sizeof(hd));
   hd.magic = kPackMagic;
-  hd.base1 = plan.base1;
-  hd.base2 = plan.base2;
+  std::memcpy(hd.t1, plan.t1, kPackTable);
+  std::memcpy(hd.t2, plan.t2, kPackTable);
+  hd.base3 = plan.base3;
   hd.values = (uint64_t)n;
   hd.esc1 = (uint64_t)plan.esc1;
   hd.esc2 = (uint64_t)plan.esc2;
+  hd.esc3 = (uint64_t)plan.esc3;
   hd.bytes = (uint64_t)bytes;
   std::memcpy(dst, &hd, sizeof(hd));
-  std::memset(dst + o.c, 0, (size_t)(bytes - o.c));   // nibble plane, alignment gap, tail
+  std::memset(dst + o.c2, 0, (size_t)(bytes - o.c2));   // code streams, list, tail
   uint8_t* pa = dst + o.a;
   uint8_t* b0 = dst + o.b0;
   uint8_t* b1 = dst + o.b1;
-  uint8_t* b2 = dst + o.b2;
   uint32_t* pre = reinterpret_cast<uint32_t*>(dst + o.p);
-  uint8_t* pc = dst + o.c;
+  uint8_t* c2s = dst + o.c2;
+  uint8_t* c3s = dst + o.c3;
   uint32_t* lidx = reinterpret_cast<uint32_t*>(dst + o.l_idx);
   uint8_t* lexp = dst + o.l_exp;
-  int64_t k1 = 0, k2 = 0;   // escapes and third-level entries so far
+  int64_t k1 = 0, k2 = 0, k3 = 0;   // escapes of each level so far
   for (int64_t i = 0; i < n; i += 8) {
     if (i % kPackBlock == 0) {
-      pre[2 * (i / kPackBlock)] = (uint32_t)k1;
-      pre[2 * (i / kPackBlock) + 1] = (uint32_t)k2;
+      pre[3 * (i / kPackBlock)] = (uint32_t)k1;
+      pre[3 * (i / kPackBlock) + 1] = (uint32_t)k2;
+      pre[3 * (i / kPackBlock) + 2] = (uint32_t)k3;
     }
-    uint32_t p0 = 0, p1 = 0, p2 = 0;
+    uint32_t p0 = 0, p1 = 0;
     for (int q = 0; q < 8; ++q) {
       const uint16_t x = v[i + q];
       const uint32_t e = (x >> 7) & 0xFF;
       pa[i + q] = (uint8_t)(((x >> 8) & 0x80) | (x & 0x7F));
-      uint32_t c = e - plan.base1;   // wraps for e < base1
-      if (c >= (uint32_t)kPackWindow1) {
-        c = kPackWindow1;
-        uint32_t c2 = e - plan.base2;
-        if (c2 >= (uint32_t)kPackWindow2) {
-          c2 = kPackWindow2;
-          lidx[k2] = (uint32_t)(i + q);
-          lexp[k2] = (uint8_t)e;
+      const uint32_t c = table_code(plan.t1, e);
+      if (c == (uint32_t)kPackTable) {
+        const uint32_t c2 = table_code(plan.t2, e);
+        c2s[k1 >> 2] |= (uint8_t)(c2 << (2 * (k1 & 3)));
+        ++k1;
+        if (c2 == (uint32_t)kPackTable) {
+          uint32_t c3 = e - plan.base3;   // wraps for e < base3
+          if (c3 >= (uint32_t)kPackWindow3) {
+            c3 = kPackWindow3;
+            lidx[k3] = (uint32_t)(i + q);
+            lexp[k3] = (uint8_t)e;
+            ++k3;
+          }
+          c3s[k2 >> 1] |= (uint8_t)(c3 << (4 * (k2 & 1)));
           ++k2;
         }
-        pc[k1 >> 1] |= (uint8_t)(c2 << (4 * (k1 & 1)));
-        ++k1;
       }
       p0 |= (c & 1u) << q;
       p1 |= ((c >> 1) & 1u) << q;
-      p2 |= ((c >> 2) & 1u) << q;
     }
     b0[i / 8] = (uint8_t)p0;
     b1[i / 8] = (uint8_t)p1;
-    b2[i / 8] = (uint8_t)p2;
   }
   const int64_t nb = (n + kPackBlock - 1) / kPackBlock;
-  pre[2 * nb] = (uint32_t)k1;
-  pre[2 * nb + 1] = (uint32_t)k2;
+  pre[3 * nb] = (uint32_t)k1;
+  pre[3 * nb + 1] = (uint32_t)k2;
+  pre[3 * nb + 2] = (uint32_t)k3;
 }
 
 // Run f(i) for i in [0, n) on `threads` threads.
@@ -140,7 +176,7 @@ extern "C" int ferry_pack_row(const void* src, int64_t n, void* dst, int64_t cap
   }
   ferry::PackPlan plan;
   ferry::pack_plan((const uint16_t*)src, n, &plan);
-  const int64_t bytes = ferry::packed_bytes(n, plan.esc1, plan.esc2);
+  const int64_t bytes = ferry::plan_bytes(n, plan);
   *bytes_out = bytes;
   if (bytes >= 2 * n) return 1;
   if (!dst) return 0;

@@ -166,10 +166,12 @@ class H2DEngine:
 
 class PackedPool:
     """A lossless packed copy of a pool for the host link (ferry_pack_pool), in pinned memory:
-    per value a sign|mantissa byte and a 3-bit exponent code against the row's 7 most populated
-    exponents, the rest as 4-bit codes against a second window of 15 or in an (index, exponent)
-    list -- about 11.1 bits instead of 16 for weights that span few binades (rows that would
-    not shrink are kept raw; rows hold a multiple of 32 values).  The source pool may be
+    per value a sign|mantissa byte and a 2-bit exponent code against the row's 3 most populated
+    exponents, the escapes as 2-bit codes against the next 3, their escapes as 4-bit codes
+    against a window of 15 or in an (index, exponent) list -- about 10.7 bits instead of 16 for
+    weights that span few binades (rows that would not shrink are kept raw; rows hold a
+    multiple of 32 values).  Engines fetch it in DMA mode (staging buffers) or in kernel mode
+    (the unpack kernel reads it over the link).  The source pool may be
     pageable and may be freed afterwards; engines fetch from the packed pool alone
     (``H2DEngine.from_packed``) or attach it to an engine of the same pinned pool
     (``use_packed``)."""

@@ -263,17 +263,20 @@ int32_t ferry_h2d_engine(const ferry_h2d* h);
 int ferry_h2d_set_kernel_stream(ferry_h2d* h, void* stream);
 /* Lossless packing of the pool for the host link (no counterpart in the reference, whose
  * engine copies raw bf16 rows).  ferry_pack_pool copies every pool row into pinned host memory,
- * in a packed form where it shrinks: per value one byte sign | mantissa and a 3-bit exponent
- * code against the row's most populated window of 7 exponents; the other exponents follow as
- * 4-bit codes against a second window of 15, and the rest in an (index, exponent) list (about
- * 11.1 bits per value for weights that span few binades); a row that would not shrink is
- * copied raw.  Rows hold a multiple of 32 values.  It reads the pool (pinned or pageable host memory, not changed
- * afterwards) on `threads` host threads; the packed pool then stands alone.  An engine made
- * from it (ferry_h2d_create_packed) or given it (ferry_h2d_use_packed, an engine of the same
- * pinned pool; null detaches it) fetches in DMA mode: packed rows go into `ring_rows` device
- * staging buffers it allocates, and an unpack kernel writes the slots -- the slot bytes are
- * exactly the pool row's.  A call is fetched in sub-batches of about 4 MiB, each unpacked on a
- * stream of its own while the DMA lanes copy the next.  A packed pool outlives the engines that use it. */
+ * in a packed form where it shrinks: per value one byte sign | mantissa and a 2-bit exponent
+ * code against the row's 3 most populated exponents; the escapes' exponents follow as 2-bit
+ * codes against the next 3, theirs as 4-bit codes against a window of 15, and the rest in an
+ * (index, exponent) list (about 10.7 bits per value for weights that span few binades); a row
+ * that would not shrink is copied raw.  Rows hold a multiple of 32 values.  It reads the pool
+ * (pinned or pageable host memory, not changed afterwards) on `threads` host threads; the
+ * packed pool then stands alone.  An engine made from it (ferry_h2d_create_packed) or given it
+ * (ferry_h2d_use_packed, an engine of the same pinned pool; null detaches it) fetches in DMA
+ * mode: packed rows go into `ring_rows` device staging buffers it allocates, and an unpack
+ * kernel writes the slots -- the slot bytes are exactly the pool row's.  A call is fetched in
+ * sub-batches of about 4 MiB, each unpacked on a stream of its own while the DMA lanes copy the
+ * next.  In kernel mode (ferry_h2d_set_engine) the unpack kernel reads the packed rows over the
+ * link through the packed pool's device mapping, with no staging.  A packed pool outlives the
+ * engines that use it. */
 typedef struct ferry_packed_pool ferry_packed_pool;
 int ferry_pack_pool(const void* pool, int64_t rows, int64_t row_bytes, int32_t threads,
                     ferry_packed_pool** out);

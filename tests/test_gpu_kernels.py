@@ -514,7 +514,7 @@ def test_h2d_copy_order_across_modes(device):
 
 def _spread_block(row, block, count, g):
     """Row with `count` values of block `block` (8192 values) spread over ~160 binades, so that
-    the packed block holds hundreds of third-level entries."""
+    the packed block holds hundreds of list entries."""
     out = row.clone()
     k = torch.randint(20, 100, (count,), generator=g).float()
     sign = torch.where(torch.rand(count, generator=g) < 0.5, -1.0, 1.0)
@@ -528,7 +528,7 @@ def _spread_block(row, block, count, g):
 def test_h2d_packed_pool_fetch_byte_exact(device, kind):
     """Fetches from a packed pool write the pool rows' exact bytes: Gaussian rows, a row with
     special values (+-0, +-inf, NaN, denormals, huge: escapes), a row with hundreds of
-    third-level entries in one block, a row of random bits (left raw);
+    list entries in one block, a row of random bits (left raw);
     calls of 1 to 10 rows through 3 staging buffers (ring reuse inside a call and across calls),
     a slot named twice, a GPU-side wait, and raw fetches again after detaching.  kind 'kernel':
     the unpack kernel reads the packed rows over the link itself (no staging, no DMA)."""
@@ -558,7 +558,7 @@ def test_h2d_packed_pool_fetch_byte_exact(device, kind):
         if size >= 7:
             keys[0] = 7          # the raw row
             keys[1] = 5          # the row with escapes
-            keys[2] = 9          # the row with many third-level entries
+            keys[2] = 9          # the row with many list entries
         eng.fetch(slots, keys)
         eng.wait_host(slots)
         assert torch.equal(bits(cache.cpu()[slots]), bits(pool[keys])), size
