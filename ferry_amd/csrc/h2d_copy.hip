@@ -67,12 +67,15 @@ __device__ __forceinline__ uint32_t list_global(const uint32_t* idx, const uint8
   return ex[lo];
 }
 
+constexpr int kEscStride = 9;   // words per thread in UnpackLds::esc (8 + 1 against bank conflicts)
+
 struct UnpackLds {
   uint32_t c2[kPackBlock / 16 + 4];   // level-2 code words of the block (16 codes a word)
-  uint32_t c3[kPackBlock / 8 + 4];    // level-3 code words (8 codes a word)
+  uint32_t c3[kPackBlock / 8 + 8];    // level-3 code words (8 codes a word)
   uint16_t li[kListLds];
   uint8_t le[kListLds];
   uint32_t wave[2][kUnpackThreads / 64];
+  uint32_t esc[kUnpackThreads * kEscStride];   // per thread: its escapes' exponents, byte q = value q
 };
 
 // exclusive block-wide prefix sum of cnt over the workgroup's threads (all of them call it);
@@ -114,6 +117,18 @@ __device__ __forceinline__ void unpack_block(const UnpackList& list, int64_t n, 
     }
     return;
   }
+  // the planes of this thread's 32 values (their offsets do not depend on the header)
+  const int64_t v0 = blk * kPackBlock + 32 * t;
+  const bool active = v0 < n;   // n is a multiple of 32: a thread has 32 values or none
+  u32x4 a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
+  uint32_t p0 = 0, p1 = 0;
+  if (active) {
+    const u32x4* pa = reinterpret_cast<const u32x4*>(src + kPackHeaderBytes + v0);
+    a0 = pa[0];
+    a1 = pa[1];
+    p0 = *reinterpret_cast<const uint32_t*>(src + kPackHeaderBytes + n + v0 / 8);
+    p1 = *reinterpret_cast<const uint32_t*>(src + kPackHeaderBytes + n + n / 8 + v0 / 8);
+  }
   const PackHeader* hd = reinterpret_cast<const PackHeader*>(src);
   const uint32_t t10 = hd->t1[0], t11 = hd->t1[1], t12 = hd->t1[2];
   const uint32_t t20 = hd->t2[0], t21 = hd->t2[1], t22 = hd->t2[2];
@@ -138,17 +153,6 @@ __device__ __forceinline__ void unpack_block(const UnpackList& list, int64_t n, 
       lds.li[i] = (uint16_t)(lidx[e3_lo + i] - (uint32_t)(blk * kPackBlock));
       lds.le[i] = lexp[e3_lo + i];
     }
-  const int64_t v0 = blk * kPackBlock + 32 * t;
-  const bool active = v0 < n;   // n is a multiple of 32: a thread has 32 values or none
-  u32x4 a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
-  uint32_t p0 = 0, p1 = 0;
-  if (active) {
-    const u32x4* pa = reinterpret_cast<const u32x4*>(src + o.a + v0);
-    a0 = pa[0];
-    a1 = pa[1];
-    p0 = *reinterpret_cast<const uint32_t*>(src + o.b0 + v0 / 8);
-    p1 = *reinterpret_cast<const uint32_t*>(src + o.b1 + v0 / 8);
-  }
   const uint32_t m1 = p0 & p1;   // level-1 code 3
   const uint32_t cnt1 = (uint32_t)__popc(m1);
   const uint32_t rank1 = block_rank(cnt1, lds.wave[0]);   // also publishes the staged slices
@@ -164,7 +168,47 @@ __device__ __forceinline__ void unpack_block(const UnpackList& list, int64_t n, 
   const uint32_t cnt2 = (uint32_t)__popcll(codes2 & (codes2 >> 1) & 0x5555555555555555ull);
   const uint32_t rank2 = block_rank(cnt2, lds.wave[1]);
   if (!active) return;
+  // escapes, in value order (level-2 table, else the level-3 window, else the list): their
+  // exponents go to this thread's bytes of lds.esc, which start cleared
+  uint32_t* esc = lds.esc + t * kEscStride;
+  if (m1) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) esc[i] = 0;
+    uint8_t* escb = reinterpret_cast<uint8_t*>(esc);
+    uint32_t pos3 = (e2_lo & 7) + rank2;   // this thread's next level-3 code in the slice
+    for (uint32_t m = m1, k = 0; m != 0; m &= m - 1, ++k) {
+      const int q = __builtin_ctz(m);
+      const uint32_t c2 = (uint32_t)(codes2 >> (2 * k)) & 3u;
+      uint32_t e;
+      if (c2 < (uint32_t)kPackTable) {
+        e = pick3(c2, t20, t21, t22);
+      } else {
+        const uint32_t c3 = (lds.c3[pos3 >> 3] >> (4 * (pos3 & 7))) & 0xFu;
+        ++pos3;
+        if (c3 < (uint32_t)kPackWindow3) {
+          e = base3 + c3;
+        } else {
+          const uint32_t li = (uint32_t)(32 * t + q);   // index within the block
+          if (l_cnt <= kListLds) {
+            int j = 0;
+            while (j + 1 < l_cnt && lds.li[j] != li) ++j;
+            e = lds.le[j];
+          } else {
+            e = list_global(lidx, lexp, e3_lo, e3_hi, (uint32_t)(blk * kPackBlock) + li);
+          }
+        }
+      }
+      escb[q] = (uint8_t)e;
+    }
+  }
   const uint32_t a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+  // code 3 reads 0 from the table word, and the escape bytes are 0 for the other values
+  const uint32_t lut1 = t10 | (t11 << 8) | (t12 << 16);
+  uint32_t ew[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (m1) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ew[i] = esc[i];
+  }
   uint32_t w[16];
 #pragma unroll
   for (int h = 0; h < 16; ++h) {
@@ -174,38 +218,10 @@ __device__ __forceinline__ void unpack_block(const UnpackList& list, int64_t n, 
       const int q = 2 * h + q2;
       const uint32_t b = (a[q >> 2] >> (8 * (q & 3))) & 0xFFu;
       const uint32_t c = ((p0 >> q) & 1u) | (((p1 >> q) & 1u) << 1);
-      const uint32_t e = c == (uint32_t)kPackTable ? 0u : pick3(c, t10, t11, t12);   // escapes: below
+      const uint32_t e = __builtin_amdgcn_ubfe(lut1, 8 * c, 8) | ((ew[q >> 2] >> (8 * (q & 3))) & 0xFFu);
       pair |= (((b & 0x80u) << 8) | (e << 7) | (b & 0x7Fu)) << (16 * q2);
     }
     w[h] = pair;
-  }
-  // escapes, in value order: level-2 table, else the level-3 window, else the list
-  uint32_t pos3 = (e2_lo & 7) + rank2;   // this thread's next level-3 code in the slice
-  for (uint32_t m = m1, k = 0; m != 0; m &= m - 1, ++k) {
-    const int q = __builtin_ctz(m);
-    const uint32_t c2 = (uint32_t)(codes2 >> (2 * k)) & 3u;
-    uint32_t e;
-    if (c2 < (uint32_t)kPackTable) {
-      e = pick3(c2, t20, t21, t22);
-    } else {
-      const uint32_t c3 = (lds.c3[pos3 >> 3] >> (4 * (pos3 & 7))) & 0xFu;
-      ++pos3;
-      if (c3 < (uint32_t)kPackWindow3) {
-        e = base3 + c3;
-      } else {
-        const uint32_t li = (uint32_t)(32 * t + q);   // index within the block
-        if (l_cnt <= kListLds) {
-          int j = 0;
-          while (j + 1 < l_cnt && lds.li[j] != li) ++j;
-          e = lds.le[j];
-        } else {
-          e = list_global(lidx, lexp, e3_lo, e3_hi, (uint32_t)(blk * kPackBlock) + li);
-        }
-      }
-    }
-    const uint32_t bits = e << (7 + 16 * (q & 1));
-#pragma unroll
-    for (int h = 0; h < 16; ++h) w[h] |= (h == (q >> 1)) ? bits : 0u;
   }
   u32x4* dst = reinterpret_cast<u32x4*>(list.dst[r] + v0);
 #pragma unroll
