@@ -357,6 +357,38 @@ def run_prefill(args, device, config=3):
                 kernel_avg_launch_us={n: v['avg_us'] for n, v in kern.items()})
 
 
+def gemm_ceiling(device):
+    """bf16 rate of AMD's tuned library (hipBLASLt through torch.matmul) on dense GEMMs shaped
+    like the largest expert of each prefill layer, and on 8192^3, measured in the same run: the
+    practical ceiling against which the grouped kernels' MFMA utilisation reads."""
+    shapes = {'qwen3_largest_expert_up_8192x1536x2048': (8192, 1536, 2048),
+              'deepseek_largest_expert_up_57344x2816x2048': (57344, 2816, 2048),
+              'dense_8192x8192x8192': (8192, 8192, 8192)}
+    g = torch.Generator(device=device)
+    g.manual_seed(11)
+    out = {}
+    for name, (m, n, k) in shapes.items():
+        a = torch.randn((m, k), generator=g, device=device).to(torch.bfloat16)
+        b = torch.randn((k, n), generator=g, device=device).to(torch.bfloat16)
+        c = torch.empty((m, n), dtype=torch.bfloat16, device=device)
+        for _ in range(3):
+            torch.matmul(a, b, out=c)
+        ts = []
+        for _ in range(10):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            torch.matmul(a, b, out=c)
+            e1.record()
+            e1.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        ms = float(np.median(ts))
+        tflops = 2 * m * n * k / (ms * 1e-3) / 1e12
+        out[name] = dict(tflops=tflops, frac=tflops / BF16_PEAK_TFLOPS, ms=ms)
+        del a, b, c
+    torch.cuda.empty_cache()
+    return out
+
+
 def prefill_roofline(pre):
     """MFMA roofline of the tiled up-projection launch of the Qwen3 prefill layer."""
     tflops = pre['tiled_up_launch_tflop'] / (pre['tiled_up_avg_us'] * 1e-6)
@@ -615,7 +647,7 @@ def main():
         link_gbs=(dec['copies'] * pk['packed_bytes'] / pk['packed_rows'])
         / (dec['fetch_ms'] * 1e-3) / 1e9 if dec['fetch_ms'] else None,
         note='the misses cross the host link as packed rows (per value a sign|mantissa byte and '
-             'a 3-bit exponent code, escapes in two more levels, lossless) into staging buffers '
+             'a 2-bit exponent code, escapes in three more levels, lossless) into staging buffers '
              'and are unpacked into the cache slots on the GPU; h2d_gbs counts expert bytes '
              'delivered, link_gbs the packed bytes copied')
     line = dict(
@@ -659,6 +691,7 @@ def main():
         line['prefill'] = run_prefill(args, device, 3)
         line['roofline_prefill'] = prefill_roofline(line['prefill'])
         line['prefill_deepseek'] = run_prefill(args, device, 4)
+        line['gemm_ceiling_hipblaslt'] = gemm_ceiling(device)
         print('# prefill layers done', file=sys.stderr, flush=True)
     if not args.no_stacks:
         line.update(run_stacks(args, device))
