@@ -445,6 +445,54 @@ def test_h2d_copy_waits_for_last_use(device, kind):
     eng.close()
 
 
+@pytest.mark.parametrize('packed', [False, True])
+def test_h2d_mark_used_record_orders_copies(device, packed):
+    """mark_used_record: one event both marks the slots (a later copy into slot 0 waits for the
+    reads queued before it) and, once event_synchronize returns, the host sees what the
+    stream's kernels wrote to mapped host memory -- as the runtime reads its routing IDs."""
+    ops = _ops()
+    from ferry_amd.h2d import H2DEngine, PackedPool
+    from ferry_amd.hostmem import mapped_buffer
+    H, I, T, E = 2048, 768, 64, 2
+    rows_w = _pool(2, H, I, seed=23)
+    pool = rows_w.pin_memory()
+    cache = torch.zeros((1, 3 * H * I), dtype=torch.bfloat16, device=device)
+    pk = PackedPool(pool, threads=4) if packed else None
+    eng = H2DEngine.from_packed(cache, pk) if packed else H2DEngine(cache, pool)
+    eng.fetch([0], [0])
+    s = torch.cuda.current_stream()
+    eng.wait_stream([0], s)
+    x = torch.randn((T, H)).to(torch.bfloat16)
+    sel = torch.zeros((T, 1), dtype=torch.int64)
+    w = torch.ones((T, 1), dtype=torch.bfloat16)
+    lay = ops.layout(sel.to(device), w.to(device), E)
+    act = torch.empty((T, I), dtype=torch.bfloat16, device=device)
+    part = torch.empty((T, H), dtype=torch.bfloat16, device=device)
+    for _ in range(20):   # a long read of slot 0 on the compute stream
+        ops.expert_ffn(cache, x.to(device), lay.w_sorted, lay.starts, lay.rows, lay.cols, [0],
+                       np.zeros(E, np.int32), H, I, act, part)
+    host, dptr = mapped_buffer(4096)
+    host.zero_()
+    ids = torch.arange(1, 65, dtype=torch.int64, device=device).reshape(64, 1)
+    hist = dict(ring=torch.zeros(128, dtype=torch.int32, device=device),
+                counts=torch.zeros(E + 62, dtype=torch.int32, device=device),
+                meta=torch.zeros(2, dtype=torch.int32, device=device))
+    ops.history_update(ids % 64, 64, 128, 0, hist['ring'], hist['counts'], hist['meta'], dptr,
+                       dptr + 4 * 64)   # scores and uint8 IDs straight into host memory
+    ev = eng.mark_used_record([0], s)
+    eng.event_synchronize(ev)
+    assert np.array_equal(host[256:320].numpy(), (np.arange(1, 65) % 64).astype(np.uint8))
+    eng.fetch([0], [1])          # overwrite slot 0 with expert 1: must wait for the reads
+    torch.cuda.synchronize()
+    eng.synchronize()
+    ref = execute_experts_ref([rows_w[0]], x, w, [torch.arange(T)], [torch.zeros(T, dtype=torch.long)], H, I)[0]
+    torch.testing.assert_close(part.cpu().float(), ref.float(), rtol=2e-2, atol=1e-2)
+    assert torch.equal(cache[0].cpu(), rows_w[1])
+    empty = eng.mark_used_record([], s)   # no slots: still an event to wait on
+    eng.event_synchronize(empty)
+    eng.close()
+
+
 def test_h2d_kernel_copy_on_caller_stream(device):
     """Kernel-mode copies queued on the caller's stream -- torch's default stream, whose handle
     is 0, and a side stream -- are ordered before that stream's next kernels with no wait."""
