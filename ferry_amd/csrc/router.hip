@@ -564,7 +564,10 @@ __device__ __forceinline__ float sleef_expf(float d) {
 // Sum of e[0..n) (in LDS) in the order of torch's vec::reduce_all(+) for 16-lane vectors:
 // n < 16: left to right; otherwise lane l of an accumulator vector adds e[16c + l] over the
 // full chunks c in order, the tail chunk adds into its first n % 16 lanes, and the 16 lanes are
-// combined by the halving butterfly (l + 8, then l + 4, l + 2, l + 1).  Wave-uniform result.
+// combined by the halving butterfly (l + 8, then l + 4, l + 2, l + 1).  The chunks are read
+// into registers at once; the butterfly moves lanes with DPP row shifts (row_shl:h, lane l
+// reads lane l + h of its row of 16), and lane 0 holds the sum.  Wave-uniform result.
+template <int NS>
 __device__ __forceinline__ float torch_softmax_sum(const float* e, int n, int lane) {
   float acc = 0.f;
   if (n < 16) {
@@ -572,16 +575,27 @@ __device__ __forceinline__ float torch_softmax_sum(const float* e, int n, int la
       acc = e[0];
       for (int i = 1; i < n; ++i) acc += e[i];
     }
-  } else if (lane < 16) {
-    acc = e[lane];
-    const int full = n - n % 16;
-    for (int c = 16; c < full; c += 16) acc += e[c + lane];
-    if (lane < n - full) acc += e[full + lane];
+    return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(acc), 0));
   }
-  if (n >= 16) {
+  const int full = n - n % 16;
+  const int l16 = lane & 15;
+  float v[4 * NS];
 #pragma unroll
-    for (int h = 8; h >= 1; h >>= 1) acc += __shfl_down(acc, h, 16);
-  }
+  for (int c = 0; c < 4 * NS; ++c) v[c] = 16 * c < full ? e[16 * c + l16] : 0.f;
+  const float tail = l16 < n - full ? e[full + l16] : 0.f;
+  acc = v[0];
+#pragma unroll
+  for (int c = 1; c < 4 * NS; ++c)
+    if (16 * c < full) acc += v[c];
+  if (l16 < n - full) acc += tail;
+  uint32_t u = __float_as_uint(acc);
+  acc += dpp_asf(dpp_u<0x108>(u, u));
+  u = __float_as_uint(acc);
+  acc += dpp_asf(dpp_u<0x104>(u, u));
+  u = __float_as_uint(acc);
+  acc += dpp_asf(dpp_u<0x102>(u, u));
+  u = __float_as_uint(acc);
+  acc += dpp_asf(dpp_u<0x101>(u, u));
   return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(acc), 0));
 }
 
@@ -664,7 +678,7 @@ __global__ __launch_bounds__(64 * kWaves) void router_kernel(
       if (e < n) ws.prob[e] = ex[s];
     }
     wave_sync_lds();
-    const float sum = torch_softmax_sum(ws.prob, n, lane);
+    const float sum = torch_softmax_sum<NS>(ws.prob, n, lane);
     wave_sync_lds();
     const float inv = 1.0f / sum;
     uint32_t key[NS];

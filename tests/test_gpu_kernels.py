@@ -290,6 +290,8 @@ def test_expert_ffn_and_combine_vs_oracle(device, T, E, k, H, I, zipf):
     (2048, 768, [1, 5, 16, 17, 31, 32, 33, 47, 64, 3, 0, 64], False),
     (2048, 768, [1, 5, 16, 17, 31, 32, 33, 47, 64, 3, 0, 64], True),
     (2048, 768, [1, 2, 3, 4, 8, 12, 16, 16], True),          # decode: skinny kernels only
+    # decode, six experts: the one-launch kernel with 8-column up workgroups
+    (2048, 768, [16, 1, 7, 3, 9, 16], True),
     # other multiples of 256: the unpipelined 8-row x 128-byte phase-1 path (the pipelined one
     # serves H = 2048)
     (1024, 256, [1, 3, 16, 9], True),
