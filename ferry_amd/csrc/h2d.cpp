@@ -605,23 +605,25 @@ extern "C" int ferry_h2d_wait_stream(ferry_h2d* h, const int64_t* slots, int64_t
 extern "C" int ferry_h2d_mark_used(ferry_h2d* h, const int64_t* slots, int64_t n, void* stream) {
   ferry::clear_error();
   if (n == 0) return 0;
-  std::shared_ptr<Event> ev;
-  H2D_HIP(record_event(h, (hipStream_t)stream, &ev));
-  for (int64_t i = 0; i < n; ++i) {
-    const int64_t slot = slots[i];
-    if (slot < 0 || slot >= h->cache_rows) {
-      ferry::set_error("h2d_mark_used: slot %lld out of range", (long long)slot);
+  if (!h || !slots || n < 0) {
+    ferry::set_error("h2d_mark_used: bad arguments");
+    return 2;
+  }
+  for (int64_t i = 0; i < n; ++i)
+    if (slots[i] < 0 || slots[i] >= h->cache_rows) {
+      ferry::set_error("h2d_mark_used: slot %lld out of range", (long long)slots[i]);
       return 2;
     }
-    h->used[(size_t)slot] = ev;
-  }
+  std::shared_ptr<Event> ev;
+  H2D_HIP(record_event(h, (hipStream_t)stream, &ev));
+  for (int64_t i = 0; i < n; ++i) h->used[(size_t)slots[i]] = ev;
   return 0;
 }
 
 extern "C" int ferry_h2d_mark_used_record(ferry_h2d* h, const int64_t* slots, int64_t n,
                                           void* stream, void** event_out) {
   ferry::clear_error();
-  if (!h || !event_out || n < 0) {
+  if (!h || !event_out || n < 0 || (n > 0 && !slots)) {
     ferry::set_error("h2d_mark_used_record: bad arguments");
     return 2;
   }

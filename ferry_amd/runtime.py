@@ -258,6 +258,11 @@ class OffloadRuntime:
         resident_list = np.flatnonzero(active & ~missing)
         slot32 = slot_of.astype(np.int32)
         common = (self.cache, hidden.contiguous(), lay.w_sorted, lay.starts, lay.rows, lay.cols)
+        if not self.timing:
+            # the reads below are marked by the next call's ID event on this stream (or by
+            # _flush_used); set before they are queued, so that a call that fails part-way still
+            # orders later copies into these slots after whatever it queued
+            self._pending_used = (slot_of[np.flatnonzero(active)], stream.cuda_stream, stream)
         if not self.overlap and len(fetches):
             started = time.perf_counter_ns()
             self.h2d.wait_host(fetches[:, 2])
@@ -290,8 +295,6 @@ class OffloadRuntime:
                 self._ffn(common, np.sort(missing_keys[g]), slot32, buf, stream, counts_e)
         if self.timing:
             self.h2d.mark_used(slot_of[np.flatnonzero(active)], stream)
-        else:   # marked by the next call's ID event on this stream (or by _flush_used)
-            self._pending_used = (slot_of[np.flatnonzero(active)], stream.cuda_stream, stream)
         if timing:
             self.timings.append((ev, waits, (mark, self.ops.timing_mark())))
             self.step_marks.append((d2h, ev[0], ev[1], waits[-1][1] if waits else None))
