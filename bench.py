@@ -389,6 +389,47 @@ def gemm_ceiling(device):
     return out
 
 
+def read_ceiling(device, block, expert_bytes, reps=9):
+    """Plain cold reads (the library's hbm_read, 32 KiB workgroups) of the byte counts of a decode
+    step's two FFN launches (the resident experts', the fetched experts'), measured in the same
+    run: the practical ceiling against which the decode FFN's HBM fraction reads.  A 1 GiB read
+    before each repeat evicts the buffers from the memory-side cache."""
+    from ferry_amd import expert_ops as ops
+    fetched = block['misses_per_step']
+    resident = block['active_experts_per_step'] - fetched
+    sizes = {'resident_launch': resident * expert_bytes, 'fetched_launch': fetched * expert_bytes}
+    flush = torch.ones(1 << 30, dtype=torch.uint8, device=device)
+    bufs = {k: torch.ones(int(v) // 256 * 256, dtype=torch.uint8, device=device)
+            for k, v in sizes.items()}
+    sink = torch.empty(int(flush.numel() // 512) + 16, dtype=torch.uint8, device=device)
+    times = {k: [] for k in bufs}
+    for _ in range(reps):
+        ops.hbm_read(flush, sink)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(bufs) + 1)]
+        ev[0].record()
+        for i, b in enumerate(bufs.values()):
+            ops.hbm_read(b, sink)
+            ev[i + 1].record()
+        ev[-1].synchronize()
+        for i, k in enumerate(bufs):
+            times[k].append(ev[i].elapsed_time(ev[i + 1]) * 1e3)
+    out = {}
+    total_b = total_us = 0.0
+    for k, b in bufs.items():
+        us = float(np.median(times[k]))
+        out[k] = dict(bytes=b.numel(), us=us, gbs=b.numel() / (us * 1e-6) / 1e9,
+                      frac=b.numel() / (us * 1e-6) / 1e9 / HBM_PEAK_GBS)
+        total_b += b.numel()
+        total_us += us
+    read_gbs = total_b / (total_us * 1e-6) / 1e9
+    out.update(kernel='hbm_read_kernel (plain read, 32 KiB workgroups, data cold)',
+               both_gbs=read_gbs, both_frac=read_gbs / HBM_PEAK_GBS,
+               ffn_over_read=block['ffn_gbs'] / read_gbs)
+    del flush, bufs
+    torch.cuda.empty_cache()
+    return out
+
+
 def prefill_roofline(pre):
     """MFMA roofline of the tiled up-projection launch of the Qwen3 prefill layer."""
     tflops = pre['tiled_up_launch_tflop'] / (pre['tiled_up_avg_us'] * 1e-6)
@@ -675,6 +716,7 @@ def main():
                     fetch='hipMemcpyAsync of packed rows on two DMA streams, unpacked on the GPU',
                     parallelism='single GPU (one expert-parallel share)'),
         roofline=roofline, decode=block)
+    block['read_ceiling'] = read_ceiling(device, block, w.spec.expert_bytes)
     print(f'# decode done: {line["value"]:.0f} tokens/s', file=sys.stderr, flush=True)
     # the same decode stream with the copy kernel on the compute stream (not the reference's
     # fetch scheme, so not the headline): one launch per fetch, then one FFN launch

@@ -69,6 +69,8 @@ SIGNATURES = [
     ('ferry_timing_mark', _i64, []),
     ('ferry_timing_range', ctypes.c_int, [_i64, _i64, _c_p]),
     ('ferry_timing_overlap', ctypes.c_int, [_i64, _i64, _c_p, _c_p, _c_p]),
+    ('ferry_hbm_read_sink_bytes', ctypes.c_int64, [_i64]),
+    ('ferry_hbm_read', ctypes.c_int, [_c_p, _i64, _c_p, _i64, _c_p]),
     ('ferry_timing_summary', ctypes.c_int,
      [ctypes.c_char_p, ctypes.POINTER(_i64), ctypes.POINTER(ctypes.c_double)]),
 ]

@@ -204,6 +204,22 @@ def ffn_sync_timeouts():
     return int(n.value)
 
 
+def hbm_read(buf, sink=None):
+    """Read every byte of ``buf`` (a contiguous CUDA tensor, nbytes a multiple of 16) once at the
+    HBM read rate, on the current stream: the measured read ceiling for the memory-bound
+    kernels (no reference counterpart).  Returns ``sink`` (uint8, created when not given): one
+    16-byte record per wavefront, the XOR of the 16-byte words it read."""
+    if not (isinstance(buf, torch.Tensor) and buf.is_cuda and buf.is_contiguous()):
+        raise RuntimeError('hbm_read: buf must be a contiguous CUDA tensor')
+    nbytes = buf.numel() * buf.element_size()
+    need = int(lib().ferry_hbm_read_sink_bytes(nbytes))
+    if sink is None:
+        sink = torch.empty(max(need, 16), dtype=torch.uint8, device=buf.device)
+    st = torch.cuda.current_stream(buf.device).cuda_stream
+    check(lib().ferry_hbm_read(buf.data_ptr(), nbytes, sink.data_ptr(), sink.numel(), st), 'hbm_read')
+    return sink
+
+
 def combine(part, tokens, topk, hidden, pair_pos=None, out=None, addend=None):
     """out[t] = bf16(sum_j fp32(part[src(t, j)])), j ascending (expert_ops.cpp:75-92).
 

@@ -40,6 +40,14 @@ int ferry_timing_range(int64_t begin, int64_t end, double* total_ms);
  * flight, when t0 / t1 bracket the copies */
 int ferry_timing_overlap(int64_t begin, int64_t end, void* t0, void* t1, double* total_ms);
 
+/* A plain read of `bytes` (a multiple of 16) of device memory at `data` (16-byte aligned) on
+ * `stream`: the HBM read ceiling that memory-bound kernels are measured against (a measurement
+ * aid with no reference counterpart).  Each wavefront of the launch reads 8 KiB and stores the
+ * XOR of its 16-byte words at sink + 16 * w (device memory, 16-byte aligned, at least
+ * ferry_hbm_read_sink_bytes(bytes) bytes): the XOR of those records is the XOR of the range. */
+int64_t ferry_hbm_read_sink_bytes(int64_t bytes);
+int ferry_hbm_read(const void* data, int64_t bytes, void* sink, int64_t sink_bytes, void* stream);
+
 enum { FERRY_BF16 = 0, FERRY_F32 = 1 };
 
 /*

@@ -330,6 +330,21 @@ def test_small_expert_kernels_vs_oracle(device, H, I, counts, split):
                                    msg=lambda m: f'expert {e} ({c} rows): {m}')
 
 
+@pytest.mark.parametrize('nbytes', [16, 4096 + 16, 3 * 32768 + 48, 5_000_000 // 16 * 16])
+def test_hbm_read_xor(device, nbytes):
+    """The read-ceiling kernel reads every 16-byte word once: its per-lane XOR equals numpy's."""
+    ops = _ops()
+    data = np.random.default_rng(nbytes).integers(0, 256, nbytes, dtype=np.uint8)
+    buf = torch.from_numpy(data).to(device)
+    sink = ops.hbm_read(buf)
+    torch.cuda.synchronize()
+    want = np.bitwise_xor.reduce(data.view(np.uint32).reshape(-1, 4), axis=0)
+    got = np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32).reshape(-1, 4), axis=0)
+    assert np.array_equal(got, want)
+    with pytest.raises(RuntimeError, match='multiple of 16'):
+        ops.hbm_read(buf[:nbytes - 8] if nbytes > 16 else buf[:8])
+
+
 def test_execute_experts_api(device):
     """The reference's execute_experts signature (expert_ops.cpp:16-45) on groups of any size."""
     ops = _ops()
