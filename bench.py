@@ -717,6 +717,8 @@ def main():
                     parallelism='single GPU (one expert-parallel share)'),
         roofline=roofline, decode=block)
     block['read_ceiling'] = read_ceiling(device, block, w.spec.expert_bytes)
+    roofline['read_ceiling_gbs'] = block['read_ceiling']['both_gbs']
+    roofline['frac_of_read_ceiling'] = roofline['achieved'] / block['read_ceiling']['both_gbs']
     print(f'# decode done: {line["value"]:.0f} tokens/s', file=sys.stderr, flush=True)
     # the same decode stream with the copy kernel on the compute stream (not the reference's
     # fetch scheme, so not the headline): one launch per fetch, then one FFN launch
