@@ -34,8 +34,8 @@ Also on the line:
   * decode_copy_kernel: the headline stream through OffloadRuntime(copy='kernel'): raw misses
     copied by one kernel launch on the compute stream, then one FFN launch (no overlap);
   * cpu_baseline: the reference's op order in torch on the host cores (all cores of the
-    process's affinity), median of >= 5 repeats on the decode stream, plus one config-3 prefill
-    layer with the 48-layer extrapolation.
+    process's affinity), median of >= 5 repeats on the decode stream, plus one Qwen3 8192-token
+    prefill layer with the 48-layer extrapolation.
 """
 import argparse
 import json
@@ -85,7 +85,7 @@ def parse():
     p.add_argument('--no-cpu-baseline', action='store_true')
     p.add_argument('--cpu-seconds', type=float, default=20.0,
                    help='CPU time budget of the decode-stream baseline (5 repeats)')
-    p.add_argument('--loop-steps', type=int, default=8, help='decode-loop steps (config 5 runs 64)')
+    p.add_argument('--loop-steps', type=int, default=8, help='decode-loop steps (the reference loop runs 64)')
     p.add_argument('--copy-calibration-mib', type=int, default=0,
                    help='run one plain device copy kernel of this many MiB (read and written) '
                         'before the decode pass: the reference dispatch for scaling HBM byte '
@@ -103,14 +103,14 @@ def run_stacks(args, device):
     from ferry_amd import workloads
     from ferry_amd.h2d import PackedPool
     out = {}
-    for cfg in (3, 4):
-        w = workloads.CONFIGS[cfg]
-        layers = w.layers if cfg == 4 else 48
+    for w in (workloads.QWEN3_PREFILL_STACK, workloads.DEEPSEEK_PREFILL_STACK):
+        qwen3 = w is workloads.QWEN3_PREFILL_STACK
+        layers = 48 if qwen3 else w.layers
         t0 = time.perf_counter()
         pool = workloads.make_pool(w.spec, layers, seed=w.seed)
         pool_s = time.perf_counter() - t0
-        raw = raw_summary(run_prefill_stack(device, cfg, pool))
-        if cfg == 3:
+        raw = raw_summary(run_prefill_stack(device, w, pool))
+        if qwen3:
             loop_raw = raw_summary(run_decode_loop(device, args.loop_steps, pool))
         del pool
         gc.collect()
@@ -120,11 +120,11 @@ def run_stacks(args, device):
         pack_s = time.perf_counter() - t0
         del src
         gc.collect()
-        key = 'prefill_stack' if cfg == 3 else 'prefill_stack_deepseek'
-        out[key] = run_prefill_stack(device, cfg, packed)
+        key = 'prefill_stack' if qwen3 else 'prefill_stack_deepseek'
+        out[key] = run_prefill_stack(device, w, packed)
         out[key].update(pool_build_s=pool_s, pack_s=pack_s, pack_ratio=packed.ratio, raw=raw)
         print(f'# {key} done', file=sys.stderr, flush=True)
-        if cfg == 3:
+        if qwen3:
             out['decode_loop'] = run_decode_loop(device, args.loop_steps, packed)
             out['decode_loop']['raw'] = loop_raw
             print('# decode loop done', file=sys.stderr, flush=True)
@@ -147,7 +147,7 @@ def launch_stats(ops, name):
 
 
 # ---------------------------------------------------------------------------------------------
-# config 2: the decode layer (headline)
+# the decode layer (headline)
 # ---------------------------------------------------------------------------------------------
 
 def decode_stream(w, steps, device):
@@ -170,7 +170,7 @@ def run_decode(args, device, copy='dma', pack=False):
     from ferry_amd import workloads
     from ferry_amd.quota import Topology
     from ferry_amd.runtime import OffloadRuntime
-    w = workloads.CONFIGS[2]
+    w = workloads.QWEN3_DECODE_LAYER
     spec = w.spec
     pool = workloads.make_pool(spec, 1, seed=0)
     rt = OffloadRuntime(spec, pool, [w.cache_slots], 'ferry', Topology.uniform(1, spec.experts),
@@ -276,16 +276,15 @@ def decode_block(dec, args):
 
 
 # ---------------------------------------------------------------------------------------------
-# configs 3 / 4: one prefill layer, experts resident
+# the prefill layers: one layer, experts resident
 # ---------------------------------------------------------------------------------------------
 
-def run_prefill(args, device, config=3):
-    """One prefill layer with every expert resident in HBM: the Qwen3-shaped 8192-token layer
-    (config 3 shape) or the DeepSeek-V2-Lite-shaped 65,536-token layer with its two shared
-    experts (config 4 shape)."""
+def run_prefill(args, device, w):
+    """One prefill layer with every expert resident in HBM, of workload ``w``: the Qwen3-shaped
+    8192-token layer (QWEN3_PREFILL_STACK's shape) or the DeepSeek-V2-Lite-shaped 65,536-token
+    layer with its two shared experts (DEEPSEEK_PREFILL_STACK's shape)."""
     from ferry_amd import expert_ops as ops
     from ferry_amd import workloads
-    w = workloads.CONFIGS[config]
     spec = replace(w.spec, moe_layers=w.spec.moe_layers[:1])
     E, k, H, I, T = spec.experts, spec.topk, spec.hidden, spec.intermediate, w.tokens
     cache = workloads.expert_rows(range(E), spec.expert_elements, seed=w.seed, device=device)
@@ -332,7 +331,7 @@ def run_prefill(args, device, config=3):
     tiled_rows = int(counts[counts > 64].sum()) + (T if Is else 0)
     tiled_up_flops = 2 * 2 * H * (I * int(counts[counts > 64].sum()) + (Is * T if Is else 0))
     gemm_ms = up_ms + down_ms
-    name = ('qwen3_30b_a3b_moe_prefill_t8192_layer_resident' if config == 3 else
+    name = ('qwen3_30b_a3b_moe_prefill_t8192_layer_resident' if w is workloads.QWEN3_PREFILL_STACK else
             'deepseek_v2_lite_moe_prefill_t65536_layer_resident_shared2')
     tu = kern['ffn_tiled_up']
     # the shared experts' launches add to the tiled kernel's launch count (one per layer call)
@@ -446,17 +445,16 @@ def prefill_roofline(pre):
 
 
 # ---------------------------------------------------------------------------------------------
-# configs 3 / 4 over the whole stack, and config 5
+# the prefill stacks over every layer, and the decode loop
 # ---------------------------------------------------------------------------------------------
 
-def run_prefill_stack(device, config, pool):
+def run_prefill_stack(device, w, pool):
     """Every MoE layer of the model on one prefill batch through OffloadRuntime with the pooled
     30 % cache, from cold.  Pass 1 is timed; pass 2 (after a reset) records fetch events."""
     from ferry_amd import expert_ops as ops
     from ferry_amd import workloads
     from ferry_amd.quota import Topology
     from ferry_amd.runtime import OffloadRuntime
-    w = workloads.CONFIGS[config]
     spec = w.spec
     L, E, k, H, T = w.layers, spec.experts, spec.topk, spec.hidden, w.tokens
     gen = workloads.RouterLogits(w, device)
@@ -516,7 +514,7 @@ def run_decode_loop(device, steps, pool):
     from ferry_amd import workloads
     from ferry_amd.quota import Topology
     from ferry_amd.runtime import OffloadRuntime
-    w = workloads.CONFIGS[5]
+    w = workloads.QWEN3_DECODE_LOOP
     spec = w.spec
     L, E, H = w.layers, spec.experts, spec.hidden
     routing = workloads.decode_loop_routing(w, steps=2 * steps)
@@ -574,7 +572,7 @@ def run_decode_loop(device, steps, pool):
         hidden_cap=min(1.0, ffn / fetch_ms) if fetch_ms else None,
         eviction_state_sha1=digest.hexdigest(),
         note=('throughput, misses and eviction state from the plain steps; fetch, FFN and hidden '
-              'fractions from as many further steps with per-launch timing on; config 5 runs 64 '
+              'fractions from as many further steps with per-launch timing on; the reference\'s loop runs 64 '
               'steps'))
     rt.close()
     return res
@@ -651,11 +649,11 @@ def cpu_baseline(dec, seconds, device, with_prefill=True):
     out = dict(value=statistics.median(rates), unit='tokens/s', cores=cores, kind='port',
                cpu_model=cpu_model(), repeats=[round(r, 1) for r in rates], statistic='median of 5',
                sample=f'5 repeats x {n} decode steps ({n * w.tokens} tokens) of the same seeded '
-                      f'stream (config 2); experts read from host memory (no H2D copy on the CPU '
+                      f'stream (the decode layer); experts read from host memory (no H2D copy on the CPU '
                       f'path)')
     if with_prefill:
-        # one config-3 prefill layer (8192 tokens, experts resident in host memory)
-        w3 = workloads.CONFIGS[3]
+        # one Qwen3 8192-token prefill layer (experts resident in host memory)
+        w3 = workloads.QWEN3_PREFILL_STACK
         T = w3.tokens
         lg = workloads.RouterLogits(replace(w3, layers=1), device).next(0, T).cpu()
         x = workloads.hidden_states(T, H, seed=w3.seed + 7, device=device).cpu()
@@ -745,9 +743,10 @@ def main():
     print(f'# decode (raw rows) done: {line["decode_raw"]["tokens_per_s"]:.0f} tokens/s',
           file=sys.stderr, flush=True)
     if not args.no_prefill:
-        line['prefill'] = run_prefill(args, device, 3)
+        from ferry_amd import workloads
+        line['prefill'] = run_prefill(args, device, workloads.QWEN3_PREFILL_STACK)
         line['roofline_prefill'] = prefill_roofline(line['prefill'])
-        line['prefill_deepseek'] = run_prefill(args, device, 4)
+        line['prefill_deepseek'] = run_prefill(args, device, workloads.DEEPSEEK_PREFILL_STACK)
         line['gemm_ceiling_hipblaslt'] = gemm_ceiling(device)
         print('# prefill layers done', file=sys.stderr, flush=True)
     if not args.no_stacks:

@@ -27,27 +27,30 @@ class Workload:
     renorm: bool
     sorted: bool
     shared_intermediate: int = 0   # DeepSeek shared experts (2 x 1408)
-    steps: int = 1                 # decode steps (config 5)
-    prefill_tokens: int = 0        # synthetic prefill before decode (config 5)
+    steps: int = 1                 # decode steps (the decode loop)
+    prefill_tokens: int = 0        # synthetic prefill before decode (the decode loop)
 
 
 def _one_layer(spec):
     return replace(spec, moe_layers=spec.moe_layers[:1])
 
 
-CONFIGS = {
-    1: Workload('deepseek_v2_lite_layer_t256_resident', _one_layer(DEEPSEEK_V2_LITE), 256, 64, 0.0, 0,
-                1, torch.float32, False, False, shared_intermediate=2 * 1408),
-    2: Workload('qwen3_30b_a3b_moe_layer_decode_t16_cache38', _one_layer(QWEN3_30B_A3B), 16, 38, 1.1, 1,
-                1, torch.bfloat16, True, True),
-    3: Workload('qwen3_30b_a3b_moe_prefill_t8192_48layers', QWEN3_30B_A3B, 8192,
-                int(48 * 128 * 0.30), 1.1, 1, 48, torch.bfloat16, True, True),
-    4: Workload('deepseek_v2_lite_moe_prefill_t65536_26layers', DEEPSEEK_V2_LITE, 65536,
-                int(26 * 64 * 0.30), 0.9, 2, 26, torch.float32, False, False,
-                shared_intermediate=2 * 1408),
-    5: Workload('qwen3_30b_a3b_decode_loop_t64_48layers', QWEN3_30B_A3B, 64, int(48 * 128 * 0.30),
-                1.1, 1, 48, torch.bfloat16, True, True, steps=64, prefill_tokens=1024),
-}
+# the evaluated workloads, by what they are
+DEEPSEEK_LAYER_T256 = Workload('deepseek_v2_lite_layer_t256_resident', _one_layer(DEEPSEEK_V2_LITE), 256,
+                               64, 0.0, 0, 1, torch.float32, False, False,
+                               shared_intermediate=2 * 1408)
+QWEN3_DECODE_LAYER = Workload('qwen3_30b_a3b_moe_layer_decode_t16_cache38', _one_layer(QWEN3_30B_A3B), 16,
+                              38, 1.1, 1, 1, torch.bfloat16, True, True)
+QWEN3_PREFILL_STACK = Workload('qwen3_30b_a3b_moe_prefill_t8192_48layers', QWEN3_30B_A3B, 8192,
+                               int(48 * 128 * 0.30), 1.1, 1, 48, torch.bfloat16, True, True)
+DEEPSEEK_PREFILL_STACK = Workload('deepseek_v2_lite_moe_prefill_t65536_26layers', DEEPSEEK_V2_LITE, 65536,
+                                  int(26 * 64 * 0.30), 0.9, 2, 26, torch.float32, False, False,
+                                  shared_intermediate=2 * 1408)
+QWEN3_DECODE_LOOP = Workload('qwen3_30b_a3b_decode_loop_t64_48layers', QWEN3_30B_A3B, 64,
+                             int(48 * 128 * 0.30), 1.1, 1, 48, torch.bfloat16, True, True, steps=64,
+                             prefill_tokens=1024)
+WORKLOADS = {w.name: w for w in (DEEPSEEK_LAYER_T256, QWEN3_DECODE_LAYER, QWEN3_PREFILL_STACK,
+                                 DEEPSEEK_PREFILL_STACK, QWEN3_DECODE_LOOP)}
 
 
 def zipf_log_bias(experts, s, rng):
@@ -165,7 +168,7 @@ def decode_loop_routing(workload, seed=None, steps=None, keep=0.8):
 
 
 def temporal_routing(workload, steps, tokens, seed, keep=0.8):
-    """Config 5 routing: each token keeps each previous expert with p = keep, else resamples
+    """Routing of the 48-layer decode loop: each token keeps each previous expert with p = keep, else resamples
     from Zipf(s) without duplicates.  Returns int64 [steps, layers, tokens, k] and the fp32
     logits whose renormalised softmax over the chosen set gives the weights."""
     w = workload

@@ -281,7 +281,7 @@ def test_workload_generators_are_seeded():
     assert np.array_equal(a, b)
     p = np.exp(a.astype(np.float64))
     assert abs(p.sum() - 1) < 1e-5 and np.isclose(p.max() / p.min(), 128 ** 1.1, rtol=1e-3)
-    w = workloads.CONFIGS[5]
+    w = workloads.QWEN3_DECODE_LOOP
     sel, logits = workloads.temporal_routing(w, steps=3, tokens=4, seed=0)
     assert sel.shape == (3, 48, 4, 8)
     for row in sel.reshape(-1, 8):

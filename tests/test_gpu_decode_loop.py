@@ -20,7 +20,7 @@ def test_decode_loop_eviction_sequence_bit_exact(device):
     from ferry_amd import workloads
     from ferry_amd.quota import Topology
     from ferry_amd.runtime import OffloadRuntime
-    w = workloads.CONFIGS[5]
+    w = workloads.QWEN3_DECODE_LOOP
     spec = replace(w.spec, hidden=256, intermediate=128)
     L, E, k = w.layers, spec.experts, spec.topk
     cap = w.cache_slots
@@ -64,14 +64,14 @@ def test_decode_loop_eviction_sequence_bit_exact(device):
 
 
 def test_decode_steps_full_expert_shape(device):
-    """The config-5 call shapes with full-size Qwen3-30B-A3B experts (H = 2048, I = 768): a
+    """The decode loop's call shapes with full-size Qwen3-30B-A3B experts (H = 2048, I = 768): a
     1024-token prefill and three 64-token decode steps over 4 layers of the temporal-locality
     routing, with a cache small enough to fetch and evict every step.  Every token's output is
     checked against the oracle, and the eviction sequence against the oracle planner."""
     from ferry_amd import workloads
     from ferry_amd.quota import Topology
     from ferry_amd.runtime import OffloadRuntime
-    w = replace(workloads.CONFIGS[5], layers=4)
+    w = replace(workloads.QWEN3_DECODE_LOOP, layers=4)
     spec = replace(w.spec, moe_layers=w.spec.moe_layers[:4])
     L, E, k, H, I = 4, spec.experts, spec.topk, spec.hidden, spec.intermediate
     assert (H, I, w.tokens, w.prefill_tokens) == (2048, 768, 64, 1024)

@@ -71,7 +71,7 @@ def test_deepseek_layer_t256_all_resident(device):
     from ferry_amd.model import deepseek_moe
     from ferry_amd.quota import Topology
     from ferry_amd.runtime import OffloadRuntime
-    w = workloads.CONFIGS[1]
+    w = workloads.DEEPSEEK_LAYER_T256
     spec = w.spec
     E, k, H, I, T = spec.experts, spec.topk, spec.hidden, spec.intermediate, w.tokens
     pool = workloads.make_pool(spec, 1, seed=w.seed)
@@ -115,7 +115,7 @@ def test_deepseek_prefill_t65536_sampled_tokens(device):
     from ferry_amd.model import deepseek_moe
     from ferry_amd.quota import Topology
     from ferry_amd.runtime import OffloadRuntime
-    w = workloads.CONFIGS[4]
+    w = workloads.DEEPSEEK_PREFILL_STACK
     spec = replace(w.spec, moe_layers=w.spec.moe_layers[:1])
     E, k, H, I, T = spec.experts, spec.topk, spec.hidden, spec.intermediate, w.tokens
     assert (E, k, H, I, T, w.shared_intermediate) == (64, 6, 2048, 1408, 65536, 2816)

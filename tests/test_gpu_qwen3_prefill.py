@@ -60,7 +60,7 @@ def test_qwen3_prefill_t8192_full_layer(device):
     from ferry_amd import workloads
     from ferry_amd.quota import Topology
     from ferry_amd.runtime import OffloadRuntime
-    w = workloads.CONFIGS[3]
+    w = workloads.QWEN3_PREFILL_STACK
     spec = replace(w.spec, moe_layers=w.spec.moe_layers[:1])
     E, k, H, I, T = spec.experts, spec.topk, spec.hidden, spec.intermediate, w.tokens
     assert (E, k, H, I, T) == (128, 8, 2048, 768, 8192)
