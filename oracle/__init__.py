@@ -3,7 +3,7 @@
 Restatements of the reference algorithms on the CPU (numpy, torch-CPU, and C in
 ref_core.c), each citing the reference file:line it follows.  Only the test suite,
 ``__graft_entry__.smoke()`` and the CPU-baseline leg of ``bench.py`` may import this package,
-and only as the checker; the product (ferry_amd) never calls it.
+and only to check results or as the timed CPU baseline; the product (ferry_amd) never calls it.
 
 How each function is pinned (beyond restating the reference):
   topk (ref_core.c)      -- index-for-index against torch.topk on the CPU (the library the

@@ -1,7 +1,7 @@
 /*
  * CPU oracle (test infrastructure only): C restatements of the integer/selection parts of
  * FERRY's per-GPU MoE path.  Nothing in the product links this file; only tests, the smoke
- * check and the CPU-baseline leg of the benchmark load it, as the checker.
+ * check and the CPU-baseline leg of the benchmark load it, to check results.
  *
  *  1. oracle_topk   -- torch's CPU top-k (ATen/native/TopKImpl.h, topk_impl_loop), which the
  *                      reference router calls at ferry/model.py:143.  torch selects with
