@@ -661,6 +661,31 @@ extern "C" int ferry_h2d_synchronize(ferry_h2d* h) {
   return 0;
 }
 
+extern "C" int ferry_h2d_reset(ferry_h2d* h) {
+  ferry::clear_error();
+  if (!h) {
+    ferry::set_error("h2d_reset: null engine");
+    return 2;
+  }
+  if (ferry_h2d_synchronize(h) != 0) return 3;
+  const size_t rows = (size_t)h->cache_rows;
+  for (int l = 0; l < kLanes; ++l) h->copy_done[l].assign(rows, nullptr);
+  h->copy_seq.assign(rows, -1);
+  h->batch_of.assign(rows, 0);
+  h->used.assign(rows, nullptr);
+  h->ring_ev.assign(h->ring_ev.size(), nullptr);
+  h->ring_next = 0;
+  h->kernel_last.clear();
+  h->marker.reset();
+  h->kind = FERRY_H2D_DMA;
+  h->kernel_stream = h->stream[0];
+  h->defer_last = false;
+  h->batch = 0;
+  h->seq = 0;
+  h->copies = 0;
+  return 0;
+}
+
 extern "C" int64_t ferry_h2d_copies(const ferry_h2d* h) { return h ? h->copies : 0; }
 
 extern "C" int ferry_h2d_set_engine(ferry_h2d* h, int32_t kind) {

@@ -99,6 +99,12 @@ class H2DEngine:
     def synchronize(self):
         check(lib().ferry_h2d_synchronize(self._h), 'H2DEngine.synchronize')
 
+    def reset(self):
+        """The state of a new engine (no copies or reads recorded, ``copies`` 0, DMA mode) on the
+        same streams and buffers, after all of its work has finished."""
+        check(lib().ferry_h2d_reset(self._h), 'H2DEngine.reset')
+        self._defer_last = False
+
     @property
     def engine(self):
         """How rows are copied: ``KERNEL`` or ``DMA``."""

@@ -102,9 +102,11 @@ class OffloadRuntime:
         self.history = GateHistory(spec.layers, spec.experts, self.window)
         self.device_history = DeviceGateHistory(spec.layers, spec.experts, spec.topk, self.window,
                                                 self.device)
+        # the engine is reset in place rather than rebuilt: a new engine's streams can land on
+        # the hardware queue of this runtime's compute stream and serialise with it
         if self.h2d is not None:
-            self.h2d.close()
-        if self.packed is not None:
+            self.h2d.reset()
+        elif self.packed is not None:
             self.h2d = self.ops.H2DEngine.from_packed(self.cache, self.packed)
         else:
             self.h2d = self.ops.H2DEngine(self.cache, self.pool)

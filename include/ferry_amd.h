@@ -239,6 +239,12 @@ int ferry_h2d_mark_used_record(ferry_h2d* h, const int64_t* slots, int64_t n, vo
 int ferry_h2d_event_synchronize(ferry_h2d* h, void* event);
 /* expert_ops.cpp:130-133 */
 int ferry_h2d_synchronize(ferry_h2d* h);
+/* The state of a new engine on the same streams and buffers (runtime.py:51-62 builds a new
+ * H2DEngine on reset): waits for all of the engine's work, then forgets every slot's copies and
+ * reads and zeroes the copy counter; DMA mode, the engine's own kernel stream, no deferred
+ * unpack.  Keeping the streams keeps their hardware queues: a new engine's streams can land on
+ * the queue of the caller's compute stream and serialise with it. */
+int ferry_h2d_reset(ferry_h2d* h);
 /* expert_ops.cpp:135 */
 int64_t ferry_h2d_copies(const ferry_h2d* h);
 /* the engine's copy stream (for event timing by the caller): after a fetch call its queue ends

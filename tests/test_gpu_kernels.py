@@ -428,6 +428,33 @@ def test_h2d_fetch_and_counters(device, kind):
     eng.close()
 
 
+@pytest.mark.parametrize('packed', [False, True])
+def test_h2d_reset_in_place(device, packed):
+    """reset(): a new engine's state on the same streams -- copies 0, DMA mode, no deferred
+    unpack -- and fetches afterwards byte-exact, also into slots written before the reset."""
+    from ferry_amd import h2d
+    from ferry_amd.h2d import H2DEngine, PackedPool
+    rows, cap = 8, 4
+    pool = (torch.randn((rows, 3 * 256 * 128)) * 0.02).to(torch.bfloat16).pin_memory()
+    cache = torch.zeros((cap, pool.shape[1]), dtype=torch.bfloat16, device=device)
+    pk = PackedPool(pool) if packed else None
+    eng = H2DEngine.from_packed(cache, pk) if packed else H2DEngine(cache, pool)
+    if packed:
+        eng.defer_last = True
+    eng.fetch([0, 1, 2], [5, 6, 7])
+    eng.wait_stream([0, 1, 2], torch.cuda.current_stream())
+    eng.engine = h2d.KERNEL
+    eng.reset()
+    assert eng.copies == 0 and eng.engine == h2d.DMA and not eng.defer_last
+    eng.wait_stream([0, 3], torch.cuda.current_stream())   # nothing recorded: no wait
+    eng.fetch([3, 0, 1], [1, 2, 3])
+    eng.wait_host([3, 0, 1])
+    assert eng.copies == 3
+    for slot, key in ((3, 1), (0, 2), (1, 3), (2, 7)):
+        assert torch.equal(cache[slot].cpu(), pool[key]), (packed, slot)
+    eng.close()
+
+
 @pytest.mark.parametrize('kind', ['kernel', 'dma'])
 def test_h2d_copy_waits_for_last_use(device, kind):
     """A fetch into a slot must not overwrite it before the compute that reads it ends."""
