@@ -174,6 +174,48 @@ def test_runtime_packed_pool_matches_raw(device, tokens):
             assert torch.equal(u, v), i
 
 
+def test_runtime_packed_reset_and_serial(device):
+    """A reset in the middle of a run (the engine reset in place, not rebuilt) and the serial
+    mode, with packed fetches: outputs, eviction state and copy counts equal the raw, overlapped
+    run's, call by call."""
+    from dataclasses import replace
+
+    from ferry_amd import expert_ops as ops
+    from ferry_amd import workloads
+    from ferry_amd.model import QWEN3_30B_A3B
+    from ferry_amd.quota import Topology
+    from ferry_amd.runtime import OffloadRuntime
+    spec = replace(QWEN3_30B_A3B, moe_layers=(0, 1))
+    pool = workloads.make_pool(spec, spec.layers, seed=5)
+    bias = torch.from_numpy(workloads.zipf_log_bias(spec.experts, 1.1, np.random.default_rng(1)))
+    runs = []
+    for pack, overlap in ((True, True), (True, False), (False, True)):
+        rt = OffloadRuntime(spec, pool, [80], 'ferry', Topology.uniform(1, spec.experts), pack=pack,
+                            overlap=overlap)
+        streams = [id(rt.h2d)]
+        g = torch.Generator(device=device)
+        g.manual_seed(9)
+        outs, copies = [], []
+        for call in range(8):
+            if call == 4:
+                rt.reset()
+                streams.append(id(rt.h2d))
+                assert rt.h2d.copies == 0
+            x = torch.randn((16, spec.hidden), generator=g, device=device).to(torch.bfloat16)
+            z = torch.randn((16, spec.experts), generator=g, device=device) + bias.to(device)
+            w, sel = ops.router_topk(z.to(torch.bfloat16), spec.topk)
+            outs.append(rt.execute(call % 2, x, sel, w, None).cpu())
+            copies.append(rt.h2d.copies)
+        assert streams[0] == streams[1]   # the same engine object after the reset
+        runs.append((outs, rt.controller.slots[0].copy(), copies))
+        rt.close()
+    base_outs, base_slots, base_copies = runs[-1]
+    for outs, slots, copies in runs[:-1]:
+        assert copies == base_copies and np.array_equal(slots, base_slots)
+        for i, (u, v) in enumerate(zip(outs, base_outs)):
+            assert torch.equal(u, v), i
+
+
 def test_runtime_serial_mode(device):
     from ferry_amd.model import ModelSpec
     spec = ModelSpec('qwen3_moe', (0, 1), 16, 4, 256, 128)
