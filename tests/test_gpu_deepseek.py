@@ -64,8 +64,10 @@ def test_combine_add_is_bf16_addition(device):
     assert torch.equal(plain.cpu(), routed)
 
 
-def test_deepseek_layer_t256_all_resident(device):
-    """One DeepSeek-V2-Lite MoE layer, 256 tokens, every expert resident (64 slots)."""
+@pytest.mark.parametrize('pack', [False, True])
+def test_deepseek_layer_t256_all_resident(device, pack):
+    """One DeepSeek-V2-Lite MoE layer, 256 tokens, every expert resident (64 slots); with packed
+    fetches (17.3 MB rows of 2816-wide experts) the output equals the raw fetches' bit for bit."""
     from ferry_amd import expert_ops as ops
     from ferry_amd import workloads
     from ferry_amd.model import deepseek_moe
@@ -78,10 +80,17 @@ def test_deepseek_layer_t256_all_resident(device):
     gate = workloads.router_gates(spec, 1, seed=w.seed, device=device)[0]
     srow = workloads.shared_rows(1, H, w.shared_intermediate, seed=w.seed, device=device)[0]
     x = workloads.hidden_states(T, H, seed=w.seed + 7, device=device)
-    rt = OffloadRuntime(spec, pool, [w.cache_slots], 'ferry', Topology.uniform(1, E))
+    rt = OffloadRuntime(spec, pool, [w.cache_slots], 'ferry', Topology.uniform(1, E), pack=pack)
     shared = ops.SharedExpert(srow, H, w.shared_intermediate)
     out, logits = deepseek_moe(rt, 0, x, gate, k, shared=shared)
     torch.cuda.synchronize()
+    if pack:
+        assert rt.packed.ratio > 1.3
+        raw_rt = OffloadRuntime(spec, pool, [w.cache_slots], 'ferry', Topology.uniform(1, E))
+        raw_out, _ = deepseek_moe(raw_rt, 0, x, gate, k, shared=shared)
+        torch.cuda.synchronize()
+        assert torch.equal(out.cpu(), raw_out.cpu())
+        raw_rt.close()
     # routing: the oracle on the identical fp32 logits (the GEMM is not part of the parity claim)
     lg = logits.cpu()
     w_ref, sel_ref, _ = deepseek_router(lg, k)
