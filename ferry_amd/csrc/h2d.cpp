@@ -124,6 +124,8 @@ struct ferry_h2d {
   std::vector<std::pair<hipStream_t, std::shared_ptr<Event>>> kernel_last;
   std::vector<int64_t> batch_of;      // per slot: last batch of rows that wrote it (one call)
   int64_t batch = 0;
+  std::vector<int64_t> call_of;       // per slot: last packed DMA call that wrote it
+  int64_t call = 0;
   // packed pool (ferry_h2d_use_packed): DMA copies move packed rows into device staging
   // buffers, and an unpack kernel writes the slots
   const ferry_packed_pool* packed = nullptr;
@@ -247,6 +249,7 @@ extern "C" int ferry_h2d_create(void* cache, int64_t cache_rows, const void* poo
   h->kernel_stream = h->stream[0];
   h->copy_seq.assign((size_t)cache_rows, -1);
   h->batch_of.assign((size_t)cache_rows, 0);
+  h->call_of.assign((size_t)cache_rows, 0);
   h->used.assign((size_t)cache_rows, nullptr);
   *out = h.release();
   return 0;
@@ -297,8 +300,16 @@ static int sub_batch_level(int64_t remaining) {
 // staging buffers (rows that stayed raw go straight into their slots); the unpack stream waits
 // for both lanes' copies of the sub-batch and runs one unpack launch that writes the slots, and
 // every slot of the sub-batch is ready at the event after it.  The lanes never wait for the
-// unpack stream (except to reuse a staging buffer that an unpack has yet to read), so each
-// sub-batch's unpack runs while the lanes copy the next.
+// unpack stream (except to reuse a staging buffer that an unpack has yet to read, or when a
+// sub-batch writes a slot that an earlier sub-batch of the call wrote), so each sub-batch's
+// unpack runs while the lanes copy the next.
+//
+// A slot named twice in a call gets its rows in two sub-batches, and the later row must win,
+// as with copies in stream order.  The two writes can be an unpack (unpack stream) and a raw
+// row's lane copies (cut into per-lane byte ranges that differ between sub-batches), so before
+// copying a sub-batch that rewrites a slot the lanes wait for the end of the previous
+// sub-batch: its unpack ran after its own lane copies and, in stream order, after every earlier
+// unpack of the call.
 static int fetch_packed(ferry_h2d* h, const int64_t* slots, const int64_t* keys, int64_t n) {
   struct Seg {
     const char* src;
@@ -310,6 +321,8 @@ static int fetch_packed(ferry_h2d* h, const int64_t* slots, const int64_t* keys,
   const int64_t per_batch = h->ring_rows < ferry::kUnpackRows ? h->ring_rows : ferry::kUnpackRows;
   int64_t remaining = 0;   // bytes of the call not yet in a sub-batch
   for (int64_t i = 0; i < n; ++i) remaining += pp->size[(size_t)keys[i]];
+  ++h->call;
+  std::shared_ptr<Event> prev;   // the end of the previous sub-batch of this call
   int64_t i0 = 0;
   while (i0 < n) {
     std::vector<Seg> segs;
@@ -317,21 +330,27 @@ static int fetch_packed(ferry_h2d* h, const int64_t* slots, const int64_t* keys,
     ul.n_rows = 0;
     std::vector<int64_t> entries;
     int64_t i1 = i0, total = 0;
+    bool rewrites = false;   // writes a slot that an earlier sub-batch of the call wrote
     const int level = sub_batch_level(remaining);
     ++h->batch;   // a slot named twice starts a new sub-batch, so that the later row wins
     for (; i1 < n && (i1 == i0 || sub_batch_level(remaining - total) == level); ++i1) {
       const int64_t key = keys[i1];
-      if (h->batch_of[(size_t)slots[i1]] == h->batch) break;
+      const size_t sl = (size_t)slots[i1];
+      if (h->batch_of[sl] == h->batch) break;
       char* slot_ptr = h->cache + slots[i1] * rb;
       const char* src = (const char*)pp->data + pp->off[(size_t)key];
       if (pp->raw[(size_t)key]) {
-        h->batch_of[(size_t)slots[i1]] = h->batch;
+        rewrites = rewrites || h->call_of[sl] == h->call;
+        h->call_of[sl] = h->call;
+        h->batch_of[sl] = h->batch;
         segs.push_back({src, slot_ptr, rb});
         total += rb;
         continue;
       }
       if (ul.n_rows == per_batch) break;
-      h->batch_of[(size_t)slots[i1]] = h->batch;
+      rewrites = rewrites || h->call_of[sl] == h->call;
+      h->call_of[sl] = h->call;
+      h->batch_of[sl] = h->batch;
       const int64_t k = h->ring_next;
       h->ring_next = (k + 1) % h->ring_rows;
       char* st = (char*)h->ring + k * h->entry_bytes;
@@ -361,6 +380,8 @@ static int fetch_packed(ferry_h2d* h, const int64_t* slots, const int64_t* keys,
       (void)hipGetLastError();
       for (int l = 0; l < kLanes; ++l) H2D_HIP(hipStreamWaitEvent(h->stream[l], ev->e, 0));
     }
+    if (rewrites && prev)
+      for (int l = 0; l < kLanes; ++l) H2D_HIP(hipStreamWaitEvent(h->stream[l], prev->e, 0));
     // each lane's byte range as copies; issued round-robin over the lanes, so that every lane
     // starts as early as the host can queue it
     std::vector<Seg> lane_segs[kLanes];
@@ -415,6 +436,7 @@ static int fetch_packed(ferry_h2d* h, const int64_t* slots, const int64_t* keys,
       h->copy_seq[(size_t)slots[i]] = h->seq++;
     }
     for (int64_t k : entries) h->ring_ev[(size_t)k] = ev;
+    prev = ev;
     h->copies += i1 - i0;
     remaining -= total;
     i0 = i1;
@@ -668,10 +690,23 @@ extern "C" int ferry_h2d_reset(ferry_h2d* h) {
     return 2;
   }
   if (ferry_h2d_synchronize(h) != 0) return 3;
+  // reads of the slots that callers' streams may still have in flight: the fetches after the
+  // reset no longer know of them, so they end first
+  std::vector<const Event*> reads;
+  for (const auto& ev : h->used)
+    if (ev && (reads.empty() || reads.back() != ev.get())) reads.push_back(ev.get());
+  if (h->marker) reads.push_back(h->marker.get());
+  for (size_t i = 0; i < reads.size(); ++i) {
+    bool seen = false;
+    for (size_t j = 0; j < i && !seen; ++j) seen = reads[j] == reads[i];
+    if (!seen) H2D_HIP(hipEventSynchronize(reads[i]->e));
+  }
   const size_t rows = (size_t)h->cache_rows;
   for (int l = 0; l < kLanes; ++l) h->copy_done[l].assign(rows, nullptr);
   h->copy_seq.assign(rows, -1);
   h->batch_of.assign(rows, 0);
+  h->call_of.assign(rows, 0);
+  h->call = 0;
   h->used.assign(rows, nullptr);
   h->ring_ev.assign(h->ring_ev.size(), nullptr);
   h->ring_next = 0;
@@ -879,6 +914,7 @@ extern "C" int ferry_h2d_create_packed(void* cache, int64_t cache_rows,
   h->kernel_stream = h->stream[0];
   h->copy_seq.assign((size_t)cache_rows, -1);
   h->batch_of.assign((size_t)cache_rows, 0);
+  h->call_of.assign((size_t)cache_rows, 0);
   h->used.assign((size_t)cache_rows, nullptr);
   ferry_h2d* raw = h.release();
   const int rc = ferry_h2d_use_packed_any(raw, pp, ring_rows);

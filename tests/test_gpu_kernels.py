@@ -729,6 +729,49 @@ def test_h2d_packed_sub_batches_and_ring_reuse(device, defer):
     packed.close()
 
 
+@pytest.mark.parametrize('defer', [False, True])
+def test_h2d_packed_slot_named_twice_raw_and_packed(device, defer):
+    """A slot named twice in one packed DMA call, its rows in different sub-batches: raw then
+    packed, packed then raw, raw then raw, and within one sub-batch -- the later row wins in
+    every case (a raw row is copied by both lanes in byte ranges that differ between
+    sub-batches, a packed one by the unpack stream)."""
+    from ferry_amd.h2d import H2DEngine, PackedPool
+    rows, cap, width = 16, 14, (1 << 21) + 8192
+    g = torch.Generator().manual_seed(9)
+    pool = (torch.randn((rows, width), generator=g) * 0.02).to(torch.bfloat16)
+    for r in (6, 9, 13):     # random bits: stored raw
+        pool[r] = torch.randint(-32768, 32767, (width,), generator=g,
+                                dtype=torch.int16).view(torch.bfloat16)
+    packed = PackedPool(pool, threads=8)
+    assert packed.packed_rows == rows - 3
+    cache = torch.zeros((cap, width), dtype=torch.bfloat16, device=device)
+    eng = H2DEngine.from_packed(cache, packed, ring_rows=3)
+    eng.defer_last = defer
+    bits = lambda t: t.view(torch.int16)   # noqa: E731
+    calls = [
+        # raw then packed (slot 3), packed then raw (slot 5), raw then raw (slot 8)
+        ([3, 0, 1, 2, 5, 4, 8, 7, 3, 10, 5, 11, 8],
+         [6, 0, 1, 2, 3, 4, 9, 5, 7, 8, 13, 10, 6]),
+        # within the first sub-batch: packed then raw, then more rows after
+        ([2, 2, 6, 7, 9, 12], [1, 9, 0, 2, 3, 4]),
+        # raw row last, after the slot's packed row several sub-batches earlier
+        ([4, 0, 1, 5, 6, 7, 10, 11, 4], [5, 0, 1, 2, 3, 7, 8, 10, 13]),
+    ]
+    want = torch.zeros((cap, width), dtype=torch.bfloat16)
+    for slots, keys in calls:
+        for sl, k in zip(slots, keys):
+            want[sl] = pool[k]
+        eng.fetch(slots, keys)
+        consumer = torch.cuda.Stream()
+        eng.wait_stream(sorted(set(slots)), consumer)
+        with torch.cuda.stream(consumer):
+            snap = cache.clone()
+        torch.cuda.synchronize()
+        assert torch.equal(bits(snap.cpu()), bits(want)), slots
+    eng.close()
+    packed.close()
+
+
 @pytest.mark.parametrize('kind', ['dma', 'kernel'])
 @pytest.mark.parametrize('width', [2 * 8192 + 96, 32, 8192])
 def test_h2d_packed_pool_ragged_widths(device, width, kind):
