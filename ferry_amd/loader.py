@@ -152,7 +152,7 @@ def load(model_path, spec=None, device='cuda', pinned=True):
         model = AutoModelForCausalLM.from_config(config, dtype=torch.bfloat16)
     for index in spec.moe_layers:
         model.model.layers[index].mlp.experts = None
-    device = torch.device(device)
+    device = resolve_device(device)
     files = checkpoint_files(model_path)
     by_file = {}
     for name, path in files.items():
@@ -167,9 +167,28 @@ def load(model_path, spec=None, device='cuda', pinned=True):
     missing = [n for n, p in model.named_parameters() if p.device != device]
     if missing:
         raise ValueError(f'checkpoint lacks {len(missing)} tensors (first: {missing[0]})')
+    place_buffers(model, device)
+    model.eval()
+    return model, load_pool(model_path, spec, pinned=pinned)
+
+
+def resolve_device(device):
+    """``device`` with its index filled in ('cuda' -> 'cuda:<current>'), so that it compares
+    equal to the device of the tensors placed on it."""
+    return torch.empty(0, device=device).device
+
+
+def place_buffers(model, device):
+    """Buffers computed while the model was built on the host, moved to ``device``.  Rotary
+    embeddings are recomputed there with their own init function, as the reference does
+    (model.py:111-115), so that the frequencies are the device's arithmetic and
+    ``original_inv_freq`` names the same buffer."""
+    for module in model.modules():
+        if hasattr(module, 'rope_init_fn') and hasattr(module, 'inv_freq'):
+            inv, module.attention_scaling = module.rope_init_fn(module.config, device=device)
+            module.register_buffer('inv_freq', inv, persistent=False)
+            module.original_inv_freq = inv
     for module in model.modules():
         for key, buf in list(module._buffers.items()):
             if buf is not None and buf.device != device:
                 module._buffers[key] = buf.to(device)
-    model.eval()
-    return model, load_pool(model_path, spec, pinned=pinned)

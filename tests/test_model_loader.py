@@ -146,3 +146,48 @@ def test_load_rejects_incomplete_or_mismatched(tmp_path):
     save_file({'model.layers.1.mlp.experts.0.up_proj.weight': t}, str(tmp_path / 'model.safetensors'))
     with pytest.raises(ValueError, match='not a routed expert'):
         load_pool(tmp_path, spec, pinned=False)   # layer 1 is a dense MLP layer here
+
+
+def test_place_buffers_rebuilds_rotary_with_its_init_function():
+    """transformers 4.57 rotary modules carry ``rope_init_fn``: place_buffers recomputes the
+    frequencies on the target device with it and points ``original_inv_freq`` at the new
+    buffer (reference model.py:111-115); other buffers are moved; 5.x modules (no
+    ``rope_init_fn``) keep their values."""
+    from ferry_amd.loader import place_buffers, resolve_device
+    calls = []
+
+    class Rotary457(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.config = 'cfg'
+            self.register_buffer('inv_freq', torch.zeros(4), persistent=False)
+            self.original_inv_freq = self.inv_freq
+
+        def rope_init_fn(self, config, device=None):
+            calls.append((config, device))
+            return torch.arange(4, dtype=torch.float32, device=device) + 1, 0.5
+
+    model = torch.nn.Module()
+    model.rot = Rotary457()
+    model.other = torch.nn.Module()
+    model.other.register_buffer('scale', torch.ones(3, dtype=torch.float64))
+    dev = resolve_device('cpu')
+    place_buffers(model, dev)
+    assert calls == [('cfg', dev)]
+    assert torch.equal(model.rot.inv_freq, torch.tensor([1.0, 2.0, 3.0, 4.0]))
+    assert model.rot.original_inv_freq is model.rot.inv_freq
+    assert model.rot.attention_scaling == 0.5
+    assert 'inv_freq' in model.rot._buffers and 'inv_freq' in model.rot._non_persistent_buffers_set
+    assert torch.equal(model.other.scale, torch.ones(3, dtype=torch.float64))
+    # a 5.x model built on the host: its rotary buffers (no rope_init_fn) are left as built
+    cfg = tiny_qwen3_config()
+    m5 = tiny_model(cfg, seed=1)
+    before = {n: b.clone() for n, b in m5.named_buffers()}
+    place_buffers(m5, dev)
+    assert all(torch.equal(before[n], b) for n, b in m5.named_buffers())
+
+
+def test_resolve_device_fills_the_index():
+    from ferry_amd.loader import resolve_device
+    assert resolve_device('cpu') == torch.device('cpu')
+    assert resolve_device(torch.device('cpu')).type == 'cpu'
