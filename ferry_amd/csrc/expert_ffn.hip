@@ -1013,7 +1013,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void f
 // atomic words.  Workgroups are dispatched in index order, so every producer a down
 // workgroup waits for has been dispatched before it: the wait ends.  It is still bounded
 // (kSyncSpinLimit sleeps, about a second); a down workgroup that runs out counts a timeout and
-// skips its expert rather than read unfinished rows.
+// skips its expert rather than read unfinished rows.  The count lives in device memory
+// (g_sync_timeouts); the history kernel copies it into the caller's mapped host buffer at the
+// start of every layer call, so that the runtime raises on the next call's routing readback
+// instead of returning unwritten rows as output.
 //
 // Arrival flags: one 32-bit word per up workgroup, holding the epoch (a number unique to the
 // call) once that workgroup's rows are stored.  A down workgroup's first wavefront checks all
@@ -1034,6 +1037,7 @@ struct FusedSync {
   uint32_t epoch;
   int32_t up_wgs;    // up workgroups per expert (I / 16)
   int32_t down_wgs;  // down workgroups per expert (H / 64)
+  int32_t spin_limit;  // polls before a down workgroup gives up (0: gives up at once)
 };
 
 __device__ __forceinline__ void sync_arrive(const FusedSync& fs, int li, int bx) {
@@ -1046,16 +1050,15 @@ __device__ __forceinline__ void sync_arrive(const FusedSync& fs, int li, int bx)
 __device__ __forceinline__ bool sync_wait(const FusedSync& fs, int li) {
   const int lane = threadIdx.x & 63;
   const uint32_t* f = fs.flags + li * kMaxUpWgs;
-  int spins = 0;
-  for (;;) {
+  for (int spins = 0;; ++spins) {
+    if (spins >= fs.spin_limit) {
+      if (lane == 0) atomicAdd(fs.timeouts, 1);
+      return false;
+    }
     bool mine = true;
     for (int j = lane; j < fs.up_wgs; j += 64)
       mine &= __hip_atomic_load(f + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == fs.epoch;
     if (__all(mine)) return true;
-    if (++spins > kSyncSpinLimit) {
-      if (lane == 0) atomicAdd(fs.timeouts, 1);
-      return false;
-    }
     __builtin_amdgcn_s_sleep(8);
   }
 }
@@ -1480,6 +1483,7 @@ std::mutex g_sync_mu;
 uint32_t* g_sync_dev[kMaxDevices];
 int32_t* g_timeouts_dev[kMaxDevices];
 std::atomic<uint32_t> g_epoch{0};
+std::atomic<int32_t> g_spin_limit{kSyncSpinLimit};
 
 int sync_addresses(uint32_t** sync, int32_t** timeouts) {
   int dev = -1;
@@ -1500,6 +1504,14 @@ int sync_addresses(uint32_t** sync, int32_t** timeouts) {
 }
 
 }  // namespace
+
+// device address of the fused decode kernel's timeout counter on the current device (for the
+// history kernel's copy of it)
+int ffn_timeouts_address(int32_t** timeouts) {
+  uint32_t* sync = nullptr;
+  return sync_addresses(&sync, timeouts);
+}
+
 }  // namespace ferry
 
 using namespace ferry;
@@ -1595,6 +1607,7 @@ extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t h
       fs.flags = sync + (int64_t)(epoch % kSyncSets) * kListMax * kMaxUpWgs;
       fs.up_wgs = (int32_t)(inter / 16);
       fs.down_wgs = (int32_t)(hidden / 64);
+      fs.spin_limit = g_spin_limit.load();
       launch("ffn_skinny_fused", ffn_skinny_fused,
              dim3((unsigned)((fs.up_wgs + fs.down_wgs) * cnt)), dim3(256), 0, s, args, fs);
       FERRY_LAUNCHED("ffn_skinny_fused");
@@ -1651,5 +1664,15 @@ extern "C" int ferry_expert_ffn_sync_timeouts(int64_t* count) {
   int32_t v = 0;
   FERRY_HIP(hipMemcpy(&v, timeouts, sizeof(v), hipMemcpyDeviceToHost));
   *count = v;
+  return 0;
+}
+
+// How many times a fused decode launch's down workgroup polls its up workgroups' flags before
+// giving up (limit < 0: the default, about a second of polling; 0: it gives up without polling,
+// so that a caller can check how a timeout is reported).  Applies to launches made after it.
+extern "C" int ferry_expert_ffn_set_sync_spin_limit(int64_t limit) {
+  clear_error();
+  FERRY_CHECK_ARG(limit < ((int64_t)1 << 30), "spin limit must be below 2^30");
+  g_spin_limit.store(limit < 0 ? kSyncSpinLimit : (int32_t)limit);
   return 0;
 }

@@ -12,6 +12,7 @@
 #include "common.h"
 
 namespace ferry {
+int ffn_timeouts_address(int32_t** timeouts);
 namespace {
 
 constexpr int kMaxE = 512;
@@ -23,7 +24,8 @@ constexpr int kIdsPerBlock = kThreads * 16;
 __global__ __launch_bounds__(kThreads) void history_kernel(
     const int64_t* __restrict__ selected, int64_t tokens, int k, int E, int W, int64_t layer,
     int32_t* __restrict__ ring, int32_t* __restrict__ counts, int32_t* __restrict__ meta,
-    float* __restrict__ scores_out, uint8_t* __restrict__ ids_out) {
+    float* __restrict__ scores_out, uint8_t* __restrict__ ids_out,
+    const int32_t* __restrict__ timeouts_src, int32_t* __restrict__ timeouts_out) {
   if (blockIdx.x > 0) {
     const int64_t n = tokens * k;
     const int64_t i0 = (int64_t)(blockIdx.x - 1) * kIdsPerBlock;
@@ -74,6 +76,8 @@ __global__ __launch_bounds__(kThreads) void history_kernel(
   if (threadIdx.x == 0) {
     meta[layer * 2 + 0] = new_count;
     meta[layer * 2 + 1] = replace ? 0 : (head + tail) % W;
+    if (timeouts_out)
+      *timeouts_out = __hip_atomic_load(timeouts_src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -85,7 +89,8 @@ using namespace ferry;
 extern "C" int ferry_history_update(const int64_t* selected, int64_t tokens, int64_t topk,
                                     int64_t experts, int64_t window, int64_t layer,
                                     int32_t* ring, int32_t* counts, int32_t* meta,
-                                    float* scores_out, uint8_t* ids_out, void* stream) {
+                                    float* scores_out, uint8_t* ids_out,
+                                    int32_t* ffn_timeouts_out, void* stream) {
   clear_error();
   FERRY_CHECK_ARG(tokens >= 0 && topk >= 1 && layer >= 0, "bad sizes");
   FERRY_CHECK_ARG(experts >= 1 && experts <= kMaxE, "experts must be in [1, %d]", kMaxE);
@@ -96,9 +101,14 @@ extern "C" int ferry_history_update(const int64_t* selected, int64_t tokens, int
   const int64_t nids = ids_out ? tokens * topk : 0;
   const int64_t grid = 1 + ceil_div(nids, kIdsPerBlock);
   FERRY_CHECK_ARG(grid < (1 << 30), "too many tokens");
+  int32_t* timeouts_src = nullptr;
+  if (ffn_timeouts_out) {
+    const int rc = ffn_timeouts_address(&timeouts_src);
+    if (rc != 0) return rc;
+  }
   launch("history_kernel", history_kernel, dim3((unsigned)grid), dim3(kThreads), 0, (hipStream_t)stream,
                      selected, tokens, (int)topk, (int)experts, (int)window, layer, ring, counts,
-                     meta, scores_out, ids_out);
+                     meta, scores_out, ids_out, timeouts_src, ffn_timeouts_out);
   FERRY_LAUNCHED("history_kernel");
   return 0;
 }

@@ -204,6 +204,14 @@ def ffn_sync_timeouts():
     return int(n.value)
 
 
+def ffn_set_sync_spin_limit(limit):
+    """How often a one-launch decode FFN's down phase polls for its up phase before it gives up
+    (launches after the call): None or < 0 restores the default; 0 makes every wait give up at
+    once, to check how a timeout is reported (no reference counterpart)."""
+    check(lib().ferry_expert_ffn_set_sync_spin_limit(-1 if limit is None else int(limit)),
+          'ffn_set_sync_spin_limit')
+
+
 def hbm_read(buf, sink=None):
     """Read every byte of ``buf`` (a contiguous CUDA tensor, nbytes a multiple of 16) once at the
     HBM read rate, on the current stream: the measured read ceiling for the memory-bound
@@ -285,19 +293,25 @@ class SharedExpert:
                           out_mode=1, experts=1, counts=[T])
 
 
-def history_update(selected, experts, window, layer, ring, counts, meta, scores, ids_out=None):
+def history_update(selected, experts, window, layer, ring, counts, meta, scores, ids_out=None,
+                   timeouts_out=None):
     """Device GateHistory update of ``layer`` (ferry/metadata.py:15-38, frequency rows).
 
-    ``scores`` (fp32 [E]) and ``ids_out`` (uint8 [T*k]) are CUDA tensors or raw device
-    addresses (ints), e.g. of a mapped host buffer that the kernel writes directly."""
+    ``scores`` (fp32 [E]), ``ids_out`` (uint8 [T*k]) and ``timeouts_out`` (int32 [1]: the
+    device's count of one-launch decode FFN waits that gave up, as ``ffn_sync_timeouts``) are
+    CUDA tensors or raw device addresses (ints), e.g. of a mapped host buffer that the kernel
+    writes directly."""
     T, k = selected.shape
     sp = scores if isinstance(scores, int) else _dev(scores, 'scores', torch.float32)
     ip = (ids_out if isinstance(ids_out, int) or ids_out is None
           else _dev(ids_out, 'ids_out', torch.uint8))
+    tp = (timeouts_out if isinstance(timeouts_out, int) or timeouts_out is None
+          else _dev(timeouts_out, 'timeouts_out', torch.int32))
     check(lib().ferry_history_update(
         _dev(selected, 'selected', torch.int64), T, k, experts, window, layer,
         _dev(ring, 'ring', torch.int32), _dev(counts, 'counts', torch.int32),
-        _dev(meta, 'meta', torch.int32), sp, ip, current_stream(selected.device)), 'history_update')
+        _dev(meta, 'meta', torch.int32), sp, ip, tp, current_stream(selected.device)),
+        'history_update')
 
 
 # ------------------------------------------------------------------------------------------

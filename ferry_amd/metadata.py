@@ -51,10 +51,11 @@ class DeviceGateHistory:
         self.counts = torch.zeros((layers, experts), dtype=torch.int32, device=device)
         self.meta = torch.zeros((layers, 2), dtype=torch.int32, device=device)
 
-    def update(self, layer, selected, scores_out, ids_out=None):
-        """Append the last min(T, W) tokens of ``selected`` and write the layer's scores."""
+    def update(self, layer, selected, scores_out, ids_out=None, timeouts_out=None):
+        """Append the last min(T, W) tokens of ``selected`` and write the layer's scores (and,
+        where given, the uint8 IDs and the device's decode-FFN timeout count)."""
         ops.history_update(selected, self.experts, self.window, layer, self.ring, self.counts,
-                           self.meta, scores_out, ids_out)
+                           self.meta, scores_out, ids_out, timeouts_out)
 
 
 def frequency_rows(expert_ids, experts, window, world=1):

@@ -20,6 +20,11 @@ Per MoE layer call (world = 1):
      cross-queue wait, but no overlap either (the copy kernel's host reads slow the HBM-bound
      kernels that run beside it, so nothing runs beside it);
   5. the combine kernel sums each token's k expert rows in fp32 (ascending expert ID).
+
+The one-launch decode FFN bounds its cross-workgroup wait; a wait that gives up leaves rows
+unwritten and counts a timeout on the device.  The history kernel copies that count next to the
+routing IDs, so the next call raises RuntimeError when it grew (an earlier call's output is then
+invalid), and so do ``reset`` and ``close``.
 """
 import time
 
@@ -83,8 +88,7 @@ class OffloadRuntime:
         self.controller = Controller(spec, capacities, policy, topology, balance_tol_bps, salt)
         self.gather = RouteGather(spec.topk, spec.experts, history_window, eviction_score)
         self.transport = Transport(self.ops, spec.topk, spec.experts)
-        self._stage_dev = None   # device staging (probability mode): [scores fp32 E | IDs uint8 T*k]
-        self._stage_host = None  # mapped host staging buffer of the same layout
+        self._stage_host = None  # mapped host staging: [scores f32 E | IDs u8 T*k | pad | timeouts i32]
         self._bufs = {}
         self.h2d = None
         self.reset()
@@ -92,11 +96,13 @@ class OffloadRuntime:
     # -- state -------------------------------------------------------------------------------
 
     def reset(self):
-        """Empty expert cache and routing history (start of every measured run)."""
+        """Empty expert cache and routing history (start of every measured run).  Raises
+        RuntimeError (after the reset) if a decode FFN wait gave up since the last check."""
         self._flush_used()
         if self.h2d is not None:
             self.h2d.synchronize()
         torch.cuda.synchronize(self.device)
+        late = self._timeouts_since_check()
         self.controller.reset()
         spec = self.spec
         self.history = GateHistory(spec.layers, spec.experts, self.window)
@@ -126,6 +132,27 @@ class OffloadRuntime:
         # wait for the routing IDs and the fetch enqueue is on the critical path of a step
         self.host_ns = dict(enqueue_before_wait=0, wait_for_ids=0, plan=0, fetch_enqueue=0,
                             enqueue_after_fetch=0)
+        if late:
+            raise RuntimeError(self._timeout_message(late))
+
+    # -- decode FFN timeouts -----------------------------------------------------------------
+
+    def _timeouts_since_check(self):
+        """Device-wide decode FFN timeouts counted since the last check (reads the device)."""
+        now = self.ops.ffn_sync_timeouts()
+        seen = getattr(self, '_timeouts_seen', now)
+        self._timeouts_seen = now
+        return now - seen
+
+    @staticmethod
+    def _timeout_message(n):
+        return (f'{n} wait(s) of the one-launch decode FFN gave up on this device: the rows of '
+                f'those experts were not written, so the output of an earlier layer call is '
+                f'invalid')
+
+    def _status_offset(self, tokens):
+        """Byte offset of the timeout word in the staging buffer of a ``tokens``-token call."""
+        return 4 * self.spec.experts + (tokens * self.spec.topk + 3) // 4 * 4
 
     def _buffers(self, tokens):
         b = self._bufs.get(tokens)
@@ -137,12 +164,11 @@ class OffloadRuntime:
                                       device=self.device),
                      layout=None)
             self._bufs[tokens] = b
-        n = 4 * self.spec.experts + tokens * self.spec.topk
+        n = self._status_offset(tokens) + 4
         if self._stage_host is None or self._stage_host.numel() < n:
-            # coherent mapped host memory: the history kernel writes the layer's scores and the
-            # uint8 IDs straight into it, so the host needs no separate D2H copy
+            # coherent mapped host memory: the history kernel writes the layer's scores, the
+            # uint8 IDs and the timeout count straight into it, so the host needs no D2H copy
             self._stage_host, self._stage_ptr = mapped_buffer(max(n, 4096))
-            self._stage_dev = torch.zeros(n, dtype=torch.uint8, device=self.device)
         return b
 
     # -- one layer call ------------------------------------------------------------------------
@@ -162,16 +188,14 @@ class OffloadRuntime:
         selected = selected.contiguous()
         weights = weights.to(torch.bfloat16).contiguous()
 
-        # 1. history; the kernel writes scores and IDs into the mapped host staging buffer
+        # 1. history; the kernel writes scores, IDs and the device's decode FFN timeout count
+        # into the mapped host staging buffer (with probability scores its scores go unused)
         frequency = self.gather.score == 'frequency'
         nbytes = 4 * E + T * k
         stage_host = self._stage_host[:nbytes]
-        if frequency:
-            self.device_history.update(layer, selected, self._stage_ptr, self._stage_ptr + 4 * E)
-        else:
-            ids_dev = self._stage_dev[4 * E:nbytes]
-            ids_dev.copy_(selected.reshape(-1).to(torch.uint8))
-            stage_host.copy_(self._stage_dev[:nbytes], non_blocking=True)
+        status = self._status_offset(T)
+        self.device_history.update(layer, selected, self._stage_ptr, self._stage_ptr + 4 * E,
+                                   self._stage_ptr + status)
         tail_host = None
         if not frequency:
             tail = min(T, self.window)
@@ -209,6 +233,10 @@ class OffloadRuntime:
         t_sync = time.perf_counter_ns()
         wait_ids()
         t_ready = time.perf_counter_ns()
+        count = int(self._stage_host[status:status + 4].view(torch.int32)[0])
+        if count != self._timeouts_seen:
+            late, self._timeouts_seen = count - self._timeouts_seen, count
+            raise RuntimeError(self._timeout_message(late))
         self._set_copy_mode(on_stream, stream)
         # with chunks or timing the copies are queued here; otherwise the planner's native call
         # queues them itself, right after planning
@@ -384,6 +412,12 @@ class OffloadRuntime:
                     calls=len(plan))
 
     def close(self):
+        """Drain the runtime's work; raises RuntimeError if a decode FFN wait gave up since the
+        last check."""
         self._flush_used()
         if self.h2d is not None:
             self.h2d.synchronize()
+        torch.cuda.synchronize(self.device)
+        late = self._timeouts_since_check()
+        if late:
+            raise RuntimeError(self._timeout_message(late))

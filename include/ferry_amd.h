@@ -131,7 +131,12 @@ enum { FERRY_MAX_EXPERTS = 512 };
  * ferry_expert_ffn_sync_timeouts (a diagnostic with no counterpart in the reference) returns
  * how many waits of such launches on the current device gave up: each wait is bounded (about a
  * second), and the count stays 0 when workgroups are dispatched in index order, as the
- * hardware does.  A wait that gave up leaves its rows of `out` unwritten. */
+ * hardware does.  A wait that gave up leaves its rows of `out` unwritten; ferry_history_update
+ * copies the count where a caller reads its routing IDs, so that the caller can fail.
+ * ferry_expert_ffn_set_sync_spin_limit (no counterpart in the reference) sets how often such a
+ * wait polls before it gives up, for launches made after the call: limit < 0 restores the
+ * default, 0 makes every wait give up at once (for tests of how a timeout is reported; every
+ * workgroup still exits normally). */
 int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t hidden, int64_t inter,
                      const void* x, int64_t rows_in, int64_t topk, const void* w_sorted,
                      const int64_t* starts, const int64_t* rows, const int64_t* cols,
@@ -140,6 +145,7 @@ int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t hidden, int6
                      int64_t min_rows_per_expert, void* act, void* out, int32_t out_mode,
                      int32_t phases, void* stream);
 int ferry_expert_ffn_sync_timeouts(int64_t* count);
+int ferry_expert_ffn_set_sync_spin_limit(int64_t limit);
 
 /*
  * Combine: out[t, :] = bf16( sum_{j<k} fp32(part[src(t, j), :]) ), j ascending (= ascending
@@ -185,10 +191,15 @@ int ferry_unpack_dispatch(const void* payload, int64_t packets, int64_t hidden_s
  * Update with the last min(T, W) tokens of selected[T, k]; then scores_out[E] =
  * float32(count_e / max(1, n)).  ids_out (nullable, needs E <= 255) receives selected as
  * uint8 [T*k] (the D2H payload of the host planner), with 0xFF for an ID outside [0, E).
+ * ffn_timeouts_out (nullable; no counterpart in the reference) receives the device's count of
+ * fused decode FFN workgroups that gave up waiting (ferry_expert_ffn_sync_timeouts), as the
+ * stream's earlier kernels left it: a caller that reads its routing IDs from host memory reads
+ * this word with them and can fail the layer call instead of using unwritten rows.
  */
 int ferry_history_update(const int64_t* selected, int64_t tokens, int64_t topk, int64_t experts,
                          int64_t window, int64_t layer, int32_t* ring, int32_t* counts,
-                         int32_t* meta, float* scores_out, uint8_t* ids_out, void* stream);
+                         int32_t* meta, float* scores_out, uint8_t* ids_out,
+                         int32_t* ffn_timeouts_out, void* stream);
 
 /*
  * Host planner at world = 1.  Replaces ferry/policy.py:130-194 (plan_layer with
@@ -240,9 +251,10 @@ int ferry_h2d_event_synchronize(ferry_h2d* h, void* event);
 /* expert_ops.cpp:130-133 */
 int ferry_h2d_synchronize(ferry_h2d* h);
 /* The state of a new engine on the same streams and buffers (runtime.py:51-62 builds a new
- * H2DEngine on reset): waits for all of the engine's work, then forgets every slot's copies and
+ * H2DEngine on reset): waits for all of the engine's work and for every read of a slot marked
+ * on a caller's stream (mark_used, mark_used_record), then forgets every slot's copies and
  * reads and zeroes the copy counter; DMA mode, the engine's own kernel stream, no deferred
- * unpack.  Keeping the streams keeps their hardware queues: a new engine's streams can land on
+ * unpack.  Reads that were never marked are the caller's to finish.  Keeping the streams keeps their hardware queues: a new engine's streams can land on
  * the queue of the caller's compute stream and serialise with it. */
 int ferry_h2d_reset(ferry_h2d* h);
 /* expert_ops.cpp:135 */

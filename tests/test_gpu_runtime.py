@@ -13,13 +13,18 @@ pytestmark = pytest.mark.gpu
 
 
 def _run(device, spec, cap, calls, tokens_of, seed, zipf, overlap=True, check_every=1,
-         gate_scale=8.0, copy='dma'):
+         gate_scale=8.0, copy='dma', score='frequency', pack=False):
+    """``calls`` layer calls through OffloadRuntime against the oracle: GateHistoryRef fed with
+    the reference's history rows (one-hot rows of the last min(T, W) tokens for the frequency
+    score; those tokens' fp32 router probabilities for the probability score, metadata.py:
+    55-59,77-78) and PlannerRef; the planner state bit-exact after every call, the output
+    within tolerance every ``check_every`` calls."""
     from ferry_amd import workloads
     from ferry_amd.quota import Topology
     from ferry_amd.runtime import OffloadRuntime
     pool = workloads.make_pool(spec, spec.layers, seed=seed)
     rt = OffloadRuntime(spec, pool, [cap], 'ferry', Topology.uniform(1, spec.experts),
-                        overlap=overlap, copy=copy)
+                        overlap=overlap, copy=copy, eviction_score=score, pack=pack)
     planner = PlannerRef(spec.layers, spec.experts, cap)
     hist = GateHistoryRef(spec.layers, spec.experts, 128)
     g = torch.Generator(device=device)
@@ -41,15 +46,21 @@ def _run(device, spec, cap, calls, tokens_of, seed, zipf, overlap=True, check_ev
         else:   # N(0, 1) logits as in the synthetic decode stream
             z = torch.randn((T, spec.experts), generator=g, device=device)
         logits = (z + biases[layer]).to(torch.bfloat16)
-        w_ref, sel_ref, _ = qwen3_router(logits.cpu(), spec.topk)
+        w_ref, sel_ref, probs_ref = qwen3_router(logits.cpu(), spec.topk)
         if len(np.unique(sel_ref.numpy())) > cap:
             skipped += 1
             continue   # the reference asserts on such a call (quota.py:63)
         from ferry_amd import expert_ops as ops
-        w, sel = ops.router_topk(logits, spec.topk)
-        out = rt.execute(layer, x, sel, w, None)
+        if score == 'probability':
+            w, sel, probs = ops.router_topk(logits, spec.topk, return_probs=True)
+            out = rt.execute(layer, x, sel, w, probs[-128:])
+            rows = probs_ref[-min(T, 128):].numpy()          # fp32 rows, as gathered
+        else:
+            w, sel = ops.router_topk(logits, spec.topk)
+            out = rt.execute(layer, x, sel, w, None)
+            rows = frequency_rows(sel_ref.numpy(), spec.experts, 128)
         # oracle: history -> plan -> trace
-        hist.update(layer, frequency_rows(sel_ref.numpy(), spec.experts, 128))
+        hist.update(layer, rows)
         fetches, _ = planner.plan(rt.event - 1, layer, sel_ref.numpy(), hist.scores(layer))
         assert np.array_equal(rt.controller.slots[0], planner.slots), f'call {call}: slots differ'
         assert np.array_equal(rt.controller.last, planner.last)
@@ -69,6 +80,22 @@ def test_runtime_small_evicting(device):
     rt, skipped = _run(device, spec, cap=20, calls=60,
                        tokens_of=lambda c: [3, 16, 40, 1, 130][c % 5], seed=5, zipf=1.0)
     assert rt.h2d.copies == int(rt.fetches_per_rank.sum()) > 20   # evictions happened
+
+
+@pytest.mark.parametrize('pack', [False, True])
+def test_runtime_probability_score_evicting(device, pack):
+    """eviction_score='probability' (the reference's Eq. 12 score, run_cell.py:187): the
+    history rows are the fp32 router probabilities of the last min(T, W) tokens; calls shorter
+    and longer than W, with evictions every few calls; the planner state (slots, owners, last
+    use, scores) bit-exact with the oracle after every call, outputs within tolerance."""
+    from ferry_amd.model import ModelSpec
+    spec = ModelSpec('qwen3_moe', (0, 1, 2), 32, 4, 256, 128)
+    # 32 slots hold any one call's experts but not three layers' (96 keys): evictions
+    rt, skipped = _run(device, spec, cap=32, calls=45,
+                       tokens_of=lambda c: [3, 16, 40, 1, 200][c % 5], seed=7, zipf=1.0,
+                       score='probability', pack=pack, check_every=3)
+    assert rt.gather.score == 'probability'
+    assert skipped == 0 and rt.h2d.copies == int(rt.fetches_per_rank.sum()) > 64
 
 
 def test_runtime_mixed_copy_modes(device):
@@ -268,6 +295,7 @@ def test_fused_decode_ffn_matches_two_launch_path(device, family):
     g = torch.Generator(device=device)
     g.manual_seed(3)
     act = torch.empty((64 * k, I), dtype=torch.bfloat16, device=device)
+    timeouts0 = ops.ffn_sync_timeouts()
     for T in (16, 1, 64 // 8, 16, 3):
         sel = torch.stack([torch.from_numpy(np.random.default_rng(T + i).choice(experts, k, replace=False))
                            for i in range(T)]).to(device)
@@ -285,4 +313,60 @@ def test_fused_decode_ffn_matches_two_launch_path(device, family):
         ops.expert_ffn(*args, act[:T * k], two, experts=E, counts=counts, phases=ops.PHASE_DOWN)
         torch.cuda.synchronize()
         assert torch.equal(fused, two), T
-    assert ops.ffn_sync_timeouts() == 0
+    assert ops.ffn_sync_timeouts() == timeouts0
+
+
+def test_runtime_raises_after_decode_ffn_timeout(device):
+    """A one-launch decode FFN whose down phase gives up -- forced from the host with a spin
+    limit of 0, so that every workgroup still exits normally -- leaves its experts' rows
+    unwritten.  The runtime must not pass that off as a layer output: the next call raises at
+    its routing readback, as do reset() and close(); after the error the runtime works again
+    and matches the oracle."""
+    from ferry_amd import expert_ops as ops
+    from ferry_amd import workloads
+    from ferry_amd.model import ModelSpec
+    from ferry_amd.quota import Topology
+    from ferry_amd.runtime import OffloadRuntime
+    spec = ModelSpec('qwen3_moe', (0, 1), 32, 4, 256, 128)
+    pool = workloads.make_pool(spec, spec.layers, seed=12)
+    rt = OffloadRuntime(spec, pool, [64], 'ferry', Topology.uniform(1, spec.experts))
+    g = torch.Generator(device=device)
+    g.manual_seed(2)
+    T = 8
+    x = torch.randn((T, spec.hidden), generator=g, device=device).to(torch.bfloat16)
+    logits = torch.randn((T, spec.experts), generator=g, device=device).to(torch.bfloat16)
+    w, sel = ops.router_topk(logits, spec.topk)
+    w_ref, sel_ref, _ = qwen3_router(logits.cpu(), spec.topk)
+
+    def check(out, layer):
+        torch.cuda.synchronize()
+        ref = moe_layer_ref(lambda e: pool[layer * spec.experts + e], x.cpu(), sel_ref, w_ref,
+                            spec.experts, spec.hidden, spec.intermediate)
+        torch.testing.assert_close(out.cpu().float(), ref.float(), rtol=2e-2, atol=1e-2)
+
+    check(rt.execute(0, x, sel, w, None), 0)
+    try:
+        ops.ffn_set_sync_spin_limit(0)
+        rt.execute(1, x, sel, w, None)       # the fused launch's down waits give up at once
+    finally:
+        ops.ffn_set_sync_spin_limit(None)
+    with pytest.raises(RuntimeError, match='gave up'):
+        rt.execute(0, x, sel, w, None)
+    rt.reset()                               # the error was reported: a clean reset
+    check(rt.execute(1, x, sel, w, None), 1)
+    check(rt.execute(1, x, sel, w, None), 1)  # resident now: the other launch path
+    try:
+        ops.ffn_set_sync_spin_limit(0)
+        rt.execute(0, x, sel, w, None)
+    finally:
+        ops.ffn_set_sync_spin_limit(None)
+    with pytest.raises(RuntimeError, match='gave up'):
+        rt.reset()
+    check(rt.execute(0, x, sel, w, None), 0)
+    try:
+        ops.ffn_set_sync_spin_limit(0)
+        rt.execute(1, x, sel, w, None)
+    finally:
+        ops.ffn_set_sync_spin_limit(None)
+    with pytest.raises(RuntimeError, match='gave up'):
+        rt.close()
