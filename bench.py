@@ -29,6 +29,10 @@ Also on the line:
   * decode_loop: the 48-layer Qwen3 decode loop (1024-token prefill, then 64-token steps,
     pooled cache of 1,843, W = 128 eviction), ``--loop-steps`` steps (default 8, bounded);
     packed fetches, with the raw-row run under ``raw``;
+  * generate: end-to-end greedy generation through a Qwen3-30B-A3B-shaped model with random
+    weights, every MoE block hooked into OffloadRuntime (the 48-layer packed pool, pooled 30 %
+    cache): the reference's serving protocol (warm-up, discarded and measured runs from an empty
+    cache, 200 ms release delay) and metrics, TTFT / TPOT / E2E / TPS as mean and sample std;
   * decode_raw: the headline stream with raw rows over the host link (OffloadRuntime(pack=
     False), the reference's transfer format);
   * decode_copy_kernel: the headline stream through OffloadRuntime(copy='kernel'): raw misses
@@ -86,6 +90,15 @@ def parse():
     p.add_argument('--cpu-seconds', type=float, default=20.0,
                    help='CPU time budget of the decode-stream baseline (5 repeats)')
     p.add_argument('--loop-steps', type=int, default=8, help='decode-loop steps (the reference loop runs 64)')
+    p.add_argument('--no-generate', action='store_true',
+                   help='skip the end-to-end generate block (TTFT / TPOT / E2E / TPS)')
+    p.add_argument('--gen-batch', type=int, default=16, help='generate: requests per run')
+    p.add_argument('--gen-prompt', type=int, default=512, help='generate: prompt tokens per request')
+    p.add_argument('--gen-output', type=int, default=16,
+                   help='generate: output tokens per request (the reference cells use 64)')
+    p.add_argument('--gen-repeats', type=int, default=3, help='generate: measured runs')
+    p.add_argument('--gen-discard', type=int, default=1,
+                   help='generate: unreported runs on the target prompts before the measured ones')
     p.add_argument('--copy-calibration-mib', type=int, default=0,
                    help='run one plain device copy kernel of this many MiB (read and written) '
                         'before the decode pass: the reference dispatch for scaling HBM byte '
@@ -128,6 +141,9 @@ def run_stacks(args, device):
             out['decode_loop'] = run_decode_loop(device, args.loop_steps, packed)
             out['decode_loop']['raw'] = loop_raw
             print('# decode loop done', file=sys.stderr, flush=True)
+            if not args.no_generate:
+                out['generate'] = run_generate(args, device, packed)
+                print('# generate done', file=sys.stderr, flush=True)
         packed.close()
         del packed
         gc.collect()
@@ -362,6 +378,8 @@ def gemm_ceiling(device):
     practical ceiling against which the grouped kernels' MFMA utilisation reads."""
     shapes = {'qwen3_largest_expert_up_8192x1536x2048': (8192, 1536, 2048),
               'deepseek_largest_expert_up_57344x2816x2048': (57344, 2816, 2048),
+              'dense_up_65536x1536x2048': (65536, 1536, 2048),
+              'dense_down_65536x2048x768': (65536, 2048, 768),
               'dense_8192x8192x8192': (8192, 8192, 8192)}
     g = torch.Generator(device=device)
     g.manual_seed(11)
@@ -386,6 +404,47 @@ def gemm_ceiling(device):
         del a, b, c
     torch.cuda.empty_cache()
     return out
+
+
+def tiled_dense(device, reps=10):
+    """The tiled kernels on one dense Qwen3-shaped expert of 65,536 rows (every row routed to
+    it with weight 1): the up projection 65536 x 1536 x 2048 (gate and up columns, SwiGLU
+    epilogue) and the down projection 65536 x 2048 x 768 (routing-weight epilogue), M x N x K,
+    each timed per launch with HIP events (median over ``reps``), next to hipBLASLt on the same
+    shapes in gemm_ceiling_hipblaslt."""
+    from ferry_amd import expert_ops as ops
+    from ferry_amd import workloads
+    M, H, I = 65536, 2048, 768
+    cache = workloads.expert_rows([0], 3 * H * I, seed=17, device=device)
+    x = workloads.hidden_states(M, H, seed=18, device=device)
+    sel = torch.zeros((M, 1), dtype=torch.int64, device=device)
+    lay = ops.layout(sel, torch.ones((M, 1), dtype=torch.bfloat16, device=device), 1)
+    act = torch.empty((M, I), dtype=torch.bfloat16, device=device)
+    out = torch.empty((M, H), dtype=torch.bfloat16, device=device)
+    one = np.zeros(1, np.int32)
+    res = {}
+    for name, phase, flops in (('up_65536x1536x2048', ops.PHASE_UP, 2 * M * 2 * I * H),
+                               ('down_65536x2048x768', ops.PHASE_DOWN, 2 * M * H * I)):
+        def launch():
+            ops.expert_ffn(cache, x, lay.w_sorted, lay.starts, lay.rows, lay.cols, one, one, H, I,
+                           act, out, max_rows=M, phases=phase)
+        for _ in range(3):
+            launch()
+        ts = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            launch()
+            e1.record()
+            e1.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        ms = float(np.median(ts))
+        tflops = flops / (ms * 1e-3) / 1e12
+        res[name] = dict(kernel='ffn_tiled_up' if phase == ops.PHASE_UP else 'ffn_tiled_down',
+                         us=ms * 1e3, tflops=tflops, frac=tflops / BF16_PEAK_TFLOPS)
+    del cache, x, act, out, lay
+    torch.cuda.empty_cache()
+    return res
 
 
 def read_ceiling(device, block, expert_bytes, reps=9):
@@ -579,6 +638,84 @@ def run_decode_loop(device, steps, pool):
 
 
 # ---------------------------------------------------------------------------------------------
+# end-to-end generation: the reference's serving metrics
+# ---------------------------------------------------------------------------------------------
+
+def qwen3_30b_a3b_config():
+    """The HF config of Qwen3-30B-A3B's architecture (its published config.json values)."""
+    from transformers import Qwen3MoeConfig
+    return Qwen3MoeConfig(
+        vocab_size=151936, hidden_size=2048, intermediate_size=6144, moe_intermediate_size=768,
+        num_hidden_layers=48, num_attention_heads=32, num_key_value_heads=4, head_dim=128,
+        num_experts=128, num_experts_per_tok=8, norm_topk_prob=True, decoder_sparse_step=1,
+        mlp_only_layers=[], max_position_embeddings=40960, rms_norm_eps=1e-6,
+        tie_word_embeddings=False, rope_parameters={'rope_type': 'default', 'rope_theta': 1e6})
+
+
+def run_generate(args, device, packed):
+    """The reference's serving measurement (scripts/run_cell.py:124-158) on one GPU: greedy
+    generation through a Qwen3-30B-A3B-shaped model with random weights (dense weights N(0,
+    0.02) on the GPU; the routed experts are the 48-layer pool's rows, fetched packed into a
+    pooled 30 % cache of 1,843 slots, FERRY policy, W = 128), every MoE block hooked into
+    OffloadRuntime.  One warm-up run on other prompts, ``--gen-discard`` unreported runs and
+    ``--gen-repeats`` measured runs on the target prompts, each from an empty cache and
+    released 200 ms after it is called; TTFT / TPOT / E2E / TPS as mean and sample std."""
+    from ferry_amd.harness import run_repeats, summarize, synthetic_model
+    from ferry_amd.model import QWEN3_30B_A3B, install_hooks, spec_from_config
+    from ferry_amd.quota import Topology
+    from ferry_amd.runtime import OffloadRuntime
+    cfg = qwen3_30b_a3b_config()
+    spec = spec_from_config(cfg)
+    assert spec == QWEN3_30B_A3B
+    cap = spec.cache_slots(0.30, 1)[0]
+    t0 = time.perf_counter()
+    model = synthetic_model(cfg, spec, device, seed=3)
+    rt = OffloadRuntime(spec, packed, [cap], 'ferry', Topology.uniform(1, spec.experts))
+    install_hooks(model, spec, rt, history_window=128)
+    build_s = time.perf_counter() - t0
+    g = torch.Generator(device=device)
+    g.manual_seed(5)
+    B, P = args.gen_batch, args.gen_prompt
+    warm = torch.randint(0, cfg.vocab_size, (B, P), generator=g, device=device)
+    target = torch.randint(0, cfg.vocab_size, (B, P), generator=g, device=device)
+
+    def log(rec):
+        print(f"# generate run {rec['repeat']} ({rec['phase']}): TTFT {rec['TTFT']:.3f} s, "
+              f"TPOT {rec['TPOT'] * 1e3:.1f} ms, TPS {rec['TPS']:.1f}, "
+              f"{rec['h2d_copies']} copies", file=sys.stderr, flush=True)
+
+    t0 = time.perf_counter()
+    records = run_repeats(model, rt, warm, target, steps=args.gen_output,
+                          repeats=args.gen_repeats, discard=args.gen_discard, log=log)
+    wall_s = time.perf_counter() - t0
+    rt.close()
+    summary = summarize(records)
+    keep = ('repeat', 'phase', 'TTFT', 'TPOT', 'E2E', 'TPS', 'h2d_copies',
+            'decode_fetches_per_rank', 'serial_wait_s', 'peak_allocated_bytes')
+    out = dict(
+        workload='qwen3_30b_a3b_generate_synthetic',
+        config=dict(layers=spec.layers, experts=spec.experts, topk=spec.topk,
+                    hidden=spec.hidden, intermediate=spec.intermediate, vocab=cfg.vocab_size,
+                    attention='32 heads x 128, 4 KV heads, SDPA', batch=B, prompt_tokens=P,
+                    output_tokens=args.gen_output, cache_slots=cap, history_window=128,
+                    policy='ferry', fetch='packed rows, two DMA streams',
+                    weights='random: dense N(0, 0.02) seed 3; experts = the stack pool rows',
+                    prompts='uniform random token IDs, seeded'),
+        repeats=args.gen_repeats, discarded=args.gen_discard,
+        **{key: summary[key] for key in ('TTFT', 'TPOT', 'E2E', 'TPS')},
+        units=dict(TTFT='s', TPOT='s', E2E='s', TPS='tokens/s'),
+        runs=[{key: r[key] for key in keep} for r in records],
+        model_build_s=build_s, wall_s=wall_s,
+        note=('TTFT = first token - release, TPOT = (last - first) / (output_tokens - 1), '
+              'TPS = batch * output_tokens / (last - release), as scripts/run_cell.py:150-154; '
+              'random weights route near-uniformly, so the expert cache hits less often than '
+              'with a trained model\'s temporal locality'))
+    del model
+    torch.cuda.empty_cache()
+    return out
+
+
+# ---------------------------------------------------------------------------------------------
 # CPU baseline: the reference's op order in torch on the host cores
 # ---------------------------------------------------------------------------------------------
 
@@ -748,6 +885,11 @@ def main():
         line['roofline_prefill'] = prefill_roofline(line['prefill'])
         line['prefill_deepseek'] = run_prefill(args, device, workloads.DEEPSEEK_PREFILL_STACK)
         line['gemm_ceiling_hipblaslt'] = gemm_ceiling(device)
+        line['tiled_dense'] = tiled_dense(device)
+        for key, shape in (('up_65536x1536x2048', 'dense_up_65536x1536x2048'),
+                           ('down_65536x2048x768', 'dense_down_65536x2048x768')):
+            line['tiled_dense'][key]['vs_hipblaslt'] = (
+                line['tiled_dense'][key]['tflops'] / line['gemm_ceiling_hipblaslt'][shape]['tflops'])
         print('# prefill layers done', file=sys.stderr, flush=True)
     if not args.no_stacks:
         line.update(run_stacks(args, device))
