@@ -114,11 +114,32 @@ def test_deepseek_layer_t256_all_resident(device, pack):
     rt.close()
 
 
+def _tile_edge_tokens(starts, rows, rng, tile_m=256, block=32):
+    """Per expert, tokens at the edges of its last (partial) M tile: the tile's first row, the
+    first and last rows of its last 32-row block that holds rows (the kernel skips the blocks
+    past the expert's end), two random rows of that tile; and the largest expert's first and
+    last rows."""
+    pick = set()
+    counts = np.diff(starts)
+    for e, n in enumerate(counts):
+        if n == 0:
+            continue
+        a = int(starts[e])
+        last0 = (n - 1) // tile_m * tile_m
+        blk0 = max(last0, (n - 1) // block * block)
+        for p in {last0, blk0, n - 1, *rng.integers(last0, n, 2).tolist()}:
+            pick.add(int(rows[a + p]))
+    big = int(np.argmax(counts))
+    pick.update((int(rows[starts[big]]), int(rows[starts[big + 1] - 1])))
+    return np.array(sorted(pick), np.int64)
+
+
 def test_deepseek_prefill_t65536_sampled_tokens(device):
     """The DeepSeek-V2-Lite prefill layer at full size (65,536 tokens, top-6 of 64, plus the
     shared experts), experts resident.  Each token's output depends only on its own row and
-    experts, so the oracle is evaluated exactly on a sample of tokens; routing and the layout
-    are checked on every token."""
+    experts, so the oracle is evaluated exactly on a sample of tokens that covers every
+    expert's partial last M tile and the largest expert's tail; routing and the layout are
+    checked on every token."""
     from ferry_amd import expert_ops as ops
     from ferry_amd import workloads
     from ferry_amd.model import deepseek_moe
@@ -145,9 +166,17 @@ def test_deepseek_prefill_t65536_sampled_tokens(device):
     ref_lay = layout_closed_form(sel_ref.numpy(), E, w_ref.float().numpy())
     for key in ('starts', 'rows', 'cols'):
         assert np.array_equal(getattr(lay, key).cpu().numpy(), ref_lay[key]), key
-    assert int(np.diff(ref_lay['starts']).max()) > 4096   # tiled MFMA path on the big experts
+    counts = np.diff(ref_lay['starts'])
+    assert int(counts.max()) > 4096   # tiled MFMA path on the big experts
+    # every expert's partial last M tile (its first row and its last 32-row block, where the
+    # kernel skips the row blocks past the expert's end), the largest expert's first and last
+    # rows, plus random tokens
+    assert (counts % 256 != 0).sum() >= 56
+    targeted = _tile_edge_tokens(ref_lay['starts'], ref_lay['rows'], np.random.default_rng(4))
     g = torch.Generator().manual_seed(4)
-    pick = torch.cat([torch.tensor([0, T - 1]), torch.randperm(T, generator=g)[:62]])
+    pick = torch.unique(torch.cat([torch.from_numpy(targeted), torch.tensor([0, T - 1]),
+                                   torch.randperm(T, generator=g)[:62]]))
+    assert len(pick) >= 200
     xs = x.cpu()[pick]
     ref = deepseek_layer_ref(lambda e: pool[e], srow.cpu(), xs, sel_ref[pick], w_ref[pick], E, H, I,
                              w.shared_intermediate)

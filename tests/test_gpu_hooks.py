@@ -23,7 +23,7 @@ SHAPE = dict(hidden_size=256, moe_intermediate_size=128, intermediate_size=512, 
              num_attention_heads=4, vocab_size=512)
 
 
-def _setup(family, device, cap=None):
+def _setup(family, device, cap=None, score='frequency'):
     from ferry_amd.loader import pool_from_model
     from ferry_amd.model import spec_from_config
     from ferry_amd.quota import Topology
@@ -39,7 +39,8 @@ def _setup(family, device, cap=None):
     spec = spec_from_config(cfg)
     pool = pool_from_model(model, spec)
     cap = cap or spec.layers * spec.experts
-    rt = OffloadRuntime(spec, pool, [cap], 'ferry', Topology.uniform(1, spec.experts))
+    rt = OffloadRuntime(spec, pool, [cap], 'ferry', Topology.uniform(1, spec.experts),
+                        eviction_score=score)
     return cfg, model, spec, pool, rt
 
 
@@ -91,6 +92,58 @@ def test_hooked_block_matches_oracle_and_hf(device, family):
 
 
 @pytest.mark.parametrize('family', ['qwen3_moe', 'deepseek_v2'])
+def test_hooked_block_probability_score(device, family):
+    """eviction_score='probability' through the hooks: the hook hands the runtime the fp32
+    router probabilities of the last W tokens (reference model.py:146 for Qwen3, :154-156 for
+    DeepSeek-V2), the runtime's history takes them as rows, and the eviction trace equals the
+    oracle's (GateHistoryRef fed the same probability rows, PlannerRef) call by call, with a
+    cache small enough to evict; the block outputs match the oracle."""
+    import numpy as np
+    from oracle.history import GateHistoryRef
+    from oracle.policy import PlannerRef
+    from ferry_amd.model import install_hooks
+    cap = 20     # above any one call's experts (16), below the layers' (32 or 48): evictions
+    cfg, model, spec, pool, rt = _setup(family, device, cap=cap, score='probability')
+    E, k, H, I = spec.experts, spec.topk, spec.hidden, spec.intermediate
+    blocks = [model.model.layers[i].mlp for i in spec.moe_layers]
+    gates = [b.gate.weight.detach().clone() for b in blocks]
+    shared = [None] * len(blocks)
+    if family == 'deepseek_v2':
+        shared = [torch.cat([b.shared_experts.gate_proj.weight.reshape(-1),
+                             b.shared_experts.up_proj.weight.reshape(-1),
+                             b.shared_experts.down_proj.weight.reshape(-1)]).cpu() for b in blocks]
+    install_hooks(model, spec, rt, history_window=128)
+    hist, planner = GateHistoryRef(spec.layers, E, 128), PlannerRef(spec.layers, E, cap)
+    g = torch.Generator(device=device).manual_seed(8)
+    calls = 0
+    for step, T in enumerate([5, 150, 1, 40, 200, 3, 9, 130, 2, 60]):
+        pos = step % spec.layers
+        x = torch.randn((1, T, H), generator=g, device=device).to(torch.bfloat16)
+        flat = x.reshape(-1, H)
+        if family == 'qwen3_moe':
+            w_ref, sel_ref, probs_ref = qwen3_router(F.linear(flat, gates[pos]).cpu(), k)
+        else:
+            w_ref, sel_ref, probs_ref = deepseek_router(
+                F.linear(flat.float(), gates[pos].float()).cpu(), k)
+        with torch.no_grad():
+            out = blocks[pos](x)
+        out = (out[0] if isinstance(out, tuple) else out).reshape(-1, H)
+        hist.update(pos, probs_ref[-min(T, 128):].numpy())
+        planner.plan(rt.event - 1, pos, sel_ref.numpy(), hist.scores(pos))
+        assert np.array_equal(rt.controller.slots[0], planner.slots), step
+        assert np.array_equal(rt.controller.last, planner.last), step
+        assert np.array_equal(rt.controller.scores, planner.scores), step
+        torch.cuda.synchronize()
+        ref = moe_layer_ref(lambda e: pool[pos * E + e], flat.cpu(), sel_ref, w_ref, E, H, I)
+        if shared[pos] is not None:
+            ref = ref + shared_mlp_ref(shared[pos], flat.cpu(), H, 2 * I)
+        torch.testing.assert_close(out.cpu().float(), ref.float(), rtol=2e-2, atol=1e-2)
+        calls += 1
+    assert calls == 10 and rt.h2d.copies > cap
+    rt.close()
+
+
+@pytest.mark.parametrize('family', ['qwen3_moe', 'deepseek_v2'])
 def test_hooked_model_greedy_decode(device, family):
     """Prefill + 8 greedy decode steps with a KV cache through the hooked model, with a cache
     smaller than the experts so that fetches and evictions happen every step."""
@@ -136,3 +189,26 @@ def test_hooks_on_transformers_457_block_layout(device):
     torch.testing.assert_close(logits, F.linear(x.reshape(-1, spec.hidden), old.gate.weight))
     assert old.experts is None
     rt.close()
+
+
+@pytest.mark.parametrize('family', ['qwen3_moe', 'deepseek_v2'])
+def test_load_default_device_cuda(device, tmp_path, family):
+    """``load(path, spec)`` with its default device='cuda' places every dense tensor on the
+    current GPU (a device without an index must compare equal to 'cuda:<current>'), equal to
+    the saved ones, and the pool equals the experts' rows."""
+    from ferry_amd.loader import load
+    from ferry_amd.model import spec_from_config
+    from test_model_loader import expert_rows
+    cfg = tiny_qwen3_config() if family == 'qwen3_moe' else tiny_deepseek_config()
+    model = tiny_model(cfg, seed=6)
+    spec = spec_from_config(cfg)
+    model.save_pretrained(tmp_path)
+    loaded, pool = load(tmp_path, spec)
+    assert pool.is_pinned() and torch.equal(pool, expert_rows(model, spec))
+    cur = torch.device('cuda', torch.cuda.current_device())
+    ref = {n: t for n, t in model.state_dict().items() if '.experts.' not in n}
+    got = loaded.state_dict()
+    for n, t in ref.items():
+        assert got[n].device == cur, n
+        assert torch.equal(got[n].cpu(), t), n
+    assert all(b.device == cur for b in loaded.buffers())

@@ -112,3 +112,79 @@ def test_qwen3_prefill_t8192_full_layer(device):
     ref = moe_layer_ref(lambda e: pool[e], x.cpu()[pick], sel_ref[pick], wts_c[pick], E, H, I)
     torch.testing.assert_close(out_rt.cpu()[pick].float(), ref.float(), rtol=2e-2, atol=1e-2)
     rt.close()
+
+
+def _edge_tokens(starts, rows, rng):
+    """A compact sample per layer: one row of every small expert; per tiled expert the first
+    row of its last M tile, the first and last rows of that tile's last 32-row block and one
+    random row of the tile; the largest expert's first and last rows."""
+    pick = set()
+    counts = np.diff(starts)
+    for e, n in enumerate(counts):
+        if n == 0:
+            continue
+        a = int(starts[e])
+        if n <= SMALL_MAX_ROWS:
+            pick.add(int(rows[a + rng.integers(n)]))
+            continue
+        last0 = (n - 1) // TILE_M * TILE_M
+        blk0 = max(last0, (n - 1) // 32 * 32)
+        for p in {last0, blk0, n - 1, int(rng.integers(last0, n))}:
+            pick.add(int(rows[a + p]))
+    big = int(np.argmax(counts))
+    pick.update((int(rows[starts[big]]), int(rows[starts[big + 1] - 1])))
+    return np.array(sorted(pick), np.int64)
+
+
+def test_qwen3_prefill_stack_4_layers_packed_pooled_cache(device):
+    """Four layers of the Qwen3-30B-A3B-shaped prefill stack (8192 tokens each, the stack's
+    seeded routing) through OffloadRuntime with packed fetches and a pooled cache of 153 slots
+    (30 % of 4 x 128): each layer's ~127 active experts evict most of the previous layer's, and
+    its misses are copied in chunks, heaviest first.  The fetch / eviction trace equals the
+    oracle's (GateHistoryRef + PlannerRef) after every layer, and each layer's output matches
+    the reference op order on a sample of tokens at the tile edges."""
+    from ferry_amd import expert_ops as ops
+    from ferry_amd import workloads
+    from ferry_amd.h2d import PackedPool
+    from ferry_amd.quota import Topology
+    from ferry_amd.runtime import OffloadRuntime
+    from oracle.history import GateHistoryRef, frequency_rows
+    from oracle.policy import PlannerRef
+    w = workloads.QWEN3_PREFILL_STACK
+    L = 4
+    spec = replace(w.spec, moe_layers=w.spec.moe_layers[:L])
+    E, k, H, I, T = spec.experts, spec.topk, spec.hidden, spec.intermediate, w.tokens
+    cap = int(0.30 * L * E)
+    assert cap == 153
+    print(f'qwen3 prefill stack: {L} layers, T={T}, cap={cap}, packed', flush=True)
+    gen = workloads.RouterLogits(replace(w, layers=L), device)
+    logits = [gen.next(layer, T) for layer in range(L)]
+    x = workloads.hidden_states(T, H, seed=w.seed + 7, device=device)
+    pool = workloads.make_pool(spec, L, seed=w.seed, pinned=False)
+    packed = PackedPool(pool, threads=16)
+    rt = OffloadRuntime(spec, packed, [cap], 'ferry', Topology.uniform(1, E))
+    hist, planner = GateHistoryRef(L, E, 128), PlannerRef(L, E, cap)
+    rng = np.random.default_rng(5)
+    misses = 0
+    for layer in range(L):
+        wts, sel = ops.router_topk(logits[layer], k)
+        out = rt.execute(layer, x, sel, wts, None)
+        w_ref, sel_ref, _ = qwen3_router(logits[layer].cpu(), k)
+        assert torch.equal(sel.cpu(), sel_ref) and torch.equal(wts.cpu(), w_ref), layer
+        hist.update(layer, frequency_rows(sel_ref.numpy(), E, 128))
+        fetches, _ = planner.plan(rt.event - 1, layer, sel_ref.numpy(), hist.scores(layer))
+        misses += len(fetches)
+        assert np.array_equal(rt.controller.slots[0], planner.slots), layer
+        assert np.array_equal(rt.controller.owner, planner.owner), layer
+        assert np.array_equal(rt.controller.last, planner.last), layer
+        assert np.array_equal(rt.controller.scores, planner.scores), layer
+        torch.cuda.synchronize()
+        ref_lay = layout_closed_form(sel_ref.numpy(), E, w_ref.view(torch.int16).numpy())
+        pick = _edge_tokens(ref_lay['starts'], ref_lay['rows'], rng)
+        ref = moe_layer_ref(lambda e: pool[layer * E + e], x.cpu()[pick], sel_ref[pick],
+                            w_ref[pick], E, H, I)
+        torch.testing.assert_close(out.cpu()[pick].float(), ref.float(), rtol=2e-2, atol=1e-2)
+        print(f'layer {layer}: {len(fetches)} misses, {len(pick)} tokens checked', flush=True)
+    assert rt.h2d.copies == misses == int(rt.fetches_per_rank.sum()) > 3 * cap
+    rt.close()
+    packed.close()
