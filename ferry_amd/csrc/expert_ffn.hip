@@ -72,6 +72,14 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g * u * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
 }
 
+// two floats rounded to bf16 (round to nearest even, as f32_to_bf16) in one instruction,
+// packed as lo | hi << 16
+__device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 b16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, b16x2));
+}
+
 __device__ __forceinline__ bf16x8 load8(const bf16_t* p) {
   return *reinterpret_cast<const bf16x8*>(p);
 }
@@ -1132,6 +1140,8 @@ constexpr int kTileLds = STAGES * kStageBytes / 2;               // bf16 element
 struct TileTable {
   int32_t cum[kListMax + 1];  // cumulative M tiles over list entries
   int32_t total;
+  int64_t start[kListMax];    // per list entry: its expert's first grouped row, and row count
+  int32_t rows[kListMax];
 };
 
 // Wavefront 0 builds the cumulative M-tile counts of the big experts of the list.
@@ -1146,8 +1156,11 @@ __device__ void build_tile_table(const FfnArgs& a, TileTable& tt) {
       int c = 0;
       if (li < a.list.n) {
         const int e = a.list.expert[li];
-        const int64_t n = a.starts[e + 1] - a.starts[e];
+        const int64_t s0 = a.starts[e];
+        const int64_t n = a.starts[e + 1] - s0;
         c = n > kSkinnyMax ? (int)((n + BM - 1) / BM) : 0;
+        tt.start[li] = s0;
+        tt.rows[li] = (int32_t)n;
       }
       cnt[q] = c;
       local += c;
@@ -1200,7 +1213,7 @@ template <int MODE>
 __global__ __launch_bounds__(kTiledThreads, 1) void ffn_tiled(FfnArgs a) {
   __shared__ TileTable tt;
   __shared__ __attribute__((aligned(1024))) bf16_t smem[kTileLds];
-  __shared__ int64_t orow_s[BM];
+  __shared__ int64_t orow_s[BM];   // phase 2: byte offset of each tile row's output row
   __shared__ float wt_s[BM];
   build_tile_table(a, tt);
   const int64_t K = MODE == 0 ? a.H : a.I;
@@ -1221,9 +1234,8 @@ __global__ __launch_bounds__(kTiledThreads, 1) void ffn_tiled(FfnArgs a) {
   for (int tile = lslot; tile < total; tile += gridDim.x) {
     const int mt_global = tile / ntn, ntile = tile % ntn;
     const int li = find_entry(tt, mt_global);
-    const int e = a.list.expert[li];
-    const int64_t start = a.starts[e];
-    const int n = (int)(a.starts[e + 1] - start);
+    const int64_t start = tt.start[li];
+    const int n = tt.rows[li];
     const int m0 = (mt_global - tt.cum[li]) * BM;
     const bf16_t* slot = a.cache + (int64_t)a.list.slot[li] * 3 * a.H * a.I;
 
@@ -1280,7 +1292,7 @@ __global__ __launch_bounds__(kTiledThreads, 1) void ffn_tiled(FfnArgs a) {
             const int64_t p = start + rr;
             const int64_t t = a.rows[p], j = a.cols[p];
             wt = bf16_to_f32(a.w[t * a.k + j]);
-            orow = a.out_mode == 0 ? t * a.k + j : p;
+            orow = (a.out_mode == 0 ? t * a.k + j : p) * a.H * 2;   // byte offset of the row
           }
           orow_s[r] = orow;
           wt_s[r] = wt;
@@ -1393,12 +1405,19 @@ __global__ __launch_bounds__(kTiledThreads, 1) void ffn_tiled(FfnArgs a) {
     // 32x32 accumulator layout: column = lane & 31, row(v) = (v / 4) * 8 + (lane / 32) * 4 + v % 4.
     if constexpr (MODE == 1) {
       // phase-2 epilogue, straight from the accumulators: for each pair of rows (v, v + 1) a
-      // lane computes both of its column's outputs, swaps one with its neighbour lane (DPP
-      // quad_perm [1,0,3,2]), and stores two adjacent columns of one row as 4 bytes -- the even
-      // lane row v, the odd lane row v + 1.  No LDS staging and no barrier before the stores;
+      // lane rounds both of its column's values at once (v_cvt_pk_bf16_f32), applies the rows'
+      // routing weights and rounds again into one packed word (row v low, row v + 1 high),
+      // swaps that word with its neighbour lane (DPP quad_perm [1,0,3,2]) and picks two adjacent
+      // columns of one row with one byte permute -- the even lane row v (its own low half, the
+      // neighbour's low half), the odd lane row v + 1 (the neighbour's high half, its own high
+      // half) -- stored as 4 bytes.  This is the issue-bound part of a phase-2 tile (all eight
+      // wavefronts run it at once), so each row pair costs one address and about nine VALU
+      // instructions per 32-column block.  No LDS staging and no barrier before the stores;
       // the barrier after them keeps the row table until every wavefront has read it.
       const bool odd = lane & 1;
-      const int64_t colw = (int64_t)ntile * BN + wn * 64 + (l32 & ~1);
+      const uint32_t pick = odd ? 0x03020706u : 0x05040100u;
+      char* const obase = reinterpret_cast<char*>(a.out) +
+                          ((int64_t)ntile * BN + wn * 64 + (l32 & ~1)) * 2;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -1407,18 +1426,17 @@ __global__ __launch_bounds__(kTiledThreads, 1) void ffn_tiled(FfnArgs a) {
           const int r0 = wm * 128 + i * 32 + (v0 >> 2) * 8 + (lane >> 5) * 4 + (v0 & 3);  // even
           const float w0 = wt_s[r0], w1 = wt_s[r0 + 1];
           const int r = odd ? r0 + 1 : r0;
-          const int64_t orow = orow_s[r];
+          char* const rowp = obase + orow_s[r];
           const bool ok = m0 + r < n;
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
-            const uint32_t y0 = f32_to_bf16(bf16r(acc[i][j][v0]) * w0);
-            const uint32_t y1 = f32_to_bf16(bf16r(acc[i][j][v0 + 1]) * w1);
-            const uint32_t send = odd ? y0 : y1;
-            const uint32_t recv =
-                (uint32_t)__builtin_amdgcn_update_dpp((int)send, (int)send, 0xB1, 0xf, 0xf, false);
-            const uint32_t packed = odd ? (recv | (y1 << 16)) : (y0 | (recv << 16));
+            const uint32_t g = pk_bf16(acc[i][j][v0], acc[i][j][v0 + 1]);
+            const uint32_t y = pk_bf16(__uint_as_float(g << 16) * w0,
+                                       __uint_as_float(g & 0xffff0000u) * w1);
+            const uint32_t yn =
+                (uint32_t)__builtin_amdgcn_update_dpp((int)y, (int)y, 0xB1, 0xf, 0xf, false);
             if (ok)
-              *reinterpret_cast<uint32_t*>(&a.out[orow * a.H + colw + j * 32]) = packed;
+              *reinterpret_cast<uint32_t*>(rowp + j * 64) = __builtin_amdgcn_perm(yn, y, pick);
           }
         }
       }
@@ -1427,51 +1445,44 @@ __global__ __launch_bounds__(kTiledThreads, 1) void ffn_tiled(FfnArgs a) {
     }
     __syncthreads();  // all fragment reads done before the staging area is reused
 
-    // epilogue: bf16 tile staged in LDS, then 16-byte row stores.
-    constexpr int OC = MODE == 0 ? 128 : 256;  // output columns of the tile
-    constexpr int OLD = OC + 8;
-    constexpr int HALVES = MODE == 0 ? 1 : 2;
-    constexpr int HROWS = BM / HALVES;
-    constexpr int CPR = OC / 8;  // 16-byte chunks per row
+    // phase-1 epilogue: act[p, i0 + c] = bf16(silu(bf16 g) * bf16 u), the bf16 tile staged in
+    // LDS (128 columns), then 16-byte row stores.  g and u are rounded by one packed
+    // conversion; the results of rows (v, v + 1) of a column are packed likewise, swapped with
+    // the neighbour lane and byte-permuted into two adjacent columns of one row (as in the
+    // phase-2 epilogue), so that each LDS write carries two outputs.
+    constexpr int OC = 128, OLD = OC + 8, CPR = OC / 8;   // CPR: 16-byte chunks per row
     bf16_t* os = smem;
+    const bool odd = lane & 1;
+    const uint32_t pick = odd ? 0x03020706u : 0x05040100u;
+    const int col = wn * 32 + (l32 & ~1);
 #pragma unroll
-    for (int hf = 0; hf < HALVES; ++hf) {
-      if (HALVES == 1 || wm == hf) {
+    for (int i = 0; i < 4; ++i) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int r = wm * 128 + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-            const int rs = r - hf * HROWS;
-            if (MODE == 0) {
-              const float g = bf16r(acc[i][0][v]), u = bf16r(acc[i][1][v]);
-              os[rs * OLD + wn * 32 + l32] = f32_to_bf16(silu_mul(g, u));
-            } else {
-              const float wt = wt_s[r];
-#pragma unroll
-              for (int j = 0; j < 2; ++j)
-                os[rs * OLD + wn * 64 + j * 32 + l32] = f32_to_bf16(bf16r(acc[i][j][v]) * wt);
-            }
-          }
-        }
+      for (int vp = 0; vp < 8; ++vp) {
+        const int v0 = 2 * vp;
+        const int r0 = wm * 128 + i * 32 + (v0 >> 2) * 8 + (lane >> 5) * 4 + (v0 & 3);  // even
+        const uint32_t gu0 = pk_bf16(acc[i][0][v0], acc[i][1][v0]);
+        const uint32_t gu1 = pk_bf16(acc[i][0][v0 + 1], acc[i][1][v0 + 1]);
+        const float s0 = silu_mul(__uint_as_float(gu0 << 16), __uint_as_float(gu0 & 0xffff0000u));
+        const float s1 = silu_mul(__uint_as_float(gu1 << 16), __uint_as_float(gu1 & 0xffff0000u));
+        const uint32_t y = pk_bf16(s0, s1);
+        const uint32_t yn =
+            (uint32_t)__builtin_amdgcn_update_dpp((int)y, (int)y, 0xB1, 0xf, 0xf, false);
+        const int r = odd ? r0 + 1 : r0;
+        *reinterpret_cast<uint32_t*>(&os[r * OLD + col]) = __builtin_amdgcn_perm(yn, y, pick);
       }
-      __syncthreads();
-      for (int c = tid; c < HROWS * CPR; c += kTiledThreads) {
-        const int rs = c / CPR, cc = (c % CPR) * 8;
-        const int r = rs + hf * HROWS;
-        if (m0 + r >= n) continue;
-        const u32x4 v = *reinterpret_cast<const u32x4*>(&os[rs * OLD + cc]);
-        if (MODE == 0) {
-          *reinterpret_cast<u32x4*>(&a.act[(start + m0 + r) * a.I + ntile * 128 + cc]) = v;
-        } else {
-          *reinterpret_cast<u32x4*>(&a.out[orow_s[r] * a.H + ntile * BN + cc]) = v;
-        }
-      }
-      // the staging reads are complete (their values are in the stores); the stores stay in
-      // flight across the barrier (__syncthreads would wait for them)
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      wg_barrier();
     }
+    __syncthreads();
+    for (int c = tid; c < BM * CPR; c += kTiledThreads) {
+      const int r = c / CPR, cc = (c % CPR) * 8;
+      if (m0 + r >= n) continue;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(&os[r * OLD + cc]);
+      *reinterpret_cast<u32x4*>(&a.act[(start + m0 + r) * a.I + ntile * 128 + cc]) = v;
+    }
+    // the staging reads are complete (their values are in the stores); the stores stay in
+    // flight across the barrier (__syncthreads would wait for them)
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    wg_barrier();
   }
 }
 
