@@ -364,6 +364,8 @@ def run_prefill(args, device, w):
                 mfma_util=flops / (gemm_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
                 active_experts=int((counts > 0).sum()), max_rows=int(counts.max()),
                 median_rows=float(np.median(counts[counts > 0])), tiled_rows=tiled_rows,
+                small_experts=int(((counts > 0) & (counts <= 64)).sum()),
+                small_rows=int(counts[(counts > 0) & (counts <= 64)].sum()),
                 tiled_experts=n_tiled, routed_tiled_up_bytes=tiled_up_bytes,
                 routed_tiled_down_bytes=tiled_down_bytes,
                 tiled_up_launch_tflop=tiled_up_launch_flops / 1e12,
@@ -410,8 +412,9 @@ def tiled_dense(device, reps=10):
     """The tiled kernels on one dense Qwen3-shaped expert of 65,536 rows (every row routed to
     it with weight 1): the up projection 65536 x 1536 x 2048 (gate and up columns, SwiGLU
     epilogue) and the down projection 65536 x 2048 x 768 (routing-weight epilogue), M x N x K,
-    each timed per launch with HIP events (median over ``reps``), next to hipBLASLt on the same
-    shapes in gemm_ceiling_hipblaslt."""
+    each timed per launch with HIP events (median over ``reps`` back-to-back launches, and over
+    launches that each follow 50 ms of idle GPU), next to hipBLASLt on the same shapes in
+    gemm_ceiling_hipblaslt."""
     from ferry_amd import expert_ops as ops
     from ferry_amd import workloads
     M, H, I = 65536, 2048, 768
@@ -440,22 +443,33 @@ def tiled_dense(device, reps=10):
             ts.append(e0.elapsed_time(e1))
         ms = float(np.median(ts))
         tflops = flops / (ms * 1e-3) / 1e12
+        # the same launch after 50 ms of idle GPU each time: the clock the chip holds for a
+        # burst, against the back-to-back launches above (the MFMA loop is power-limited)
+        burst = []
+        for _ in range(5):
+            time.sleep(0.05)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            launch()
+            e1.record()
+            e1.synchronize()
+            burst.append(e0.elapsed_time(e1))
+        bms = float(np.median(burst))
         res[name] = dict(kernel='ffn_tiled_up' if phase == ops.PHASE_UP else 'ffn_tiled_down',
-                         us=ms * 1e3, tflops=tflops, frac=tflops / BF16_PEAK_TFLOPS)
+                         us=ms * 1e3, tflops=tflops, frac=tflops / BF16_PEAK_TFLOPS,
+                         launches_us=[round(t * 1e3, 1) for t in ts],
+                         after_idle_us=bms * 1e3,
+                         after_idle_tflops=flops / (bms * 1e-3) / 1e12)
     del cache, x, act, out, lay
     torch.cuda.empty_cache()
     return res
 
 
-def read_ceiling(device, block, expert_bytes, reps=9):
-    """Plain cold reads (the library's hbm_read, 32 KiB workgroups) of the byte counts of a decode
-    step's two FFN launches (the resident experts', the fetched experts'), measured in the same
-    run: the practical ceiling against which the decode FFN's HBM fraction reads.  A 1 GiB read
-    before each repeat evicts the buffers from the memory-side cache."""
+def cold_reads(device, sizes, reps=9):
+    """Plain cold reads (the library's hbm_read, 32 KiB workgroups) of buffers of the given byte
+    counts, each event-timed (median over ``reps``); a 1 GiB read before each repeat evicts them
+    from the memory-side cache.  Returns {name: dict(bytes, us, gbs, frac)}."""
     from ferry_amd import expert_ops as ops
-    fetched = block['misses_per_step']
-    resident = block['active_experts_per_step'] - fetched
-    sizes = {'resident_launch': resident * expert_bytes, 'fetched_launch': fetched * expert_bytes}
     flush = torch.ones(1 << 30, dtype=torch.uint8, device=device)
     bufs = {k: torch.ones(int(v) // 256 * 256, dtype=torch.uint8, device=device)
             for k, v in sizes.items()}
@@ -472,20 +486,54 @@ def read_ceiling(device, block, expert_bytes, reps=9):
         for i, k in enumerate(bufs):
             times[k].append(ev[i].elapsed_time(ev[i + 1]) * 1e3)
     out = {}
-    total_b = total_us = 0.0
     for k, b in bufs.items():
         us = float(np.median(times[k]))
         out[k] = dict(bytes=b.numel(), us=us, gbs=b.numel() / (us * 1e-6) / 1e9,
                       frac=b.numel() / (us * 1e-6) / 1e9 / HBM_PEAK_GBS)
-        total_b += b.numel()
-        total_us += us
+    del flush, bufs
+    torch.cuda.empty_cache()
+    return out
+
+
+def read_ceiling(device, block, expert_bytes, reps=9):
+    """Plain cold reads of the byte counts of a decode step's two FFN launches (the resident
+    experts', the fetched experts'), measured in the same run: the practical ceiling against
+    which the decode FFN's HBM fraction reads."""
+    fetched = block['misses_per_step']
+    resident = block['active_experts_per_step'] - fetched
+    out = cold_reads(device, {'resident_launch': resident * expert_bytes,
+                              'fetched_launch': fetched * expert_bytes}, reps)
+    total_b = sum(v['bytes'] for v in out.values())
+    total_us = sum(v['us'] for v in out.values())
     read_gbs = total_b / (total_us * 1e-6) / 1e9
     out.update(kernel='hbm_read_kernel (plain read, 32 KiB workgroups, data cold)',
                both_gbs=read_gbs, both_frac=read_gbs / HBM_PEAK_GBS,
                ffn_over_read=block['ffn_gbs'] / read_gbs)
-    del flush, bufs
-    torch.cuda.empty_cache()
     return out
+
+
+def small_expert_ceiling(device, pre, spec):
+    """The prefill layer's small-expert launches (experts of at most 64 rows: ffn_up_skinny,
+    ffn_down_skinny) against plain cold reads of their weight bytes, measured in the same run."""
+    n = pre['small_experts']
+    H, I = spec.hidden, spec.intermediate
+    reads = cold_reads(device, {'up_weights': n * 2 * I * H * 2, 'down_weights': n * I * H * 2})
+    up_us = pre['kernel_avg_launch_us']['ffn_up_skinny']
+    down_us = pre['kernel_avg_launch_us']['ffn_down_skinny']
+    return dict(experts=n, rows=pre['small_rows'],
+                up=dict(launch_us=up_us, read_us=reads['up_weights']['us'],
+                        launch_over_read=up_us / reads['up_weights']['us'],
+                        weight_bytes=reads['up_weights']['bytes'],
+                        launch_gbs=reads['up_weights']['bytes'] / (up_us * 1e-6) / 1e9,
+                        read_gbs=reads['up_weights']['gbs']),
+                down=dict(launch_us=down_us, read_us=reads['down_weights']['us'],
+                          launch_over_read=down_us / reads['down_weights']['us'],
+                          weight_bytes=reads['down_weights']['bytes'],
+                          launch_gbs=reads['down_weights']['bytes'] / (down_us * 1e-6) / 1e9,
+                          read_gbs=reads['down_weights']['gbs']),
+                note='launch: mean per-launch HIP-event time in the prefill block; read: the '
+                     'same weight bytes read cold by hbm_read (the token rows, read from L2, '
+                     'are not in the ceiling)')
 
 
 def prefill_roofline(pre):
@@ -883,6 +931,8 @@ def main():
         from ferry_amd import workloads
         line['prefill'] = run_prefill(args, device, workloads.QWEN3_PREFILL_STACK)
         line['roofline_prefill'] = prefill_roofline(line['prefill'])
+        line['prefill']['small_expert_ceiling'] = small_expert_ceiling(
+            device, line['prefill'], workloads.QWEN3_PREFILL_STACK.spec)
         line['prefill_deepseek'] = run_prefill(args, device, workloads.DEEPSEEK_PREFILL_STACK)
         line['gemm_ceiling_hipblaslt'] = gemm_ceiling(device)
         line['tiled_dense'] = tiled_dense(device)
