@@ -56,6 +56,7 @@ SIGNATURES = [
     ('ferry_h2d_synchronize', ctypes.c_int, [_c_p]),
     ('ferry_h2d_reset', ctypes.c_int, [_c_p]),
     ('ferry_h2d_copies', _i64, [_c_p]),
+    ('ferry_h2d_groups', _i64, [_c_p, _c_p, _i64]),
     ('ferry_h2d_stream', _c_p, [_c_p]),
     ('ferry_h2d_set_engine', ctypes.c_int, [_c_p, _i32]),
     ('ferry_h2d_set_defer_last', ctypes.c_int, [_c_p, _i32]),

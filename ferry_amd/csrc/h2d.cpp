@@ -126,6 +126,9 @@ struct ferry_h2d {
   int64_t batch = 0;
   std::vector<int64_t> call_of;       // per slot: last packed DMA call that wrote it
   int64_t call = 0;
+  // the last fetch call's groups of rows that become ready together (positions in the call,
+  // each group's end, in call order): a packed DMA call's sub-batches, one group otherwise
+  std::vector<int64_t> group_ends;
   // packed pool (ferry_h2d_use_packed): DMA copies move packed rows into device staging
   // buffers, and an unpack kernel writes the slots
   const ferry_packed_pool* packed = nullptr;
@@ -421,6 +424,7 @@ static int fetch_packed(ferry_h2d* h, const int64_t* slots, const int64_t* keys,
       }
       h->copies += i1 - i0;
       remaining -= total;
+      h->group_ends.push_back(i1);
       i0 = i1;
       continue;
     }
@@ -439,6 +443,7 @@ static int fetch_packed(ferry_h2d* h, const int64_t* slots, const int64_t* keys,
     prev = ev;
     h->copies += i1 - i0;
     remaining -= total;
+    h->group_ends.push_back(i1);
     i0 = i1;
   }
   return 0;
@@ -447,6 +452,7 @@ static int fetch_packed(ferry_h2d* h, const int64_t* slots, const int64_t* keys,
 extern "C" int ferry_h2d_fetch(ferry_h2d* h, const int64_t* slots, const int64_t* keys,
                                int64_t n) {
   ferry::clear_error();
+  h->group_ends.clear();
   if (n <= 0) return 0;
   if (resolve_deferred(h, h->unpack) != 0) return 3;
   // What a copy into a slot must follow: the last compute that read the slot (WAR) and any
@@ -522,6 +528,7 @@ extern "C" int ferry_h2d_fetch(ferry_h2d* h, const int64_t* slots, const int64_t
     if (!known) h->kernel_last.emplace_back(s, ev);
     for (int64_t i = 0; i < n; ++i) h->copy_seq[(size_t)slots[i]] = h->seq++;
     h->copies += n;
+    h->group_ends.push_back(n);
     return 0;
   }
   // No unconditional cross-lane wait: a lane waiting on an event that another DMA queue
@@ -541,6 +548,7 @@ extern "C" int ferry_h2d_fetch(ferry_h2d* h, const int64_t* slots, const int64_t
   }
   const int64_t rb = h->row_bytes;
   if (h->packed) return fetch_packed(h, slots, keys, n);
+  h->group_ends.push_back(n);
   if (!repeated) {
     const int64_t total = n * rb;
     for (int l = 0; l < kLanes; ++l) {
@@ -707,6 +715,7 @@ extern "C" int ferry_h2d_reset(ferry_h2d* h) {
   h->batch_of.assign(rows, 0);
   h->call_of.assign(rows, 0);
   h->call = 0;
+  h->group_ends.clear();
   h->used.assign(rows, nullptr);
   h->ring_ev.assign(h->ring_ev.size(), nullptr);
   h->ring_next = 0;
@@ -722,6 +731,17 @@ extern "C" int ferry_h2d_reset(ferry_h2d* h) {
 }
 
 extern "C" int64_t ferry_h2d_copies(const ferry_h2d* h) { return h ? h->copies : 0; }
+
+extern "C" int64_t ferry_h2d_groups(const ferry_h2d* h, int64_t* ends, int64_t max_groups) {
+  ferry::clear_error();
+  if (!h || max_groups < 0 || (max_groups > 0 && !ends)) {
+    ferry::set_error("h2d_groups: bad arguments");
+    return -1;
+  }
+  const int64_t n = (int64_t)h->group_ends.size();
+  for (int64_t i = 0; i < n && i < max_groups; ++i) ends[i] = h->group_ends[(size_t)i];
+  return n;
+}
 
 extern "C" int ferry_h2d_set_engine(ferry_h2d* h, int32_t kind) {
   ferry::clear_error();

@@ -153,6 +153,18 @@ class H2DEngine:
     def copies(self):
         return int(lib().ferry_h2d_copies(self._h))
 
+    def groups(self):
+        """Ends (exclusive positions in the call's slot list) of the last fetch call's groups
+        of rows that become ready together: a packed DMA call's sub-batches, otherwise one."""
+        ends = np.zeros(64, np.int64)
+        n = int(lib().ferry_h2d_groups(self._h, ends.ctypes.data, len(ends)))
+        if n < 0:
+            check(1, 'H2DEngine.groups')
+        if n > len(ends):
+            ends = np.zeros(n, np.int64)
+            n = int(lib().ferry_h2d_groups(self._h, ends.ctypes.data, len(ends)))
+        return ends[:n].tolist()
+
     @property
     def stream(self):
         """The engine's copy stream as a torch.cuda.ExternalStream."""

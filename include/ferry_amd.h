@@ -259,6 +259,13 @@ int ferry_h2d_synchronize(ferry_h2d* h);
 int ferry_h2d_reset(ferry_h2d* h);
 /* expert_ops.cpp:135 */
 int64_t ferry_h2d_copies(const ferry_h2d* h);
+/* The last fetch call's groups of rows that become ready together (no counterpart in the
+ * reference, which waits for all of a call's copies at once): with a packed pool in DMA mode
+ * its sub-batches, each unpacked as soon as its copies land, otherwise one group.  Writes the
+ * groups' ends (positions in the call's slot list, exclusive, ascending) into ends[0..max) and
+ * returns the number of groups (0 after an empty call or a reset; -1 on bad arguments).  A
+ * caller can wait for and compute each group's experts while the later groups still copy. */
+int64_t ferry_h2d_groups(const ferry_h2d* h, int64_t* ends, int64_t max_groups);
 /* the engine's copy stream (for event timing by the caller): after a fetch call its queue ends
  * with the call's copies -- the first DMA lane, which the others join, or, with a packed pool
  * attached, the stream that runs the unpacks */

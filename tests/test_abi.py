@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_errors():
     from ferry_amd._lib import last_error, lib
     L = lib()
-    assert L.ferry_abi_version() == 3
+    assert L.ferry_abi_version() == 4
     # argument validation fails before any device work
     assert L.ferry_router_topk(None, 0, 4, 300, 8, 1, 1.0, 1, None, None, None, None, None) != 0
     assert 'experts' in last_error()

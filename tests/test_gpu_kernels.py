@@ -664,6 +664,7 @@ def test_h2d_packed_pool_fetch_byte_exact(device, kind):
     eng.use_packed(None)
     assert eng.engine == mode          # the raw pool serves either kind
     eng.fetch([0, 1], [3, 5])
+    assert eng.groups() == [2]         # raw rows: one group
     eng.wait_host([0, 1])
     assert torch.equal(bits(cache.cpu()[[0, 1]]), bits(pool[[3, 5]]))
     other = pool.clone().pin_memory()
@@ -712,7 +713,10 @@ def test_h2d_packed_sub_batches_and_ring_reuse(device, defer):
     bits = lambda t: t.view(torch.int16)   # noqa: E731
     keys = np.array([0, 6, 1, 2, 11, 3, 4, 5, 7, 8, 9, 10])
     eng.fetch(np.arange(12), keys)
+    ends = eng.groups()    # the call's sub-batches, as positions in its slot list
+    assert len(ends) > 1 and ends[-1] == 12 and ends == sorted(set(ends)), ends
     eng.fetch([12, 13, 12], [13, 14, 15])      # back to back; slot 12 twice: row 15 wins
+    assert eng.groups()[-1] == 3 and len(eng.groups()) >= 2   # the repeat starts a sub-batch
     eng.wait_host(np.arange(cap))
     want = pool[np.concatenate([keys, [15, 14]])]
     assert torch.equal(bits(cache.cpu()), bits(want))
