@@ -13,9 +13,9 @@ Per MoE layer call (world = 1):
      experts already resident run; the compute stream then waits on the GPU for the copies and
      runs the fetched experts.  A prefill-sized call copies its misses in a few groups,
      heaviest expert first, each computed as soon as its copies land, so that only the
-     lightest group's compute is left after the last copy; a decode-sized call with packed
-     rows computes its misses sub-batch by sub-batch as the engine unpacks them.  ``overlap=False`` restores the
-     reference's serial host wait.  ``copy='kernel'`` (not the reference's scheme) copies a
+     lightest group's compute is left after the last copy; a decode-sized call runs all its
+     misses in one launch after the last copy.  ``overlap=False`` restores the reference's
+     serial host wait.  ``copy='kernel'`` (not the reference's scheme) copies a
      decode-sized call's misses with one copy-kernel launch on the compute stream instead and
      then runs every active expert in one FFN launch: no idle link between copies and no
      cross-queue wait, but no overlap either (the copy kernel's host reads slow the HBM-bound
@@ -42,8 +42,9 @@ from .transport import Transport
 
 # A layer call with at least this many (token, expert) pairs fetches its misses in up to CHUNKS
 # groups, heaviest first, and computes each group as soon as its copies land.  Decode calls
-# (few pairs, little compute per expert) are fetched in one call; with packed rows the engine
-# unpacks that call in sub-batches, and each sub-batch's experts run as soon as it is unpacked.
+# (few pairs, little compute per expert) keep one group and one launch for their misses: with
+# packed rows, one launch per unpacked sub-batch (or one for all but the last) shortens the
+# step by about 1 % but adds a launch's fixed cost of GPU time for each.
 CHUNK_MIN_PAIRS = 16384
 CHUNKS = 6
 
@@ -274,13 +275,6 @@ class OffloadRuntime:
         if queue_here and len(fetches):
             for g in groups:
                 self.h2d.fetch(fetches[g, 2], fetches[g, 1])
-        if not chunked and not on_stream and self.packed is not None and len(fetches) > 1:
-            # a packed call's sub-batches are unpacked one by one while the lanes copy the rest:
-            # each sub-batch's experts run as soon as it is unpacked, so only the last one's
-            # follow the call's last copy
-            ends = self.h2d.groups()
-            if len(ends) > 1:
-                groups = [np.arange(a, b) for a, b in zip([0] + ends[:-1], ends)]
         t_fetch = time.perf_counter_ns()
         self.fetches_per_rank += counts
         if self.event >= spec.layers:
