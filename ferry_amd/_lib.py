@@ -28,7 +28,7 @@ SIGNATURES = [
      [_c_p, _c_p, _i64, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p]),
     ('ferry_expert_ffn', ctypes.c_int,
      [_c_p, _i64, _i64, _i64, _c_p, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _i32, _c_p, _i64,
-      _i64, _i64, _c_p, _c_p, _i32, _i32, _c_p]),
+      _i64, _i64, _c_p, _c_p, _c_p, _i32, _i32, _c_p]),
     ('ferry_expert_ffn_sync_timeouts', ctypes.c_int, [_c_p]),
     ('ferry_expert_ffn_set_sync_spin_limit', ctypes.c_int, [_i64]),
     ('ferry_combine', ctypes.c_int, [_c_p, _c_p, _i64, _i64, _i64, _c_p, _c_p]),

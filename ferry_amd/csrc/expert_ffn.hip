@@ -30,8 +30,10 @@
 #include "common.h"
 
 #include <atomic>
+#include <cstdint>
 #include <mutex>
 #include <type_traits>
+#include <vector>
 
 namespace ferry {
 namespace {
@@ -46,6 +48,7 @@ constexpr int kSkinnyMax = 64;  // rows handled by the skinny and mid kernels (4
 
 struct ExpertList {
   int32_t n;
+  int32_t n_mid;   // small-expert up launch: the first n_mid entries take 64-column workgroups
   int16_t expert[kListMax];
   int32_t slot[kListMax];
 };
@@ -933,46 +936,63 @@ __device__ __forceinline__ void ffn_mid_body_t(const FfnArgs& a, int li, int64_t
 // Small experts (at most 64 rows), one launch for a list of mixed sizes so that together they
 // fill the GPU: up to 16 rows the skinny scheme, 17-64 rows the mid scheme.  MTMAX = 1 when no
 // expert of the list has more than 16 rows: then only the skinny scheme is compiled in and a
-// phase-1 workgroup covers 16 intermediate columns (grid (I / 16, list)).  Otherwise every
-// workgroup covers 64 columns, which the skinny experts' workgroups do as four 16-column passes
-// (as a one-tile mid workgroup when H is not a multiple of 256), so that all workgroups stream
-// the same weight bytes (grid (I / 64, list)).  Phase 2: 64 hidden rows per workgroup in both
-// schemes (grid (H / 64, list)).
+// phase-1 workgroup covers 16 intermediate columns (grid (I / 16, list)).  Otherwise the grid
+// is one-dimensional: the list's first n_mid entries (those the host knows to have 17-64 rows)
+// take I / 64 workgroups of 64 columns each, the rest I / 16 workgroups of 16 columns each, so
+// that the larger workgroups are dispatched first.  A workgroup whose expert turns out to have
+// the other scheme's row count still covers its columns: a 64-column workgroup of an expert with
+// at most 16 rows runs four 16-column skinny passes (a one-tile mid workgroup when H is not a
+// multiple of 256); of the four 16-column workgroups of a 64-column block of an expert with more
+// than 16 rows, the first runs the block's mid workgroup and the others return.  Phase 2: 64
+// hidden rows per workgroup in both schemes (grid (H / 64, list)).
 template <int MTMAX>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void ffn_up_skinny(FfnArgs a) {
   // MTMAX = 1: the K-reduction buffer (8 KiB) and four 4 KiB weight tiles
   __shared__ __attribute__((aligned(1024))) char sm[MTMAX > 1 ? kMidLds : 8192 + 4 * 4096];
-  const int li = blockIdx.y;
+  int li = blockIdx.y, bx = blockIdx.x;
+  bool wide = false;   // a 64-column workgroup
+  if (MTMAX > 1) {
+    const int per_mid = (int)(a.I / 64), per_sk = (int)(a.I / 16);
+    const int mid_wgs = a.list.n_mid * per_mid;
+    const int b = blockIdx.x;
+    wide = b < mid_wgs;
+    li = wide ? b / per_mid : a.list.n_mid + (b - mid_wgs) / per_sk;
+    bx = wide ? b % per_mid : (b - mid_wgs) % per_sk;
+  }
   if (li >= a.list.n) return;
   const int e = a.list.expert[li];
   const int64_t start = a.starts[e];
   const int n = (int)(a.starts[e + 1] - start);
   if (n == 0 || n > 16 * MTMAX) return;
-  if (MTMAX == 1) {
+  if (MTMAX == 1 || (!wide && n <= 16)) {
     if (a.H == 2048)
-      up_skinny_p<4>(a, li, start, n, blockIdx.x, reinterpret_cast<floatx4*>(sm),
+      up_skinny_p<4>(a, li, start, n, bx, reinterpret_cast<floatx4*>(sm),
                   sm + 8192 + (threadIdx.x >> 6) * 4096);
     else if (a.H % 256 == 0)
-      up_skinny_t<4>(a, li, start, n, blockIdx.x, reinterpret_cast<floatx4*>(sm),
+      up_skinny_t<4>(a, li, start, n, bx, reinterpret_cast<floatx4*>(sm),
                      sm + 8192 + (threadIdx.x >> 6) * 4096);
     else
-      up_skinny<1, 1, 1>(a, li, start, n, blockIdx.x, reinterpret_cast<floatx4*>(sm));
+      up_skinny<1, 1, 1>(a, li, start, n, bx, reinterpret_cast<floatx4*>(sm));
     return;
   }
   if constexpr (MTMAX > 1) {
+    if (!wide) {   // 16-column workgroup of an expert with more than 16 rows
+      if (bx % 4 != 0) return;
+      bx /= 4;
+    }
     if (n > 32) {
-      ffn_mid_body_t<0, 4>(a, li, start, n, blockIdx.x, sm);
+      ffn_mid_body_t<0, 4>(a, li, start, n, bx, sm);
     } else if (n > 16) {
-      ffn_mid_body_t<0, 2>(a, li, start, n, blockIdx.x, sm);
+      ffn_mid_body_t<0, 2>(a, li, start, n, bx, sm);
     } else if (a.H % 256 == 0) {
 #pragma unroll 1
       for (int j = 0; j < 4; ++j) {
-        up_skinny_t<2>(a, li, start, n, blockIdx.x * 4 + j, reinterpret_cast<floatx4*>(sm),
+        up_skinny_t<2>(a, li, start, n, bx * 4 + j, reinterpret_cast<floatx4*>(sm),
                        sm + 8192 + (threadIdx.x >> 6) * 4096);
         __syncthreads();   // the K-reduction buffer is free again
       }
     } else {
-      ffn_mid_body_t<0, 1>(a, li, start, n, blockIdx.x, sm);
+      ffn_mid_body_t<0, 1>(a, li, start, n, bx, sm);
     }
   }
 }
@@ -1527,13 +1547,18 @@ int ffn_timeouts_address(int32_t** timeouts) {
 
 using namespace ferry;
 
+static int ffn_launch_list(FfnArgs& args, const int32_t* expert_list, const int32_t* slot_of,
+                           int32_t n_list, int32_t n_mid, int64_t maxn, int64_t min_rows,
+                           int64_t pairs, int32_t phases, int64_t hidden, int64_t inter,
+                           hipStream_t s);
+
 extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t hidden,
                                 int64_t inter, const void* x, int64_t rows_in, int64_t topk,
                                 const void* w_sorted, const int64_t* starts, const int64_t* rows,
                                 const int64_t* cols, const int32_t* expert_list, int32_t n_list,
                                 const int32_t* slot_of, int64_t experts,
                                 int64_t max_rows_per_expert, int64_t min_rows_per_expert,
-                                void* act, void* out,
+                                const int32_t* list_rows, void* act, void* out,
                                 int32_t out_mode, int32_t phases, void* stream) {
   clear_error();
   FERRY_CHECK_ARG(phases >= 1 && phases <= 3, "phases must be 1 (up), 2 (down) or 3 (both)");
@@ -1567,6 +1592,10 @@ extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t h
     FERRY_CHECK_ARG(e >= 0 && e < experts, "expert_list[%d] = %d out of range", i, e);
     const int32_t s = slot_of[e];
     FERRY_CHECK_ARG(s >= 0 && s < cache_rows, "expert %d is not cached (slot %d)", e, s);
+    if (list_rows)
+      FERRY_CHECK_ARG(list_rows[i] >= min_rows_per_expert && list_rows[i] <= max_rows_per_expert,
+                      "list_rows[%d] = %d outside [min_rows_per_expert, max_rows_per_expert]", i,
+                      list_rows[i]);
   }
   if (g_num_cus == 0) {
     int dev = 0, cus = 0;
@@ -1590,13 +1619,55 @@ extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t h
   args.out_mode = out_mode;
   // max_rows_per_expert must bound every n_e from above (rows_in does for a layout from
   // ferry_layout) and min_rows_per_expert from below (0 when unknown); the kernels size their
-  // work from the device starts, the bounds only select and gate the launches
-  const int64_t maxn = max_rows_per_expert;
-  const bool any_small = min_rows_per_expert <= kSkinnyMax;
-  const int64_t pairs = rows_in * topk;
+  // work from the device starts, the bounds only select and gate the launches.  With the
+  // entries' row counts (list_rows) the list is issued as two lists with exact bounds: the
+  // small experts (1-64 rows; those with 17-64 rows first) and the tiled ones; experts without
+  // rows are left out.
+  if (!list_rows)
+    return ffn_launch_list(args, expert_list, slot_of, n_list, n_list, max_rows_per_expert,
+                           min_rows_per_expert, rows_in * topk, phases, hidden, inter, s);
+  std::vector<int32_t> small, big;
+  int32_t n_mid = 0;
+  int64_t small_max = 0, small_min = kSkinnyMax, big_max = 0, big_min = INT64_MAX;
+  for (int pass = 0; pass < 2; ++pass)   // 17-64 rows, then 1-16 rows
+    for (int32_t i = 0; i < n_list; ++i) {
+      const int64_t r = list_rows[i];
+      if (r > 16 && r <= kSkinnyMax && pass == 0) small.push_back(expert_list[i]), ++n_mid;
+      if (r >= 1 && r <= 16 && pass == 1) small.push_back(expert_list[i]);
+      if (r >= 1 && r <= kSkinnyMax && pass == 0) {
+        small_max = r > small_max ? r : small_max;
+        small_min = r < small_min ? r : small_min;
+      }
+      if (r > kSkinnyMax && pass == 0) {
+        big.push_back(expert_list[i]);
+        big_max = r > big_max ? r : big_max;
+        big_min = r < big_min ? r : big_min;
+      }
+    }
+  if (!small.empty()) {
+    const int rc = ffn_launch_list(args, small.data(), slot_of, (int32_t)small.size(), n_mid,
+                                   small_max, small_min, rows_in * topk, phases, hidden, inter, s);
+    if (rc != 0) return rc;
+  }
+  if (!big.empty())
+    return ffn_launch_list(args, big.data(), slot_of, (int32_t)big.size(), 0, big_max, big_min,
+                           rows_in * topk, phases, hidden, inter, s);
+  return 0;
+}
+
+// The launches of one list: n_mid of its leading entries are known to hold 17-64 rows (the
+// small-expert up launch gives them 64-column workgroups; the others get 16-column ones unless
+// the bounds allow no expert of more than 16 rows, n_mid = n_list when unknown).
+static int ffn_launch_list(FfnArgs& args, const int32_t* expert_list, const int32_t* slot_of,
+                           int32_t n_list, int32_t n_mid, int64_t maxn, int64_t min_rows,
+                           int64_t pairs, int32_t phases, int64_t hidden, int64_t inter,
+                           hipStream_t s) {
+  const bool any_small = min_rows <= kSkinnyMax;
   for (int32_t off = 0; off < n_list; off += kListMax) {
     const int32_t cnt = (n_list - off) < kListMax ? (n_list - off) : kListMax;
     args.list.n = cnt;
+    const int32_t mid_left = n_mid - off;
+    args.list.n_mid = mid_left < 0 ? 0 : (mid_left < cnt ? mid_left : cnt);
     for (int32_t i = 0; i < kListMax; ++i) {
       args.list.expert[i] = (int16_t)(i < cnt ? expert_list[off + i] : 0);
       args.list.slot[i] = i < cnt ? slot_of[expert_list[off + i]] : 0;
@@ -1628,11 +1699,11 @@ extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t h
       // 16 intermediate columns per workgroup, K split over the four wavefronts
       if (any_small) {
         const dim3 g1((unsigned)(inter / 16), cnt);
+        const int64_t wgs = args.list.n_mid * (inter / 64) + (cnt - args.list.n_mid) * (inter / 16);
         if (maxn <= 16)
           launch("ffn_up_skinny", ffn_up_skinny<1>, g1, dim3(256), 0, s, args);
         else
-          launch("ffn_up_skinny", ffn_up_skinny<4>, dim3((unsigned)(inter / 64), cnt), dim3(256), 0,
-                 s, args);
+          launch("ffn_up_skinny", ffn_up_skinny<4>, dim3((unsigned)wgs), dim3(256), 0, s, args);
         FERRY_LAUNCHED("ffn_up_skinny");
       }
       if (any_big) {

@@ -167,9 +167,9 @@ def expert_ffn(cache, x, w_sorted, starts, rows, cols, expert_list, slot_of, hid
 
     phases: PHASE_UP (gate/up + SwiGLU into ``act``), PHASE_DOWN (down + routing weight from
     ``act`` into ``out``) or PHASE_BOTH.  ``counts`` (optional, host, indexed by expert) holds
-    the row count of every expert, ``starts[e+1] - starts[e]``: the experts are then issued in
-    two calls, those with at most 64 rows (small-expert kernels) and the larger ones (tiled kernels),
-    each with exact row bounds, and experts without rows are skipped.
+    the row count of every expert, ``starts[e+1] - starts[e]``: the library then issues the
+    experts with at most 64 rows (small-expert kernels, 17-64 rows first) and the larger ones
+    (tiled kernels) as separate launches with exact row bounds, and skips experts without rows.
     """
     R, k = w_sorted.shape
     el = np.ascontiguousarray(expert_list, dtype=np.int32)
@@ -182,17 +182,16 @@ def expert_ffn(cache, x, w_sorted, starts, rows, cols, expert_list, slot_of, hid
     tail = (_dev(act, 'act', torch.bfloat16), _dev(out, 'out', torch.bfloat16), int(out_mode),
             int(phases), current_stream(x.device))
 
-    def call(sub, hi, lo):
-        check(lib().ferry_expert_ffn(*args, sub.ctypes.data, len(sub), so.ctypes.data, E, hi, lo,
-                                     *tail), 'expert_ffn')
-
     if counts is None:
-        call(el, int(max_rows if max_rows is not None else R), 0)
+        check(lib().ferry_expert_ffn(*args, el.ctypes.data, len(el), so.ctypes.data, E,
+                                     int(max_rows if max_rows is not None else R), 0, None, *tail),
+              'expert_ffn')
         return out
-    c = np.asarray(counts, dtype=np.int64)[el]
-    for part in ((c > 0) & (c <= SKINNY_MAX_ROWS), c > SKINNY_MAX_ROWS):
-        if part.any():
-            call(np.ascontiguousarray(el[part]), int(c[part].max()), int(c[part].min()))
+    c = np.ascontiguousarray(np.asarray(counts, dtype=np.int64)[el], dtype=np.int32)
+    if len(c):
+        check(lib().ferry_expert_ffn(*args, el.ctypes.data, len(el), so.ctypes.data, E,
+                                     int(c.max()), int(c.min()), c.ctypes.data, *tail),
+              'expert_ffn')
     return out
 
 

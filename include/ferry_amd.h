@@ -115,9 +115,15 @@ int ferry_layout_noalloc(const int64_t* selected, const void* weights_bf16, int6
  * the combine input); out_mode 1 writes row p of out (grouped order).
  * max_rows_per_expert must bound every n_e from above (R does for a layout from ferry_layout),
  * min_rows_per_expert from below (0 when unknown).  Experts with at most 64 rows run the
- * bandwidth-bound small-expert kernels (one launch per phase; their workgroups cover 64 columns
- * when max_rows_per_expert > 16, 16 otherwise), larger ones the tiled MFMA kernels; a launch is
- * skipped when the bounds show that no listed expert needs it (e.g. min_rows_per_expert > 64).
+ * bandwidth-bound small-expert kernels (one launch per phase; their gate/up workgroups cover
+ * 64 columns when max_rows_per_expert > 16, 16 otherwise), larger ones the tiled MFMA kernels;
+ * a launch is skipped when the bounds show that no listed expert needs it (e.g.
+ * min_rows_per_expert > 64).  list_rows (host, nullable) gives each list entry's row count,
+ * n_e of expert_list[i], each within the two bounds: the call then issues the experts with
+ * 1-64 rows and the larger ones as separate launches with exact bounds, skips experts without
+ * rows, and gives the small experts' gate/up launch 64-column workgroups for the experts with
+ * 17-64 rows (dispatched first) and 16-column ones for the others.  The outputs are the same
+ * with and without it (row counts that differ from the layout's only cost speed).
  * phases: 1 = gate/up projection + SwiGLU (writes act), 2 = down projection + routing weight
  * (reads act, writes out), 3 = both.  An expert's cache row (3 * H * I bf16) must be smaller
  * than 4 GiB.
@@ -142,8 +148,8 @@ int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t hidden, int6
                      const int64_t* starts, const int64_t* rows, const int64_t* cols,
                      const int32_t* expert_list, int32_t n_list, const int32_t* slot_of,
                      int64_t experts, int64_t max_rows_per_expert,
-                     int64_t min_rows_per_expert, void* act, void* out, int32_t out_mode,
-                     int32_t phases, void* stream);
+                     int64_t min_rows_per_expert, const int32_t* list_rows, void* act, void* out,
+                     int32_t out_mode, int32_t phases, void* stream);
 int ferry_expert_ffn_sync_timeouts(int64_t* count);
 int ferry_expert_ffn_set_sync_spin_limit(int64_t limit);
 

@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_errors():
     from ferry_amd._lib import last_error, lib
     L = lib()
-    assert L.ferry_abi_version() == 4
+    assert L.ferry_abi_version() == 5
     # argument validation fails before any device work
     assert L.ferry_router_topk(None, 0, 4, 300, 8, 1, 1.0, 1, None, None, None, None, None) != 0
     assert 'experts' in last_error()
@@ -43,18 +43,18 @@ def test_abi_version_and_errors():
     assert L.ferry_combine(None, None, 1, 1, 12, None, None) != 0
     assert 'hidden' in last_error()
     assert L.ferry_expert_ffn(None, 1, 100, 128, None, 1, 1, None, None, None, None, None, 0, None,
-                              1, 1, 0, None, None, 0, 3, None) != 0
+                              1, 1, 0, None, None, None, 0, 3, None) != 0
     # the tiled down projection needs hidden % 256 == 0 once an expert exceeds the skinny size
     assert L.ferry_expert_ffn(None, 1, 384, 128, None, 100, 1, None, None, None, None, None, 1, None,
-                              1, 100, 0, None, None, 0, 3, None) != 0
+                              1, 100, 0, None, None, None, 0, 3, None) != 0
     assert 'multiple of 256' in last_error()
     # the lower row bound may not exceed the upper one
     assert L.ferry_expert_ffn(None, 1, 256, 128, None, 100, 1, None, None, None, None, None, 1, None,
-                              1, 10, 11, None, None, 0, 3, None) != 0
+                              1, 10, 11, None, None, None, 0, 3, None) != 0
     assert 'min_rows_per_expert' in last_error()
     # weights are addressed with 32-bit offsets inside an expert's cache row
     assert L.ferry_expert_ffn(None, 1, 65536, 32768, None, 100, 1, None, None, None, None, None,
-                              1, None, 1, 10, 0, None, None, 0, 3, None) != 0
+                              1, None, 1, 10, 0, None, None, None, 0, 3, None) != 0
     assert '4 GiB' in last_error()
     assert L.ferry_combine_add(None, None, 4, 2, 64, None, None, None) != 0
     assert 'addend' in last_error()
