@@ -450,6 +450,14 @@ __device__ __forceinline__ void down_skinny_t(const FfnArgs& a, int li, int64_t 
     }
   const bool oka = r16 < n;
   const bf16_t* pa = a.act + (start + (oka ? r16 : 0)) * a.I + kg;
+  // the token and slot index of the expert's row lane % 16, loaded ahead of the weights by the
+  // wavefront that writes the output (the epilogue takes them from that lane by a shuffle)
+  int32_t row_t = 0, row_j = 0;
+  if (ks == 0) {
+    const int64_t p = start + (r16 < n ? r16 : 0);
+    row_t = (int32_t)a.rows[p];
+    row_j = (int32_t)a.cols[p];
+  }
   floatx4 acc[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) acc[c] = floatx4{0, 0, 0, 0};
@@ -485,15 +493,22 @@ __device__ __forceinline__ void down_skinny_t(const FfnArgs& a, int li, int64_t 
   for (; k0 + 64 * NCH <= ke; k0 += 64 * NCH) batch(k0, std::integral_constant<int, NCH>{});
   for (; k0 < ke; k0 += 64) batch(k0, std::integral_constant<int, 1>{});
   floatx4 accm[1][4] = {{acc[0], acc[1], acc[2], acc[3]}};
+  // the routing weight of each output row, loaded before the K reduction (whose barrier waits
+  // for the other wavefronts)
+  int32_t lane_orow = 0;
+  float lane_wt = 0.0f;
+  if (ks == 0) {
+    const int64_t tj = (int64_t)row_t * a.k + row_j;
+    lane_wt = bf16_to_f32(a.w[tj]);
+    lane_orow = a.out_mode == 0 ? (int32_t)tj : (int32_t)(start + (r16 < n ? r16 : 0));
+  }
   if (!skinny_reduce<4, 1>(accm, ks, 0, lane, red)) return;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int r = (lane >> 4) * 4 + q;
+    const int64_t orow = __shfl(lane_orow, r);
+    const float wt = __shfl(lane_wt, r);
     if (r < n) {
-      const int64_t p = start + r;
-      const int64_t t = a.rows[p], j = a.cols[p];
-      const float wt = bf16_to_f32(a.w[t * a.k + j]);
-      const int64_t orow = a.out_mode == 0 ? t * a.k + j : p;
 #pragma unroll
       for (int c = 0; c < 4; ++c)
         a.out[orow * a.H + h0 + 16 * c + (lane & 15)] = f32_to_bf16(bf16r(accm[0][c][q]) * wt);
@@ -736,6 +751,14 @@ __device__ __forceinline__ void down_skinny_p(const FfnArgs& a, int li, int64_t 
       }
     }
   };
+  // the token and slot index of the expert's row lane % 16, loaded ahead of the weights by the
+  // wavefront that writes the output (the epilogue takes them from that lane by a shuffle)
+  int32_t row_t = 0, row_j = 0;
+  if (ks == 0) {
+    const int64_t p = start + (r16 < n ? r16 : 0);
+    row_t = (int32_t)a.rows[p];
+    row_j = (int32_t)a.cols[p];
+  }
   bf16x8 wA[8], wB[8], xA[2], xB[2];
   load(std::integral_constant<int, 0>{}, wA, xA);
   static_for<0, NC>([&](auto c) {
@@ -755,15 +778,22 @@ __device__ __forceinline__ void down_skinny_p(const FfnArgs& a, int li, int64_t 
     mma(wc, xc);
   });
   floatx4 accm[1][4] = {{acc[0], acc[1], acc[2], acc[3]}};
+  // the routing weight of each output row, loaded before the K reduction (whose barrier waits
+  // for the other wavefronts)
+  int32_t lane_orow = 0;
+  float lane_wt = 0.0f;
+  if (ks == 0) {
+    const int64_t tj = (int64_t)row_t * a.k + row_j;
+    lane_wt = bf16_to_f32(a.w[tj]);
+    lane_orow = a.out_mode == 0 ? (int32_t)tj : (int32_t)(start + (r16 < n ? r16 : 0));
+  }
   if (!skinny_reduce<4, 1>(accm, ks, 0, lane, red)) return;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int r = (lane >> 4) * 4 + q;
+    const int64_t orow = __shfl(lane_orow, r);
+    const float wt = __shfl(lane_wt, r);
     if (r < n) {
-      const int64_t p = start + r;
-      const int64_t t = a.rows[p], j = a.cols[p];
-      const float wt = bf16_to_f32(a.w[t * a.k + j]);
-      const int64_t orow = a.out_mode == 0 ? t * a.k + j : p;
 #pragma unroll
       for (int c = 0; c < 4; ++c)
         a.out[orow * a.H + h0 + 16 * c + (lane & 15)] = f32_to_bf16(bf16r(accm[0][c][q]) * wt);
@@ -892,6 +922,15 @@ __device__ __forceinline__ void ffn_mid_body_t(const FfnArgs& a, int li, int64_t
     // token rows of chunk c+1 landed: older than w(c+2), x(c+2), w(c+3)
     wait_vmcnt<2 * NW + XD>();
   };
+  // phase 2: lane l loads the token and slot index of the expert's row l ahead of the weights,
+  // so that after the K loop only the routing weight's load (which depends on them) is left;
+  // the epilogue takes each row's output offset and weight from its lane by a shuffle
+  int32_t row_t = 0, row_j = 0;
+  if (MODE == 1) {
+    const int64_t p = start + (lane < n ? lane : 0);
+    row_t = (int32_t)a.rows[p];
+    row_j = (int32_t)a.cols[p];
+  }
   // prologue in the steady-state order: w(0), x(0), w(1), x(1), w(2)
   wload(0, wb[0]);
   stage(0);
@@ -912,22 +951,27 @@ __device__ __forceinline__ void ffn_mid_body_t(const FfnArgs& a, int li, int64_t
   vmcnt_tie<0>(wb[2]);
   // 16x16 accumulator layout: column = lane & 15, rows (lane >> 4) * 4 + [0, 4)
   const int col = col0 + (lane & 15);
+  int32_t lane_orow = 0;
+  float lane_wt = 0.0f;
+  if (MODE == 1) {
+    const int64_t tj = (int64_t)row_t * a.k + row_j;
+    lane_wt = bf16_to_f32(a.w[tj]);
+    lane_orow = a.out_mode == 0 ? (int32_t)tj : (int32_t)(start + (lane < n ? lane : 0));
+  }
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int r = mt * 16 + (lane >> 4) * 4 + q;
-      if (r < n) {
-        if (MODE == 0) {
+      if (MODE == 0) {
+        if (r < n) {
           const float g = bf16r(acc[mt][0][q]), u = bf16r(acc[mt][NB - 1][q]);
           a.act[(start + r) * a.I + col] = f32_to_bf16(silu_mul(g, u));
-        } else {
-          const int64_t p = start + r;
-          const int64_t t = a.rows[p], j = a.cols[p];
-          const float wt = bf16_to_f32(a.w[t * a.k + j]);
-          const int64_t orow = a.out_mode == 0 ? t * a.k + j : p;
-          a.out[orow * a.H + col] = f32_to_bf16(bf16r(acc[mt][0][q]) * wt);
         }
+      } else {
+        const int64_t orow = __shfl(lane_orow, r);
+        const float wt = __shfl(lane_wt, r);
+        if (r < n) a.out[orow * a.H + col] = f32_to_bf16(bf16r(acc[mt][0][q]) * wt);
       }
     }
   }
