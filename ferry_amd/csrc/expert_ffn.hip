@@ -1665,8 +1665,9 @@ extern "C" int ferry_expert_ffn(const void* cache, int64_t cache_rows, int64_t h
   // ferry_layout) and min_rows_per_expert from below (0 when unknown); the kernels size their
   // work from the device starts, the bounds only select and gate the launches.  With the
   // entries' row counts (list_rows) the list is issued as two lists with exact bounds: the
-  // small experts (1-64 rows; those with 17-64 rows first) and the tiled ones; experts without
-  // rows are left out.
+  // small experts (1-64 rows; those with 17-64 rows first), then the tiled ones (the small
+  // launches measured slower after the tiled ones, whose output writes they then meet); experts
+  // without rows are left out.
   if (!list_rows)
     return ffn_launch_list(args, expert_list, slot_of, n_list, n_list, max_rows_per_expert,
                            min_rows_per_expert, rows_in * topk, phases, hidden, inter, s);

@@ -118,12 +118,14 @@ int ferry_layout_noalloc(const int64_t* selected, const void* weights_bf16, int6
  * bandwidth-bound small-expert kernels (one launch per phase; their gate/up workgroups cover
  * 64 columns when max_rows_per_expert > 16, 16 otherwise), larger ones the tiled MFMA kernels;
  * a launch is skipped when the bounds show that no listed expert needs it (e.g.
- * min_rows_per_expert > 64).  list_rows (host, nullable) gives each list entry's row count,
- * n_e of expert_list[i], each within the two bounds: the call then issues the experts with
- * 1-64 rows and the larger ones as separate launches with exact bounds, skips experts without
- * rows, and gives the small experts' gate/up launch 64-column workgroups for the experts with
- * 17-64 rows (dispatched first) and 16-column ones for the others.  The outputs are the same
- * with and without it (row counts that differ from the layout's only cost speed).
+ * min_rows_per_expert > 64).  list_rows (host, nullable) gives each list entry's row count:
+ * list_rows[i] must equal n_e of expert_list[i] (within the two bounds).  The call then issues
+ * the experts with 1-64 rows and then those with more as separate launches with exact bounds,
+ * skips experts without rows, and gives the small experts' gate/up launch 64-column
+ * workgroups for the experts with 17-64 rows (dispatched first) and 16-column ones for the
+ * others.  The outputs are bit-identical to those of the same call without it; like the
+ * bounds, the counts decide which launches run, so an entry below its expert's row count can
+ * leave that expert uncomputed.
  * phases: 1 = gate/up projection + SwiGLU (writes act), 2 = down projection + routing weight
  * (reads act, writes out), 3 = both.  An expert's cache row (3 * H * I bf16) must be smaller
  * than 4 GiB.

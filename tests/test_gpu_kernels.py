@@ -330,6 +330,50 @@ def test_small_expert_kernels_vs_oracle(device, H, I, counts, split):
                                    msg=lambda m: f'expert {e} ({c} rows): {m}')
 
 
+@pytest.mark.parametrize('counts', [
+    [200, 1, 5, 16, 17, 31, 33, 64, 0, 90, 3, 40],      # tiled, mid and skinny experts
+    [16, 1, 7, 3, 9, 16, 0, 12],                        # decode sizes: the one-launch kernel
+])
+def test_expert_ffn_list_rows_bit_identical(device, counts):
+    """Row counts given to the library (list_rows: separate tiled and small launches, the small
+    gate/up launch's 16-column workgroups for experts of at most 16 rows) give the same bits as
+    the call without them (one list, 64-column small-expert workgroups).  Counts that put an
+    expert in the other small scheme still give the same bits: a 16-column workgroup of an
+    expert with more rows runs its block's mid workgroup, a 64-column one of an expert with
+    fewer runs four skinny passes."""
+    ops = _ops()
+    H, I, E = 2048, 768, len(counts)
+    rows_w = _pool(E, H, I, seed=sum(counts))
+    g = torch.Generator().manual_seed(E + 5)
+    ids = np.concatenate([np.full(c, e, np.int64) for e, c in enumerate(counts)])
+    ids = ids[np.random.default_rng(E).permutation(len(ids))]
+    T = len(ids)
+    sel = torch.from_numpy(ids).view(T, 1)
+    w = (torch.rand((T, 1), generator=g) + 0.5).to(torch.bfloat16)
+    x = torch.randn((T, H), generator=g).to(torch.bfloat16).to(device)
+    lay = ops.layout(sel.to(device), w.to(device), E)
+    cache = rows_w.to(device)
+    slot_of = np.arange(E, dtype=np.int32)
+    variants = {'no_rows': None, 'rows': np.array(counts)}
+    if max(counts) > 16:
+        swapped = np.array(counts)
+        swapped[counts.index(17)] = 9     # a mid expert given a skinny count
+        swapped[counts.index(5)] = 20     # a skinny expert given a mid count
+        variants['swapped_schemes'] = swapped
+    outs = {}
+    for name, c in variants.items():
+        act = torch.full((T, I), float('nan'), dtype=torch.bfloat16, device=device)
+        part = torch.full((T, H), float('nan'), dtype=torch.bfloat16, device=device)
+        ops.expert_ffn(cache, x, lay.w_sorted, lay.starts, lay.rows, lay.cols, np.arange(E),
+                       slot_of, H, I, act, part, out_mode=0, max_rows=T, counts=c)
+        torch.cuda.synchronize()
+        outs[name] = (act.cpu(), part.cpu())
+    assert not torch.isnan(outs['no_rows'][1].float()).any()
+    for name in variants:
+        assert torch.equal(outs[name][0].view(torch.int16), outs['no_rows'][0].view(torch.int16)), name
+        assert torch.equal(outs[name][1].view(torch.int16), outs['no_rows'][1].view(torch.int16)), name
+
+
 @pytest.mark.parametrize('nbytes', [16, 4096 + 16, 3 * 32768 + 48, 5_000_000 // 16 * 16])
 def test_hbm_read_xor(device, nbytes):
     """The read-ceiling kernel reads every 16-byte word once: its per-lane XOR equals numpy's."""
