@@ -320,8 +320,9 @@ def run_prefill(args, device, w):
         wts, sel = ops.router_topk(logits, k, renorm=w.renorm, sorted=w.sorted)
         lay = ops.layout(sel, wts, E)
         # the per-expert row counts on the host, as the runtime has them from the routing it
-        # reads back for its planner (one device sync per layer call)
-        rows_e = torch.bincount(sel.reshape(-1), minlength=E).cpu().numpy()
+        # reads back for its planner (one device sync per layer call): here from the layout's
+        # expert starts
+        rows_e = np.diff(lay.starts.cpu().numpy())
         ops.expert_ffn(cache, x, lay.w_sorted, lay.starts, lay.rows, lay.cols, np.arange(E), slot_of,
                        H, I, act, part, counts=rows_e)
         add = shared(x, out=shared_out) if shared is not None else None
