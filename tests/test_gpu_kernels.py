@@ -330,11 +330,23 @@ def test_small_expert_kernels_vs_oracle(device, H, I, counts, split):
                                    msg=lambda m: f'expert {e} ({c} rows): {m}')
 
 
-@pytest.mark.parametrize('counts', [
-    [200, 1, 5, 16, 17, 31, 33, 64, 0, 90, 3, 40],      # tiled, mid and skinny experts
-    [16, 1, 7, 3, 9, 16, 0, 12],                        # decode sizes: the one-launch kernel
+def _list_rows_counts_400():
+    # 400 experts: the small ones fill more than one launch's list of 256, and the 17-64-row
+    # experts (issued first) outnumber it, so the split falls among them
+    c = np.random.default_rng(400).integers(10, 41, 400)
+    c[::20] = 70     # tiled
+    c[5] = 17
+    c[11] = 5
+    c[13] = 0
+    return [int(v) for v in c]
+
+
+@pytest.mark.parametrize('counts,H,I', [
+    ([200, 1, 5, 16, 17, 31, 33, 64, 0, 90, 3, 40], 2048, 768),   # tiled, mid and skinny
+    ([16, 1, 7, 3, 9, 16, 0, 12], 2048, 768),       # decode sizes: the one-launch kernel
+    (_list_rows_counts_400(), 256, 128),            # a list split over two launches
 ])
-def test_expert_ffn_list_rows_bit_identical(device, counts):
+def test_expert_ffn_list_rows_bit_identical(device, counts, H, I):
     """Row counts given to the library (list_rows: separate tiled and small launches, the small
     gate/up launch's 16-column workgroups for experts of at most 16 rows) give the same bits as
     the call without them (one list, 64-column small-expert workgroups).  Counts that put an
@@ -342,7 +354,7 @@ def test_expert_ffn_list_rows_bit_identical(device, counts):
     expert with more rows runs its block's mid workgroup, a 64-column one of an expert with
     fewer runs four skinny passes."""
     ops = _ops()
-    H, I, E = 2048, 768, len(counts)
+    E = len(counts)
     rows_w = _pool(E, H, I, seed=sum(counts))
     g = torch.Generator().manual_seed(E + 5)
     ids = np.concatenate([np.full(c, e, np.int64) for e, c in enumerate(counts)])
