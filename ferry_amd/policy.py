@@ -113,10 +113,12 @@ class Controller:
         if self._fetch_buf is None:
             self._fetch_buf = np.empty((experts, 3), np.int64)
             self.demand = np.zeros(experts, np.int64)
+            self._fetch_ptrs = (self._fetch_buf.ctypes.data, self.demand.ctypes.data,
+                                int(self.capacities[0]))
+        fetch_ptr, demand_ptr, cap = self._fetch_ptrs
         m = lib().ferry_plan_fetch(event, layer, ids_ptr, tokens, topk, scores_ptr,
-                                   self._slots_ptr, int(self.capacities[0]), self._owner_ptr,
-                                   self._last_ptr, self._scores_ptr, experts,
-                                   self._fetch_buf.ctypes.data, None, self.demand.ctypes.data,
+                                   self._slots_ptr, cap, self._owner_ptr, self._last_ptr,
+                                   self._scores_ptr, experts, fetch_ptr, None, demand_ptr,
                                    h2d_handle)
         if m == -1:
             raise AssertionError(last_error())
