@@ -56,6 +56,16 @@ def test_abi_version_and_errors():
     assert L.ferry_expert_ffn(None, 1, 65536, 32768, None, 100, 1, None, None, None, None, None,
                               1, None, 1, 10, 0, None, None, None, 0, 3, None) != 0
     assert '4 GiB' in last_error()
+    # row counts must lie within the row bounds (checked on the host before any device work;
+    # the pointers are placeholders that are never dereferenced)
+    import numpy as np
+    el, so = np.arange(3, dtype=np.int32), np.arange(3, dtype=np.int32)
+    rows = np.array([5, 70, 2], dtype=np.int32)
+    fake = 4096
+    assert L.ferry_expert_ffn(fake, 3, 256, 128, fake, 100, 1, fake, fake, fake, fake,
+                              el.ctypes.data, 3, so.ctypes.data, 3, 64, 0, rows.ctypes.data,
+                              fake, fake, 0, 3, None) != 0
+    assert 'list_rows[1] = 70' in last_error()
     assert L.ferry_combine_add(None, None, 4, 2, 64, None, None, None) != 0
     assert 'addend' in last_error()
 
