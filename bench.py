@@ -37,6 +37,9 @@ Also on the line:
     False), the reference's transfer format);
   * decode_copy_kernel: the headline stream through OffloadRuntime(copy='kernel'): raw misses
     copied by one kernel launch on the compute stream, then one FFN launch (no overlap);
+  * reference_pattern_gpu: the reference's own per-expert torch op order for the expert FFN
+    and the combine (hipBLASLt GEMMs) timed on this GPU beside this library's launches, on the
+    Qwen3 prefill layer and one decode step, every expert resident;
   * cpu_baseline: the reference's op order in torch on the host cores (all cores of the
     process's affinity), median of >= 5 repeats on the decode stream, plus one Qwen3 8192-token
     prefill layer with the 48-layer extrapolation.
@@ -401,6 +404,92 @@ def run_prefill(args, device, w):
                 tiled_up_avg_us=tu['avg_us'], small_reads_after_layer=reads_after_layer,
                 kernel_ms={n: per(n) for n in kern},
                 kernel_avg_launch_us={n: v['avg_us'] for n, v in kern.items()})
+
+
+def reference_pattern_gpu(device, reps=5):
+    """The reference's own GPU op order for the expert FFN and the combine, restated in torch and
+    timed on this GPU beside this library's kernels on the same inputs: per expert (ascending
+    IDs) an index_select of its token rows, the gate and up GEMMs, fp32 silu(g) * u rounded to
+    bf16, the down GEMM and the routing-weight product (execute_experts, expert_ops.cpp:13-45),
+    then the fp32 index_add over the experts in ascending order and one bf16 rounding
+    (reduce_partials, expert_ops.cpp:75-92).  GEMMs are torch's (hipBLASLt), with the weights
+    read in place from the cache rows as the reference does.  Two workloads, every expert
+    resident: the Qwen3 8192-token prefill layer and one 16-token step of the decode stream.
+    Timed: FFN + combine, HIP events around the whole call, median of ``reps``; the router and
+    layout are outside both timings.  ``max_abs_diff``: the two outputs' largest difference."""
+    import torch.nn.functional as F
+
+    from ferry_amd import expert_ops as ops
+    from ferry_amd import workloads
+    out = {}
+    cases = (('qwen3_prefill_t8192', workloads.QWEN3_PREFILL_STACK),
+             ('qwen3_decode_t16', workloads.QWEN3_DECODE_LAYER))
+    for name, w in cases:
+        spec = w.spec
+        E, k, H, I = spec.experts, spec.topk, spec.hidden, spec.intermediate
+        if w is workloads.QWEN3_DECODE_LAYER:
+            logits, x = decode_stream(w, 1, device)[0]
+        else:
+            logits = workloads.RouterLogits(replace(w, layers=1), device).next(0, w.tokens)
+            x = workloads.hidden_states(w.tokens, H, seed=w.seed + 7, device=device)
+        T = x.shape[0]
+        cache = workloads.expert_rows(range(E), spec.expert_elements, seed=w.seed, device=device)
+        wts, sel = ops.router_topk(logits, k, renorm=w.renorm, sorted=w.sorted)
+        lay = ops.layout(sel, wts, E)
+        starts = lay.starts.cpu().numpy()
+        counts = np.diff(starts)
+        active = np.flatnonzero(counts)
+        act = torch.empty((T * k, I), dtype=torch.bfloat16, device=device)
+        part = torch.empty((T * k, H), dtype=torch.bfloat16, device=device)
+        slot_of = np.arange(E, dtype=np.int32)
+        groups = [(e, lay.rows[starts[e]:starts[e + 1]], lay.cols[starts[e]:starts[e + 1]])
+                  for e in active]
+        # the routing weights in each token's sorted-ID order: (rows, cols) index them
+        w_sorted = lay.w_sorted.view(T, k)
+
+        def ours():
+            ops.expert_ffn(cache, x, lay.w_sorted, lay.starts, lay.rows, lay.cols, active,
+                           slot_of, H, I, act, part, counts=counts)
+            return ops.combine(part, T, k, H)
+
+        def reference():
+            acc = torch.zeros((T, H), dtype=torch.float32, device=device)
+            for e, rows, cols in groups:
+                row = cache[e]
+                gate = row[:I * H].view(I, H)
+                up = row[I * H:2 * I * H].view(I, H)
+                down = row[2 * I * H:].view(H, I)
+                xe = x.index_select(0, rows)
+                a = (F.silu(F.linear(xe, gate).float()) * F.linear(xe, up).float()).to(torch.bfloat16)
+                y = F.linear(a, down) * w_sorted[rows, cols].unsqueeze(1)
+                acc.index_add_(0, rows, y.float())
+            return acc.to(torch.bfloat16)
+
+        res = {}
+        outs = {}
+        for label, fn in (('ours', ours), ('reference_pattern', reference)):
+            outs[label] = fn()
+            torch.cuda.synchronize()
+            ts = []
+            for _ in range(reps):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                fn()
+                e1.record()
+                e1.synchronize()
+                ts.append(e0.elapsed_time(e1))
+            res[label + '_ms'] = float(np.median(ts))
+        res.update(tokens=T, active_experts=int(len(active)),
+                   speedup=res['reference_pattern_ms'] / res['ours_ms'],
+                   max_abs_diff=float((outs['ours'].float() - outs['reference_pattern'].float())
+                                      .abs().max()))
+        out[name] = res
+        del cache, act, part, outs
+        torch.cuda.empty_cache()
+    out['note'] = ('the reference\'s per-expert torch op order on this GPU (hipBLASLt GEMMs, one '
+                   'host launch sequence per expert) against this library\'s launches, same '
+                   'inputs, FFN + combine only')
+    return out
 
 
 def gemm_ceiling(device):
@@ -969,6 +1058,7 @@ def main():
         line['prefill_deepseek'] = run_prefill(args, device, workloads.DEEPSEEK_PREFILL_STACK)
         line['gemm_ceiling_hipblaslt'] = gemm_ceiling(device)
         line['tiled_dense'] = tiled_dense(device)
+        line['reference_pattern_gpu'] = reference_pattern_gpu(device)
         for key, shape in (('up_65536x1536x2048', 'dense_up_65536x1536x2048'),
                            ('down_65536x2048x768', 'dense_down_65536x2048x768')):
             line['tiled_dense'][key]['vs_hipblaslt'] = (
