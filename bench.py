@@ -35,6 +35,8 @@ Also on the line:
     cache, 200 ms release delay) and metrics, TTFT / TPOT / E2E / TPS as mean and sample std;
   * decode_raw: the headline stream with raw rows over the host link (OffloadRuntime(pack=
     False), the reference's transfer format);
+  * decode_split_fetch: the headline stream with OffloadRuntime(split_fetch=True), each packed
+    call's fetched experts computed sub-batch by sub-batch as they are unpacked;
   * decode_copy_kernel: the headline stream through OffloadRuntime(copy='kernel'): raw misses
     copied by one kernel launch on the compute stream, then one FFN launch (no overlap);
   * reference_pattern_gpu: the reference's own per-expert torch op order for the expert FFN
@@ -184,7 +186,7 @@ def decode_stream(w, steps, device):
     return out
 
 
-def run_decode(args, device, copy='dma', pack=False):
+def run_decode(args, device, copy='dma', pack=False, split_fetch=False):
     from ferry_amd import expert_ops as ops
     from ferry_amd import workloads
     from ferry_amd.quota import Topology
@@ -193,7 +195,7 @@ def run_decode(args, device, copy='dma', pack=False):
     spec = w.spec
     pool = workloads.make_pool(spec, 1, seed=0)
     rt = OffloadRuntime(spec, pool, [w.cache_slots], 'ferry', Topology.uniform(1, spec.experts),
-                        copy=copy, pack=pack)
+                        copy=copy, pack=pack, split_fetch=split_fetch)
     packing = None
     if rt.packed is not None:
         packing = dict(ratio=rt.packed.ratio, packed_rows=rt.packed.packed_rows,
@@ -205,21 +207,10 @@ def run_decode(args, device, copy='dma', pack=False):
         wts, sel = ops.router_topk(lg, spec.topk, renorm=True)
         return rt.execute(0, x, sel, wts, None)
 
-    # pass 1 (the measurement): no instrumentation in the timed region
-    for lg, x in stream[:args.warmup]:
-        step(lg, x)
-    torch.cuda.synchronize()
-    copies0 = rt.h2d.copies
-    t0 = time.perf_counter()
-    for lg, x in stream[args.warmup:]:
-        step(lg, x)
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    rt.h2d.synchronize()
-    copies = rt.h2d.copies - copies0
-    # pass 2: the same stream from an empty cache again, with per-launch kernel timing, fetch
-    # events and host phase timing (same misses, same launches)
-    rt.reset()
+    # pass 1: the stream with per-launch kernel timing, fetch events and host phase timing.
+    # It also brings the HIP runtime's own pools (the queue, signal and argument memory that its
+    # launches, copies and events draw on) to their working size: a process's first few hundred
+    # decode steps run about 3 % slower than the same steps afterwards.
     for lg, x in stream[:args.warmup]:
         step(lg, x)
     torch.cuda.synchronize()
@@ -235,13 +226,30 @@ def run_decode(args, device, copy='dma', pack=False):
              'ffn_down_skinny', 'combine_kernel')
     ks['launch'] = {name: launch_stats(ops, name) for name in names}
     fetch_ms, exposed_ms, overlap_ms = rt.fetch_timing()   # reads the launch log: before disabling
+    critical = rt.critical_path_timing()
+    host_ns = dict(rt.host_ns)
     ops.timing_enable(False)
+    rt.timing = False
+    # pass 2 (the measurement): the same stream from an empty cache again (same misses, same
+    # launches), no instrumentation in the timed region
+    rt.reset()
+    for lg, x in stream[:args.warmup]:
+        step(lg, x)
+    torch.cuda.synchronize()
+    copies0 = rt.h2d.copies
+    t0 = time.perf_counter()
+    for lg, x in stream[args.warmup:]:
+        step(lg, x)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    rt.h2d.synchronize()
+    copies = rt.h2d.copies - copies0
     res = dict(workload=w, elapsed=t1 - t0, instrumented_elapsed=t3 - t2,
-               critical=rt.critical_path_timing(), packing=packing,
+               critical=critical, packing=packing,
                sync_timeouts=ops.ffn_sync_timeouts(),
                tokens=w.tokens * args.steps, copies=copies, kernels=ks, fetch_ms=fetch_ms,
                exposed_ms=exposed_ms, overlap_ms=overlap_ms, expert_bytes=spec.expert_bytes,
-               samples=stream[args.warmup:], host_ns=dict(rt.host_ns))
+               samples=stream[args.warmup:], host_ns=host_ns)
     rt.close()
     del pool
     return res
@@ -1038,6 +1046,22 @@ def main():
         note='copy=kernel: the misses of a step are copied by one kernel launch on the compute '
              'stream, then every active expert runs in one FFN launch (no overlap)')
     print(f'# decode (copy kernel) done: {line["decode_copy_kernel"]["tokens_per_s"]:.0f} tokens/s',
+          file=sys.stderr, flush=True)
+    # the headline stream with each packed call's fetched experts computed sub-batch by
+    # sub-batch as the engine unpacks them (OffloadRuntime(split_fetch=True)): a shorter tail
+    # after the last copy, for more and smaller FFN launches
+    ds = run_decode(args, device, pack=True, split_fetch=True)
+    rs, bs = decode_block(ds, args)
+    line['decode_split_fetch'] = dict(
+        tokens_per_s=ds['tokens'] / ds['elapsed'], ms_per_step=ds['elapsed'] / args.steps * 1e3,
+        ffn_launches=rs['launches'], ffn_avg_launch_us=rs['avg_launch_us'], ffn_gbs=rs['achieved'],
+        ffn_frac=rs['frac'], fetch_hidden_frac=bs['fetch_hidden_frac'],
+        hidden_cap=bs['hidden_cap'], critical_path_us=bs['critical_path_us'],
+        note='OffloadRuntime(pack=True, split_fetch=True): one FFN launch per unpacked '
+             'sub-batch of a call\'s fetched experts instead of one after the last copy; not '
+             'the headline, whose single fetched-expert launch keeps the decode FFN at a '
+             'higher fraction of HBM peak')
+    print(f'# decode (split fetch) done: {line["decode_split_fetch"]["tokens_per_s"]:.0f} tokens/s',
           file=sys.stderr, flush=True)
     # the same decode stream fetching raw rows, as the reference's engine does
     dr = run_decode(args, device, pack=False)

@@ -29,6 +29,7 @@
 #include <cstdint>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <utility>
 #include <vector>
 
@@ -54,12 +55,63 @@ namespace {
 // its copies): none needs a system-scope fence, and leaving it out shortens every wait on them.
 constexpr unsigned kEventFlags = hipEventDisableTiming | hipEventDisableSystemFence;
 
+// Engine events are recycled instead of created and destroyed per record (several per decode
+// step): a HIP event that is destroyed while its record is still pending stays with the
+// runtime until it fires, and a process's first few hundred decode steps ran about 3 % slower
+// than later ones on freshly created events.  A released event goes back to a free list of its
+// device and flags; re-recording it later does not disturb stream waits queued on its earlier
+// record, and no engine state refers to it any more.
+struct EventPool {
+  std::mutex mu;
+  struct Entry {
+    int device;
+    unsigned flags;
+    hipEvent_t e;
+  };
+  std::vector<Entry> free;
+};
+constexpr size_t kEventPoolMax = 4096;
+
+EventPool& event_pool() {
+  static EventPool* pool = new EventPool();   // outlives every engine (never destroyed)
+  return *pool;
+}
+
+hipError_t take_event(int device, unsigned flags, hipEvent_t* out) {
+  {
+    EventPool& p = event_pool();
+    std::lock_guard<std::mutex> lock(p.mu);
+    for (size_t i = p.free.size(); i-- > 0;)
+      if (p.free[i].device == device && p.free[i].flags == flags) {
+        *out = p.free[i].e;
+        p.free[i] = p.free.back();
+        p.free.pop_back();
+        return hipSuccess;
+      }
+  }
+  return hipEventCreateWithFlags(out, flags);
+}
+
+void give_event(int device, unsigned flags, hipEvent_t e) {
+  EventPool& p = event_pool();
+  {
+    std::lock_guard<std::mutex> lock(p.mu);
+    if (p.free.size() < kEventPoolMax) {
+      p.free.push_back({device, flags, e});
+      return;
+    }
+  }
+  (void)hipEventDestroy(e);
+}
+
 struct Event {
   hipEvent_t e = nullptr;
   hipStream_t stream = nullptr;   // the stream it was recorded on
   int64_t order = 0;              // record order among the engine's events
+  int device = 0;
+  unsigned flags = 0;
   ~Event() {
-    if (e) (void)hipEventDestroy(e);
+    if (e) give_event(device, flags, e);
   }
 };
 
@@ -174,8 +226,14 @@ struct ferry_h2d {
 static hipError_t record_event(ferry_h2d* h, hipStream_t s, std::shared_ptr<Event>* out,
                                unsigned flags = kEventFlags) {
   auto ev = std::make_shared<Event>();
-  hipError_t r = hipEventCreateWithFlags(&ev->e, flags);
-  if (r == hipSuccess) r = hipEventRecord(ev->e, s);
+  hipError_t r = take_event(h->device, flags, &ev->e);
+  if (r != hipSuccess) {
+    ev->e = nullptr;
+    return r;
+  }
+  ev->device = h->device;
+  ev->flags = flags;
+  r = hipEventRecord(ev->e, s);
   if (r != hipSuccess) return r;
   ev->stream = s;
   ev->order = ++h->order;

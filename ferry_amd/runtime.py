@@ -14,8 +14,9 @@ Per MoE layer call (world = 1):
      runs the fetched experts.  A prefill-sized call copies its misses in a few groups,
      heaviest expert first, each computed as soon as its copies land, so that only the
      lightest group's compute is left after the last copy; a decode-sized call runs all its
-     misses in one launch after the last copy.  ``overlap=False`` restores the reference's
-     serial host wait.  ``copy='kernel'`` (not the reference's scheme) copies a
+     misses in one launch after the last copy (``split_fetch=True``, with packed rows: one
+     launch per sub-batch as the engine unpacks it).  ``overlap=False`` restores the
+     reference's serial host wait.  ``copy='kernel'`` (not the reference's scheme) copies a
      decode-sized call's misses with one copy-kernel launch on the compute stream instead and
      then runs every active expert in one FFN launch: no idle link between copies and no
      cross-queue wait, but no overlap either (the copy kernel's host reads slow the HBM-bound
@@ -43,8 +44,8 @@ from .transport import Transport
 # A layer call with at least this many (token, expert) pairs fetches its misses in up to CHUNKS
 # groups, heaviest first, and computes each group as soon as its copies land.  Decode calls
 # (few pairs, little compute per expert) keep one group and one launch for their misses: with
-# packed rows, one launch per unpacked sub-batch (or one for all but the last) shortens the
-# step by about 1 % but adds a launch's fixed cost of GPU time for each.
+# packed rows, one launch per unpacked sub-batch (OffloadRuntime(split_fetch=True)) shortens
+# the step by about 1 % but adds a launch's fixed cost of GPU time for each.
 CHUNK_MIN_PAIRS = 16384
 CHUNKS = 6
 
@@ -57,7 +58,7 @@ def expert_ops():
 class OffloadRuntime:
     def __init__(self, spec, pool, capacities, policy, topology, history_window=128,
                  balance_tol_bps=200, salt=1, eviction_score='frequency', overlap=True,
-                 timing=False, copy='dma', pack=False, pack_threads=16):
+                 timing=False, copy='dma', pack=False, pack_threads=16, split_fetch=False):
         if dist.is_available() and dist.is_initialized() and dist.get_world_size() != 1:
             raise NotImplementedError('ferry_amd runs on one GPU (world = 1)')
         if len(capacities) != 1:
@@ -73,6 +74,9 @@ class OffloadRuntime:
         if copy not in ('dma', 'kernel'):
             raise ValueError("copy must be 'dma' or 'kernel'")
         self.copy = copy
+        # packed decode calls: compute the fetched experts sub-batch by sub-batch as the engine
+        # unpacks them (one FFN launch per sub-batch) instead of in one launch after the last
+        self.split_fetch = bool(split_fetch)
         # a lossless packed copy of the pool for the host link, made once; every engine of this
         # runtime fetches packed rows in DMA mode and unpacks them on the GPU
         # (pack: True, or a PackedPool of this pool built by the caller and shared; ``pool``
@@ -278,6 +282,13 @@ class OffloadRuntime:
         if queue_here and len(fetches):
             for g in groups:
                 self.h2d.fetch(fetches[g, 2], fetches[g, 1])
+        if (self.split_fetch and not chunked and not on_stream and self.packed is not None
+                and len(fetches) > 1):
+            # each sub-batch's experts run as soon as the engine has unpacked it, so only the
+            # last sub-batch's experts follow the call's last copy
+            ends = self.h2d.groups()
+            if len(ends) > 1:
+                groups = [np.arange(a, b) for a, b in zip([0] + ends[:-1], ends)]
         t_fetch = time.perf_counter_ns()
         self.fetches_per_rank += counts
         if self.event >= spec.layers:

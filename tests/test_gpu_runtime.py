@@ -159,7 +159,8 @@ def test_runtime_on_stream_matches_dma_overlap(device, tokens):
 def test_runtime_packed_pool_matches_raw(device, tokens):
     """OffloadRuntime(pack=True) -- misses copied as packed rows and unpacked on the GPU -- gives
     bit-identical outputs and the same fetch trace as raw fetches, on decode-sized and on
-    chunked prefill-sized calls."""
+    chunked prefill-sized calls; so does split_fetch=True (a packed decode call's fetched experts
+    computed sub-batch by sub-batch as they are unpacked)."""
     from dataclasses import replace
 
     from ferry_amd import expert_ops as ops
@@ -173,12 +174,15 @@ def test_runtime_packed_pool_matches_raw(device, tokens):
     cap = 200 if tokens > 64 else 80
     from ferry_amd.h2d import PackedPool
     runs = []
-    for pack in ('packed_pool', True, False):
+    for pack in ('packed_pool', True, 'split', False):
         if pack == 'packed_pool':   # the runtime given a PackedPool of a pageable pool
             src = workloads.make_pool(spec, spec.layers, seed=3, pinned=False)
             rt = OffloadRuntime(spec, PackedPool(src), [cap], 'ferry',
                                 Topology.uniform(1, spec.experts))
             del src
+        elif pack == 'split':
+            rt = OffloadRuntime(spec, pool, [cap], 'ferry', Topology.uniform(1, spec.experts),
+                                pack=True, split_fetch=True)
         else:
             rt = OffloadRuntime(spec, pool, [cap], 'ferry', Topology.uniform(1, spec.experts),
                                 pack=pack)
@@ -187,11 +191,15 @@ def test_runtime_packed_pool_matches_raw(device, tokens):
         g = torch.Generator(device=device)
         g.manual_seed(4)
         outs = []
+        sub_batches = 0
         for call in range(6):
             x = torch.randn((tokens, spec.hidden), generator=g, device=device).to(torch.bfloat16)
             z = torch.randn((tokens, spec.experts), generator=g, device=device) + bias.to(device)
             w, sel = ops.router_topk(z.to(torch.bfloat16), spec.topk)
             outs.append(rt.execute(call % 2, x, sel, w, None).cpu())
+            sub_batches = max(sub_batches, len(rt.h2d.groups()))
+        if pack == 'split' and tokens <= 64:
+            assert sub_batches >= 2   # the fetched experts did run in several launches
         runs.append((outs, rt.controller.slots[0].copy(), rt.h2d.copies))
         rt.close()
     base_outs, base_slots, base_n = runs[-1]
