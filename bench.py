@@ -119,8 +119,6 @@ def run_stacks(args, device):
     Pinned host memory is limited (about a quarter of RAM), so the raw runs use a pinned pool
     that is freed before the same seeded pool is rebuilt in pageable memory, packed (the
     packed copy is pinned) and freed again."""
-    import gc
-
     from ferry_amd import workloads
     from ferry_amd.h2d import PackedPool
     out = {}
@@ -370,6 +368,7 @@ def run_prefill(args, device, w):
     _, sel = layer()
     torch.cuda.synchronize()
     counts = np.bincount(sel.cpu().numpy().reshape(-1), minlength=E)
+    gc.collect()   # earlier blocks' pinned pools are freed here, not in the timed region
     t0 = time.perf_counter()
     for _ in range(args.prefill_reps):
         layer()
@@ -738,6 +737,7 @@ def run_prefill_stack(device, w, pool):
             rt.execute(layer, x, sel, wts, None, shared=shared[layer] if shared else None)
 
     torch.cuda.synchronize()
+    gc.collect()
     t0 = time.perf_counter()
     stack()
     torch.cuda.synchronize()
@@ -790,6 +790,7 @@ def run_decode_loop(device, steps, pool):
           for T in (w.prefill_tokens, w.tokens)}
     digest = hashlib.sha1()
     torch.cuda.synchronize()
+    gc.collect()
     t0 = time.perf_counter()
     for layer in range(L):
         sel = torch.from_numpy(routing['prefill'][layer]).to(device)
