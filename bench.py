@@ -39,6 +39,8 @@ Also on the line:
     False), the reference's transfer format);
   * decode_split_fetch: the headline stream with OffloadRuntime(split_fetch=True), each packed
     call's fetched experts computed sub-batch by sub-batch as they are unpacked;
+  * decode_serial_raw: the headline stream with the reference's fetch scheme (raw rows, the host
+    waits for every copy before any expert runs) on this library's kernels;
   * decode_copy_kernel: the headline stream through OffloadRuntime(copy='kernel'): raw misses
     copied by one kernel launch on the compute stream, then one FFN launch (no overlap);
   * reference_pattern_gpu: the reference's own per-expert torch op order for the expert FFN
@@ -187,7 +189,7 @@ def decode_stream(w, steps, device):
     return out
 
 
-def run_decode(args, device, copy='dma', pack=False, split_fetch=False):
+def run_decode(args, device, copy='dma', pack=False, split_fetch=False, overlap=True):
     from ferry_amd import expert_ops as ops
     from ferry_amd import workloads
     from ferry_amd.quota import Topology
@@ -196,7 +198,7 @@ def run_decode(args, device, copy='dma', pack=False, split_fetch=False):
     spec = w.spec
     pool = workloads.make_pool(spec, 1, seed=0)
     rt = OffloadRuntime(spec, pool, [w.cache_slots], 'ferry', Topology.uniform(1, spec.experts),
-                        copy=copy, pack=pack, split_fetch=split_fetch)
+                        copy=copy, pack=pack, split_fetch=split_fetch, overlap=overlap)
     packing = None
     if rt.packed is not None:
         packing = dict(ratio=rt.packed.ratio, packed_rows=rt.packed.packed_rows,
@@ -1103,6 +1105,15 @@ def main():
         note='OffloadRuntime(pack=False): raw bf16 rows over the host link')
     print(f'# decode (raw rows) done: {line["decode_raw"]["tokens_per_s"]:.0f} tokens/s',
           file=sys.stderr, flush=True)
+    # the reference's fetch scheme on this library's kernels: raw rows, and the host waits for
+    # every copy before any expert runs (OffloadRuntime(overlap=False, pack=False))
+    dsr = run_decode(args, device, pack=False, overlap=False)
+    line['decode_serial_raw'] = dict(
+        tokens_per_s=dsr['tokens'] / dsr['elapsed'], ms_per_step=dsr['elapsed'] / args.steps * 1e3,
+        note='OffloadRuntime(overlap=False, pack=False): the reference\'s serial fetch wait and '
+             'raw rows, with this library\'s kernels')
+    print(f'# decode (serial, raw rows) done: {line["decode_serial_raw"]["tokens_per_s"]:.0f} '
+          'tokens/s', file=sys.stderr, flush=True)
     if not args.no_prefill:
         from ferry_amd import workloads
         line['prefill'] = run_prefill(args, device, workloads.QWEN3_PREFILL_STACK)
