@@ -37,7 +37,8 @@ SIGNATURES = [
     ('ferry_unpack_dispatch', ctypes.c_int, [_c_p, _i64, _i64, _i64, _c_p, _c_p, _c_p]),
     ('ferry_combine_add', ctypes.c_int, [_c_p, _c_p, _i64, _i64, _i64, _c_p, _c_p, _c_p]),
     ('ferry_history_update', ctypes.c_int,
-     [_c_p, _i64, _i64, _i64, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p]),
+     [_c_p, _i64, _i64, _i64, _i64, _i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _i32, _c_p]),
+    ('ferry_history_ready_words', _i64, [_i64, _i64]),
     ('ferry_plan_layer', _i64,
      [_i64, _i64, _c_p, _i64, _i64, _c_p, _c_p, _i64, _c_p, _c_p, _c_p, _i64, _c_p, _c_p]),
     ('ferry_plan_fetch', _i64,
@@ -53,6 +54,7 @@ SIGNATURES = [
     ('ferry_h2d_mark_used', ctypes.c_int, [_c_p, _c_p, _i64, _c_p]),
     ('ferry_h2d_mark_used_record', ctypes.c_int, [_c_p, _c_p, _i64, _c_p, ctypes.POINTER(_c_p)]),
     ('ferry_h2d_event_synchronize', ctypes.c_int, [_c_p, _c_p]),
+    ('ferry_h2d_wait_ready', ctypes.c_int, [_c_p, _c_p, _c_p, _i64, _i32]),
     ('ferry_h2d_synchronize', ctypes.c_int, [_c_p]),
     ('ferry_h2d_reset', ctypes.c_int, [_c_p]),
     ('ferry_h2d_copies', _i64, [_c_p]),

@@ -134,4 +134,4 @@ extern "C" int ferry_timing_overlap(int64_t begin, int64_t end, void* t0, void* 
 
 extern "C" const char* ferry_last_error(void) { return ferry::g_last_error.c_str(); }
 
-extern "C" int32_t ferry_abi_version(void) { return 5; }
+extern "C" int32_t ferry_abi_version(void) { return 6; }

@@ -110,6 +110,9 @@ struct Event {
   int64_t order = 0;              // record order among the engine's events
   int device = 0;
   unsigned flags = 0;
+  // the slot reads it marks are known to be complete (ferry_h2d_wait_ready saw a kernel queued
+  // after them write its ready words), though the event itself may not have fired yet
+  bool reads_done = false;
   ~Event() {
     if (e) give_event(device, flags, e);
   }
@@ -134,6 +137,7 @@ bool pending_events(const std::vector<const std::shared_ptr<Event>*>& evs,
     if (!merged) newest.push_back(ev);
   }
   for (const Event* ev : newest) {
+    if (ev->reads_done) continue;
     const hipError_t q = hipEventQuery(ev->e);
     if (q == hipErrorNotReady) {
       (void)hipGetLastError();  // a pending event is not an error
@@ -727,6 +731,46 @@ extern "C" int ferry_h2d_mark_used_record(ferry_h2d* h, const int64_t* slots, in
   for (int64_t i = 0; i < n; ++i) h->used[(size_t)slots[i]] = ev;
   h->marker = ev;
   *event_out = (void*)ev->e;
+  return 0;
+}
+
+extern "C" int ferry_h2d_wait_ready(ferry_h2d* h, void* event, const int32_t* words, int64_t n,
+                                    int32_t value) {
+  ferry::clear_error();
+  if (!h || !event || !words || n < 1 || !h->marker || (void*)h->marker->e != event) {
+    ferry::set_error("h2d_wait_ready: bad arguments (event must be the latest "
+                     "ferry_h2d_mark_used_record event)");
+    return 2;
+  }
+  // Spin on the words (coherent host memory written by a kernel with a system-scope release);
+  // every 1024 rounds the event is queried, so that a kernel that finished without writing them
+  // is an error rather than an endless wait.
+  auto all_set = [&]() {
+    for (int64_t i = 0; i < n; ++i)
+      if (__atomic_load_n(&words[i], __ATOMIC_ACQUIRE) != value) return false;
+    return true;
+  };
+  for (uint64_t spin = 1;; ++spin) {
+    if (all_set()) break;
+    if ((spin & 1023) == 0) {
+      const hipError_t q = hipEventQuery((hipEvent_t)event);
+      if (q == hipSuccess) {
+        if (all_set()) break;
+        ferry::set_error("h2d_wait_ready: the stream passed the event but the ready words do not "
+                         "hold %d", (int)value);
+        return 3;
+      }
+      if (q != hipErrorNotReady) {
+        ferry::set_error("hipEventQuery failed: %s", hipGetErrorString(q));
+        return 3;
+      }
+      (void)hipGetLastError();   // a pending event is not an error
+    }
+  }
+  // The kernel that wrote the words ran after every kernel queued before it on the event's
+  // stream, so the slot reads the event marks are complete: later copies into those slots need
+  // not wait for the event itself.
+  h->marker->reads_done = true;
   return 0;
 }
 

@@ -20,12 +20,22 @@ constexpr int kThreads = 256;
 constexpr int kIdsPerBlock = kThreads * 16;
 
 // Block 0 updates the window of `layer`; blocks >= 1 write the uint8 copy of selected, with
-// 0xFF for an ID outside [0, E) (E <= 255 then, so the host planner rejects it).
+// 0xFF for an ID outside [0, E) (E <= 255 then, so the host planner rejects it).  With ready_out,
+// each block then writes ready_value to ready_out[block] with a system-scope release, after its
+// other writes are visible to the host.
+__device__ void history_block0(const int64_t* __restrict__ selected, int64_t tokens, int k, int E,
+                               int W, int64_t layer, int32_t* __restrict__ ring,
+                               int32_t* __restrict__ counts, int32_t* __restrict__ meta,
+                               float* __restrict__ scores_out,
+                               const int32_t* __restrict__ timeouts_src,
+                               int32_t* __restrict__ timeouts_out);
+
 __global__ __launch_bounds__(kThreads) void history_kernel(
     const int64_t* __restrict__ selected, int64_t tokens, int k, int E, int W, int64_t layer,
     int32_t* __restrict__ ring, int32_t* __restrict__ counts, int32_t* __restrict__ meta,
     float* __restrict__ scores_out, uint8_t* __restrict__ ids_out,
-    const int32_t* __restrict__ timeouts_src, int32_t* __restrict__ timeouts_out) {
+    const int32_t* __restrict__ timeouts_src, int32_t* __restrict__ timeouts_out,
+    int32_t* __restrict__ ready_out, int32_t ready_value) {
   if (blockIdx.x > 0) {
     const int64_t n = tokens * k;
     const int64_t i0 = (int64_t)(blockIdx.x - 1) * kIdsPerBlock;
@@ -33,8 +43,26 @@ __global__ __launch_bounds__(kThreads) void history_kernel(
       const int64_t e = selected[i];
       ids_out[i] = (e >= 0 && e < E) ? (uint8_t)e : (uint8_t)0xFF;
     }
-    return;
+  } else {
+    history_block0(selected, tokens, k, E, W, layer, ring, counts, meta, scores_out, timeouts_src,
+                   timeouts_out);
   }
+  if (ready_out) {
+    // every wavefront's writes reach the system scope before the block's ready word does
+    __threadfence_system();
+    __syncthreads();
+    if (threadIdx.x == 0)
+      __hip_atomic_store(&ready_out[blockIdx.x], ready_value, __ATOMIC_RELEASE,
+                         __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+}
+
+__device__ void history_block0(const int64_t* __restrict__ selected, int64_t tokens, int k, int E,
+                               int W, int64_t layer, int32_t* __restrict__ ring,
+                               int32_t* __restrict__ counts, int32_t* __restrict__ meta,
+                               float* __restrict__ scores_out,
+                               const int32_t* __restrict__ timeouts_src,
+                               int32_t* __restrict__ timeouts_out) {
   __shared__ int32_t c[kMaxE];
   int32_t* lring = ring + layer * (int64_t)W * k;
   int32_t* lcount = counts + layer * (int64_t)E;
@@ -86,11 +114,16 @@ __global__ __launch_bounds__(kThreads) void history_kernel(
 
 using namespace ferry;
 
+extern "C" int64_t ferry_history_ready_words(int64_t tokens, int64_t topk) {
+  return tokens < 0 || topk < 1 ? -1 : 1 + ceil_div(tokens * topk, kIdsPerBlock);
+}
+
 extern "C" int ferry_history_update(const int64_t* selected, int64_t tokens, int64_t topk,
                                     int64_t experts, int64_t window, int64_t layer,
                                     int32_t* ring, int32_t* counts, int32_t* meta,
                                     float* scores_out, uint8_t* ids_out,
-                                    int32_t* ffn_timeouts_out, void* stream) {
+                                    int32_t* ffn_timeouts_out, int32_t* ready_out,
+                                    int32_t ready_value, void* stream) {
   clear_error();
   FERRY_CHECK_ARG(tokens >= 0 && topk >= 1 && layer >= 0, "bad sizes");
   FERRY_CHECK_ARG(experts >= 1 && experts <= kMaxE, "experts must be in [1, %d]", kMaxE);
@@ -98,6 +131,7 @@ extern "C" int ferry_history_update(const int64_t* selected, int64_t tokens, int
   FERRY_CHECK_ARG(window >= 1 && window <= (1 << 20), "window must be in [1, 2^20]");
   FERRY_CHECK_ARG(ring && counts && meta && scores_out, "null pointer argument");
   FERRY_CHECK_ARG(tokens == 0 || selected, "null pointer argument");
+  FERRY_CHECK_ARG(ready_out == nullptr || ids_out != nullptr, "ready_out needs ids_out");
   const int64_t nids = ids_out ? tokens * topk : 0;
   const int64_t grid = 1 + ceil_div(nids, kIdsPerBlock);
   FERRY_CHECK_ARG(grid < (1 << 30), "too many tokens");
@@ -108,7 +142,8 @@ extern "C" int ferry_history_update(const int64_t* selected, int64_t tokens, int
   }
   launch("history_kernel", history_kernel, dim3((unsigned)grid), dim3(kThreads), 0, (hipStream_t)stream,
                      selected, tokens, (int)topk, (int)experts, (int)window, layer, ring, counts,
-                     meta, scores_out, ids_out, timeouts_src, ffn_timeouts_out);
+                     meta, scores_out, ids_out, timeouts_src, ffn_timeouts_out, ready_out,
+                     ready_value);
   FERRY_LAUNCHED("history_kernel");
   return 0;
 }

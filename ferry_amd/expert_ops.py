@@ -16,8 +16,8 @@ from .h2d import H2DEngine
 
 __all__ = ['execute_experts', 'pack_dispatch', 'unpack_dispatch', 'reduce_partials',
            'scatter_returned', 'H2DEngine', 'router_topk', 'layout', 'expert_ffn', 'combine',
-           'SharedExpert',
-           'history_update', 'current_stream', 'PHASE_UP', 'PHASE_DOWN', 'PHASE_BOTH']
+           'SharedExpert', 'history_update', 'history_ready_words', 'current_stream', 'PHASE_UP',
+           'PHASE_DOWN', 'PHASE_BOTH']
 
 MAX_EXPERTS = 512
 
@@ -293,24 +293,34 @@ class SharedExpert:
 
 
 def history_update(selected, experts, window, layer, ring, counts, meta, scores, ids_out=None,
-                   timeouts_out=None):
+                   timeouts_out=None, ready_out=None, ready_value=0):
     """Device GateHistory update of ``layer`` (ferry/metadata.py:15-38, frequency rows).
 
     ``scores`` (fp32 [E]), ``ids_out`` (uint8 [T*k]) and ``timeouts_out`` (int32 [1]: the
     device's count of one-launch decode FFN waits that gave up, as ``ffn_sync_timeouts``) are
     CUDA tensors or raw device addresses (ints), e.g. of a mapped host buffer that the kernel
-    writes directly."""
+    writes directly.  ``ready_out`` (device address of ``history_ready_words(T, k)`` int32
+    words, with ``ids_out``) receives ``ready_value`` in every word once the launch's other
+    writes are visible to the host."""
     T, k = selected.shape
     sp = scores if isinstance(scores, int) else _dev(scores, 'scores', torch.float32)
     ip = (ids_out if isinstance(ids_out, int) or ids_out is None
           else _dev(ids_out, 'ids_out', torch.uint8))
     tp = (timeouts_out if isinstance(timeouts_out, int) or timeouts_out is None
           else _dev(timeouts_out, 'timeouts_out', torch.int32))
+    rp = (ready_out if isinstance(ready_out, int) or ready_out is None
+          else _dev(ready_out, 'ready_out', torch.int32))
     check(lib().ferry_history_update(
         _dev(selected, 'selected', torch.int64), T, k, experts, window, layer,
         _dev(ring, 'ring', torch.int32), _dev(counts, 'counts', torch.int32),
-        _dev(meta, 'meta', torch.int32), sp, ip, tp, current_stream(selected.device)),
+        _dev(meta, 'meta', torch.int32), sp, ip, tp, rp, int(ready_value),
+        current_stream(selected.device)),
         'history_update')
+
+
+def history_ready_words(tokens, topk):
+    """Number of int32 ready words ``history_update`` writes for a call of ``tokens``."""
+    return int(lib().ferry_history_ready_words(int(tokens), int(topk)))
 
 
 # ------------------------------------------------------------------------------------------

@@ -96,6 +96,14 @@ class H2DEngine:
         """Block the host until an event of ``mark_used_record`` has fired."""
         check(lib().ferry_h2d_event_synchronize(self._h, event), 'H2DEngine.event_synchronize')
 
+    def wait_ready(self, event, words_ptr, n, value):
+        """Block the host until the ``n`` int32 words at host address ``words_ptr`` hold
+        ``value`` (ready words a kernel queued before ``event``, the latest event of
+        ``mark_used_record``, writes after its host-memory outputs); the reads that ``event``
+        marks then count as complete."""
+        check(lib().ferry_h2d_wait_ready(self._h, event, words_ptr, int(n), int(value)),
+              'H2DEngine.wait_ready')
+
     def synchronize(self):
         check(lib().ferry_h2d_synchronize(self._h), 'H2DEngine.synchronize')
 

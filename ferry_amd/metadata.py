@@ -51,11 +51,12 @@ class DeviceGateHistory:
         self.counts = torch.zeros((layers, experts), dtype=torch.int32, device=device)
         self.meta = torch.zeros((layers, 2), dtype=torch.int32, device=device)
 
-    def update(self, layer, selected, scores_out, ids_out=None, timeouts_out=None):
+    def update(self, layer, selected, scores_out, ids_out=None, timeouts_out=None,
+               ready_out=None, ready_value=0):
         """Append the last min(T, W) tokens of ``selected`` and write the layer's scores (and,
-        where given, the uint8 IDs and the device's decode-FFN timeout count)."""
+        where given, the uint8 IDs, the device's decode-FFN timeout count and the ready words)."""
         ops.history_update(selected, self.experts, self.window, layer, self.ring, self.counts,
-                           self.meta, scores_out, ids_out, timeouts_out)
+                           self.meta, scores_out, ids_out, timeouts_out, ready_out, ready_value)
 
 
 def frequency_rows(expert_ids, experts, window, world=1):

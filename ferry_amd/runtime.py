@@ -94,8 +94,13 @@ class OffloadRuntime:
         self.controller = Controller(spec, capacities, policy, topology, balance_tol_bps, salt)
         self.gather = RouteGather(spec.topk, spec.experts, history_window, eviction_score)
         self.transport = Transport(self.ops, spec.topk, spec.experts)
-        self._stage_host = None  # mapped host staging: [scores f32 E | IDs u8 T*k | pad | timeouts i32]
+        # mapped host staging: [scores f32 E | IDs u8 T*k | pad | timeouts i32 | ready i32 ...]
+        self._stage_host = None
         self._bufs = {}
+        self._ready_seq = 0
+        # calls wait for their routing IDs by polling the history kernel's ready words (False:
+        # on the event recorded after that kernel)
+        self._poll_ids = True
         self.h2d = None
         self.reset()
 
@@ -168,13 +173,16 @@ class OffloadRuntime:
                                      device=self.device),
                      part=torch.empty((tokens * k, spec.hidden), dtype=torch.bfloat16,
                                       device=self.device),
-                     layout=None)
+                     layout=None, ready_n=self.ops.history_ready_words(tokens, k))
             self._bufs[tokens] = b
-        n = self._status_offset(tokens) + 4
+        # staging layout: scores | IDs | timeout word | the history kernel's ready words
+        n = self._status_offset(tokens) + 4 + 4 * b['ready_n']
         if self._stage_host is None or self._stage_host.numel() < n:
             # coherent mapped host memory: the history kernel writes the layer's scores, the
-            # uint8 IDs and the timeout count straight into it, so the host needs no D2H copy
+            # uint8 IDs, the timeout count and its ready words straight into it, so the host
+            # needs no D2H copy
             self._stage_host, self._stage_ptr = mapped_buffer(max(n, 4096))
+            self._stage_host_ptr = self._stage_host.data_ptr()
             # int32 view for the timeout word (read right after the routing readback, on the
             # path to the first copy: a torch slice and view there cost about 10 us)
             self._stage_i32 = self._stage_host.numpy().view(np.int32)
@@ -203,8 +211,12 @@ class OffloadRuntime:
         nbytes = 4 * E + T * k
         stage_host = self._stage_host[:nbytes]
         status = self._status_offset(T)
+        # the ready words after the timeout word carry this call's number once the kernel's
+        # host-memory writes are visible
+        self._ready_seq = self._ready_seq % 0x7FFFFFFF + 1
+        seq = self._ready_seq
         self.device_history.update(layer, selected, self._stage_ptr, self._stage_ptr + 4 * E,
-                                   self._stage_ptr + status)
+                                   self._stage_ptr + status, self._stage_ptr + status + 4, seq)
         tail_host = None
         if not frequency:
             tail = min(T, self.window)
@@ -223,7 +235,13 @@ class OffloadRuntime:
                 pend = None
             self._pending_used = None
             ids_event = self.h2d.mark_used_record(pend[0] if pend is not None else [], stream)
-            wait_ids = lambda: self.h2d.event_synchronize(ids_event)   # noqa: E731
+            if self._poll_ids:
+                # poll the history kernel's ready words: about 5 us before the event's wait
+                # returns; they also show the previous call's slot reads complete
+                words, nw = self._stage_host_ptr + status + 4, buf['ready_n']
+                wait_ids = lambda: self.h2d.wait_ready(ids_event, words, nw, seq)   # noqa: E731
+            else:
+                wait_ids = lambda: self.h2d.event_synchronize(ids_event)   # noqa: E731
 
         # 2. layout (overlaps the host planning)
         buf['layout'] = self.ops.layout(selected, weights, E, out=buf['layout'])

@@ -203,11 +203,20 @@ int ferry_unpack_dispatch(const void* payload, int64_t packets, int64_t hidden_s
  * fused decode FFN workgroups that gave up waiting (ferry_expert_ffn_sync_timeouts), as the
  * stream's earlier kernels left it: a caller that reads its routing IDs from host memory reads
  * this word with them and can fail the layer call instead of using unwritten rows.
+ * ready_out (nullable, needs ids_out; no counterpart in the reference) receives ready_value in
+ * each of its ferry_history_ready_words(T, k) int32 words, each with a system-scope release
+ * after the launch's other writes of that word's workgroup: a caller whose outputs are in
+ * coherent host memory can poll the words (ferry_h2d_wait_ready) instead of waiting for an
+ * event behind the launch.
  */
 int ferry_history_update(const int64_t* selected, int64_t tokens, int64_t topk, int64_t experts,
                          int64_t window, int64_t layer, int32_t* ring, int32_t* counts,
                          int32_t* meta, float* scores_out, uint8_t* ids_out,
-                         int32_t* ffn_timeouts_out, void* stream);
+                         int32_t* ffn_timeouts_out, int32_t* ready_out, int32_t ready_value,
+                         void* stream);
+/* Number of int32 ready words a ferry_history_update call with ids_out writes: one per
+ * workgroup, 1 + ceil(tokens * topk / 4096); -1 for bad sizes. */
+int64_t ferry_history_ready_words(int64_t tokens, int64_t topk);
 
 /*
  * Host planner at world = 1.  Replaces ferry/policy.py:130-194 (plan_layer with
@@ -256,6 +265,18 @@ int ferry_h2d_mark_used(ferry_h2d* h, const int64_t* slots, int64_t n, void* str
 int ferry_h2d_mark_used_record(ferry_h2d* h, const int64_t* slots, int64_t n, void* stream,
                                void** event_out);
 int ferry_h2d_event_synchronize(ferry_h2d* h, void* event);
+/* The host's wait for a kernel's host-memory results without the event's completion latency
+ * (no counterpart in the reference, which synchronises its stream): spins until all n int32
+ * words at `words` (coherent host memory) hold `value`.  The words must be written, after the
+ * kernel's other writes, by a kernel queued on `event`'s stream after every read that `event`
+ * marks -- as ferry_history_update's ready words are when it is called before
+ * ferry_h2d_mark_used_record -- and `event` must be the engine's latest
+ * ferry_h2d_mark_used_record event.  Those reads are then complete, so later copies into the
+ * slots it marks do not wait for the event itself.  Queries the event every 1024 rounds:
+ * returns 3 (error set) if the stream passed the event and the words still do not hold
+ * `value`. */
+int ferry_h2d_wait_ready(ferry_h2d* h, void* event, const int32_t* words, int64_t n,
+                         int32_t value);
 /* expert_ops.cpp:130-133 */
 int ferry_h2d_synchronize(ferry_h2d* h);
 /* The state of a new engine on the same streams and buffers (runtime.py:51-62 builds a new

@@ -35,7 +35,13 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_errors():
     from ferry_amd._lib import last_error, lib
     L = lib()
-    assert L.ferry_abi_version() == 5
+    assert L.ferry_abi_version() == 6
+    # ready words of the history kernel: one per workgroup of 4096 IDs, plus the history one
+    assert [L.ferry_history_ready_words(t, 8) for t in (0, 16, 512, 513, 65536)] == [1, 2, 2, 3, 129]
+    assert L.ferry_history_ready_words(-1, 8) == -1 and L.ferry_history_ready_words(4, 0) == -1
+    assert L.ferry_history_update(None, 1, 8, 128, 128, 0, None, None, None, None, None, None,
+                                  None, 0, None) != 0
+    assert L.ferry_h2d_wait_ready(None, None, None, 1, 0) != 0
     # argument validation fails before any device work
     assert L.ferry_router_topk(None, 0, 4, 300, 8, 1, 1.0, 1, None, None, None, None, None) != 0
     assert 'experts' in last_error()

@@ -234,6 +234,52 @@ def test_device_history_matches_gate_history(device):
         assert np.array_equal(ids[:T * k].cpu().numpy(), sel.reshape(-1).astype(np.uint8))
 
 
+@pytest.mark.parametrize('T', [16, 1000])
+def test_history_ready_words_and_host_wait(device, T):
+    """The history kernel's ready words (one per workgroup, after its host-memory writes) end
+    the engine's polling wait with the IDs, scores and timeout word in place; a wait for a value
+    that was not written fails once the stream passed the event, and a stale event is refused."""
+    from ferry_amd.h2d import H2DEngine
+    from ferry_amd.hostmem import mapped_buffer
+    from ferry_amd.metadata import DeviceGateHistory
+    ops = _ops()
+    E, k, W = 128, 8, 128
+    nw = ops.history_ready_words(T, k)
+    assert nw == 1 + -(-T * k // 4096)
+    status = 4 * E + (T * k + 3) // 4 * 4
+    host, dptr = mapped_buffer(status + 4 + 4 * nw)
+    hp = host.data_ptr()
+    words = host.numpy()[status + 4:status + 4 + 4 * nw].view(np.int32)
+    cache = torch.zeros((4, 1 << 12), dtype=torch.bfloat16, device=device)
+    eng = H2DEngine(cache, torch.zeros((8, 1 << 12), dtype=torch.bfloat16).pin_memory())
+    hist = DeviceGateHistory(1, E, k, W, device)
+    ref = GateHistoryRef(1, E, W)
+    rng = np.random.default_rng(T)
+    stream = torch.cuda.current_stream(device)
+    for value in (7, 8, 2**31 - 1):
+        sel = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int64)
+        hist.update(0, torch.from_numpy(sel).to(device), dptr, dptr + 4 * E, dptr + status,
+                    dptr + status + 4, value)
+        ev = eng.mark_used_record([0, 1], stream)
+        eng.wait_ready(ev, hp + status + 4, nw, value)
+        assert (words == value).all()
+        ref.update(0, frequency_rows(sel, E, W))
+        assert np.array_equal(host.numpy()[:4 * E].view(np.float32), ref.scores(0))
+        assert np.array_equal(host.numpy()[4 * E:4 * E + T * k], sel.reshape(-1).astype(np.uint8))
+        assert host.numpy()[status:status + 4].view(np.int32)[0] == ops.ffn_sync_timeouts()
+        # the marked reads count as complete: a copy into slot 0 needs no wait for the event
+        eng.fetch([0], [3])
+        eng.wait_host([0])
+    with pytest.raises(RuntimeError, match='ready words'):
+        eng.wait_ready(ev, hp + status + 4, nw, 12345)
+    stale = ev
+    eng.mark_used_record([], stream)
+    with pytest.raises(RuntimeError, match='latest'):
+        eng.wait_ready(stale, hp + status + 4, nw, 2**31 - 1)
+    torch.cuda.synchronize()
+    eng.close()
+
+
 # ---------------------------------------------------------------------------------------------
 # expert FFN + combine
 # ---------------------------------------------------------------------------------------------
