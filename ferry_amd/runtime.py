@@ -222,26 +222,24 @@ class OffloadRuntime:
             tail = min(T, self.window)
             tail_host = probs_tail[-tail:].float().to('cpu', non_blocking=True)
         if self.timing:
+            # timestamp of the routing IDs (the history kernel's end) for critical_path_timing
             d2h = torch.cuda.Event(enable_timing=True)
             d2h.record(stream)
+        # one event both releases the IDs to the host and marks the slots that the previous call
+        # read on this stream (no event of their own between that call's kernels)
+        pend = self._pending_used
+        if pend is not None and pend[1] != stream.cuda_stream:
             self._flush_used()
-            wait_ids = d2h.synchronize
+            pend = None
+        self._pending_used = None
+        ids_event = self.h2d.mark_used_record(pend[0] if pend is not None else [], stream)
+        if self._poll_ids:
+            # poll the history kernel's ready words: they are seen about 5 us before the event's
+            # wait returns, and they show the previous call's slot reads complete
+            words, nw = self._stage_host_ptr + status + 4, buf['ready_n']
+            wait_ids = lambda: self.h2d.wait_ready(ids_event, words, nw, seq)   # noqa: E731
         else:
-            # one event both releases the IDs to the host and marks the slots that the previous
-            # call read on this stream (no event of their own between that call's kernels)
-            pend = self._pending_used
-            if pend is not None and pend[1] != stream.cuda_stream:
-                self._flush_used()
-                pend = None
-            self._pending_used = None
-            ids_event = self.h2d.mark_used_record(pend[0] if pend is not None else [], stream)
-            if self._poll_ids:
-                # poll the history kernel's ready words: about 5 us before the event's wait
-                # returns; they also show the previous call's slot reads complete
-                words, nw = self._stage_host_ptr + status + 4, buf['ready_n']
-                wait_ids = lambda: self.h2d.wait_ready(ids_event, words, nw, seq)   # noqa: E731
-            else:
-                wait_ids = lambda: self.h2d.event_synchronize(ids_event)   # noqa: E731
+            wait_ids = lambda: self.h2d.event_synchronize(ids_event)   # noqa: E731
 
         # 2. layout (overlaps the host planning)
         buf['layout'] = self.ops.layout(selected, weights, E, out=buf['layout'])
